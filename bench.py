@@ -1,0 +1,234 @@
+"""Benchmark of the speculative-decoding verification path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config h|c1|c2|c3|c4|c5]
+
+A step is one ``rejection_sample`` call (one fused HIP launch plus its small init launch) over
+the whole batch, inputs already resident in HBM; the default workload is the headline
+configuration (B=256, k=4, V=151936, fp32 target logits and draft probs, random T=0.8).
+Prints ONE JSON line: value = achieved GB/s (algorithmic bytes per step / step time), with
+verified tokens/s, the roofline object and a host-CPU baseline of the oracle.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "vllm-from-scratch_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="h", choices=["h", "c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--cpu-sample", type=int, default=None,
+                    help="requests in the CPU-baseline sample (default: sized to ~10-20 s)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def make_workload(name, device):
+    from mvsd.testing import configs
+
+    return {"h": configs.headline, "c1": configs.greedy_c1, "c2": configs.random_c2,
+            "c4": configs.ragged_c4, "c5": configs.eagle_c5}[name](device)
+
+
+def run_step(w):
+    from mvsd.sample.metadata import SamplingMetadata
+    from mvsd.sample.rejection_sampler import rejection_sample
+
+    sm = SamplingMetadata(temperature=w.temperature, all_greedy=w.all_greedy,
+                          all_random=w.all_random, top_k=None, top_p=None)
+
+    def step():
+        return rejection_sample(
+            w.draft_token_ids, w.num_draft_tokens, w.max_spec_len, w.cu_num_draft_tokens,
+            w.draft_probs, w.target_logits, w.bonus_token_ids, sm, uniform_probs=w.uniforms,
+            exp_noise=w.exp_noise, target_rows=w.target_rows,
+            apply_temperature=w.apply_temperature)
+    return step
+
+
+def time_steps(step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        out = step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / steps, wall / steps * 1e3, out
+
+
+def accept_histogram(outputs, num_draft_tokens, max_k):
+    hist = [0] * (max_k + 1)
+    for toks, k in zip(outputs, num_draft_tokens):
+        if k > 0:
+            hist[max(len(toks) - 1, 0)] += 1
+    return hist
+
+
+def cpu_baseline(w, sample_requests):
+    """Time the CPU oracle (torch CPU, all host threads) on the first `sample_requests`
+    requests of the same workload; returns GB/s over that sample's algorithmic bytes."""
+    from mvsd.testing import configs
+    from oracle import rejection as orc
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    ks = w.num_draft_tokens[:sample_requests]
+    P = int(sum(ks))
+    rows = (w.target_rows[:P].long() if w.target_rows is not None else torch.arange(P,
+                                                                                   device=w.target_logits.device))
+    tl = w.target_logits[rows].cpu()
+    dp = None if w.draft_probs is None else w.draft_probs[:P].cpu()
+    noise = None if w.exp_noise is None else w.exp_noise[:len(ks)].cpu()
+    u = None if w.uniforms is None else w.uniforms[:P].cpu()
+    temp = None if w.temperature is None else w.temperature[:len(ks)].cpu()
+    ids = w.draft_token_ids[:P].cpu()
+    bonus = w.bonus_token_ids[:len(ks)].cpu()
+
+    def run():
+        return orc.rejection_sample(ids, ks, w.max_spec_len, dp, tl, bonus, temperature=temp,
+                                    all_greedy=w.all_greedy, uniforms=u, exp_noise=noise,
+                                    apply_temperature=w.apply_temperature)
+
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    sec = float(np.median(times))
+    sub = configs.Workload(w.name, ks, w.max_spec_len, ids, w.cu_num_draft_tokens[:len(ks)],
+                           tl, None, dp, bonus, temp, w.all_greedy, w.all_random, u, noise)
+    nbytes = configs.algorithmic_bytes(sub)
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"first {len(ks)} of {w.batch_size} requests ({P} verify rows, V={w.vocab_size}) "
+                      f"of the same workload through oracle/rejection.py on torch-CPU; median of 3 "
+                      f"runs, {sec:.2f} s each; {nbytes} algorithmic bytes",
+            "seconds": round(sec, 3)}
+
+
+def load_traffic(config):
+    if TRAFFIC_FILE.exists():
+        data = json.loads(TRAFFIC_FILE.read_text())
+        entry = data.get(config)
+        if entry:
+            return entry.get("bytes_per_launch")
+    return None
+
+
+def bench_ngram(args, device):
+    from mvsd.spec_decode.ngram_proposer_gpu import ngram_propose_device
+    from mvsd.testing import configs
+    from oracle import ngram as ong
+
+    tokens = configs.ngram_c3(device)
+    B, L = tokens.shape
+    lens = torch.full((B,), L, dtype=torch.int32, device=device)
+
+    def step():
+        return ngram_propose_device(tokens, lens, min_n=2, max_n=5, k=5)
+
+    ms, wall_ms, (d, v) = time_steps(step, args.steps, args.warmup)
+    nbytes = B * L * 4 + B * 4 + B * 5 * 4 + B * 4
+    tn, ln = tokens.cpu().numpy(), lens.cpu().numpy()
+    t0 = time.perf_counter()
+    ong.kmp_batch(tn, ln, 2, 5, 8192, 5)
+    cpu_s = time.perf_counter() - t0
+    line = {"metric": "ngram proposer drafts/s (C3)", "value": round(B / (ms / 1e3), 1),
+            "unit": "requests/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "strong",
+            "vs_baseline": None, "dtype": "int32", "data": "synthetic",
+            "config": {"workload": "c3 ngram B=256 L=4096 min_n=2 max_n=5 k=5"},
+            "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms / 1e3) / 1e9, 2),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 5),
+                         "traffic": None},
+            "cpu_baseline": {"value": round(B / cpu_s, 1), "unit": "requests/s", "cores": 1,
+                             "kind": "port", "sample": "all 256 histories through oracle/ngram.c "
+                             "KMP (the reference CPU algorithm), one thread"}}
+    print(json.dumps(line))
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                          "(multi-GPU sharding is described in DESIGN.md, not launched)"}))
+        sys.exit(2)
+    device = torch.device("cuda", 0)
+    if args.config == "c3":
+        bench_ngram(args, device)
+        return
+    from mvsd.sample.rejection_sampler import RejectionSampler
+    from mvsd.testing import configs
+
+    w = make_workload(args.config, device)
+    step = run_step(w)
+    ms, wall_ms, out = time_steps(step, args.steps, args.warmup)
+    nbytes = configs.algorithmic_bytes(w)
+    outputs, _ = RejectionSampler.parse_output(out, w.vocab_size)
+    tokens = sum(len(o) for o in outputs)
+    gbs = nbytes / (ms / 1e3) / 1e9
+    hist = accept_histogram(outputs, w.num_draft_tokens, w.max_spec_len)
+    line = {
+        "metric": "rejection-sampler HBM GB/s (% of peak) + verified tok/s, B=256 k=4 V=152k",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if w.target_logits.dtype == torch.float32 else "bf16",
+        "data": "synthetic (seeded on-device Philox; random logits, no checkpoint)",
+        "config": {"workload": {"h": "headline B=256 k=4 V=151936 fp32 random T=0.8",
+                                "c1": "c1 greedy B=4 k=3 fp32", "c2": "c2 random B=64 k=4 fp32",
+                                "c4": "c4 ragged B=512 bf16 (no top-k/top-p)",
+                                "c5": "c5 eagle B=1024 k=7 bf16 target"}[args.config],
+                   "batch_size": w.batch_size, "num_draft_rows": w.num_tokens,
+                   "vocab_size": w.vocab_size, "algorithmic_bytes": nbytes},
+        "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "verified_tok_per_s": round(tokens / (ms / 1e3), 1),
+        "verified_tokens_per_step": tokens,
+        "accept_length_hist": hist,
+        "wall_ms_per_step": round(wall_ms, 5),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic(args.config)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        sample = args.cpu_sample or max(1, min(w.batch_size, 48 * 4 // max(w.max_spec_len, 1)))
+        line["cpu_baseline"] = cpu_baseline(w, sample)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

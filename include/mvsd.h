@@ -1,0 +1,191 @@
+/*
+ * mvsd.h — C ABI of the MI355X speculative-decoding verification library (libmvsd.so).
+ *
+ * Every entry point takes raw device pointers, element strides, dtype codes and a
+ * hipStream_t, enqueues work on that stream, never synchronises the host and never
+ * allocates device memory: scratch comes from a caller-owned workspace whose size is
+ * returned by the matching *_workspace_bytes() query.  Each returns 0 on success or a
+ * negative MVSD_E_* code; mvsd_status_string() turns a code into text.  A host-side
+ * wrapper turns a non-zero code into an exception, the same pattern the reference uses
+ * for its own ctypes-loaded kernels (minivllm/layers/ops/rms_norm_cuda.py:95-112,163-188).
+ *
+ * Row conventions follow the reference:
+ *   - "verify rows" are the P = sum_i K_i draft positions, request-major
+ *     (minivllm/spec_decode/metadata.py:31-39);
+ *   - cu_num_draft_tokens is the inclusive prefix sum of K_i WITHOUT a leading 0
+ *     (minivllm/spec_decode/metadata.py:49-52);
+ *   - outputs are [B, max_spec_len + 1] int32 padded with -1
+ *     (minivllm/sample/rejection_sampler.py:79,462-467).
+ */
+#ifndef MVSD_H_
+#define MVSD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t is an opaque pointer; callers pass torch.cuda.current_stream().cuda_stream. */
+typedef void* mvsd_stream_t;
+
+/* dtype codes for logits / probabilities / expanded values */
+enum {
+  MVSD_F32 = 0,
+  MVSD_BF16 = 1,
+  MVSD_F16 = 2,
+  MVSD_F64 = 3,
+  MVSD_I32 = 4,
+  MVSD_I64 = 5,
+  MVSD_U8 = 6
+};
+
+/* status codes */
+enum {
+  MVSD_OK = 0,
+  MVSD_E_INVALID = -1,     /* bad argument (shape, null pointer, unsupported dtype) */
+  MVSD_E_ALIGN = -2,       /* pointer/stride alignment the kernel needs is not met */
+  MVSD_E_WORKSPACE = -3,   /* workspace missing or too small */
+  MVSD_E_HIP = -4,         /* a HIP runtime call failed; see mvsd_last_hip_error() */
+  MVSD_E_RANGE = -5        /* a size exceeds what the kernel supports */
+};
+
+/* Library version, (major << 16) | (minor << 8) | patch. */
+int mvsd_version(void);
+/* Human-readable text of a status code. */
+const char* mvsd_status_string(int status);
+/* The hipError_t of the last failing HIP call in this thread (0 if none). */
+int mvsd_last_hip_error(void);
+
+/* ------------------------------------------------------------------------------------ */
+/* expand_batch_to_tokens                                                                 */
+/* Replaces: expand_batch_to_tokens + expand_kernel,                                     */
+/*           minivllm/sample/rejection_sampler.py:574-597 and :826-847.                   */
+/* out[j] = (x[i] == replace_from ? replace_to : x[i]) for every j in request i's range   */
+/* [cu[i-1], cu[i]).  dtype in {F32, F64, I32, I64, U8}; out has x's dtype.               */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_expand_batch_to_tokens(void* out, const void* x, int dtype,
+                                const int32_t* cu_num_tokens, int64_t batch_size,
+                                int64_t num_tokens, double replace_from, double replace_to,
+                                mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* rejection_sample — fused verification of a whole batch in one persistent launch.      */
+/* Replaces: rejection_sample (minivllm/sample/rejection_sampler.py:414-534) together    */
+/* with what it launches: target softmax (:502), target argmax (:485),                   */
+/* rejection_greedy_sample_kernel (:678-740), sample_recovered_tokens + its kernel       */
+/* (:627-670, :850-928) and rejection_random_sample_kernel (:744-822); and, when          */
+/* apply_temperature != 0, the temperature divide of apply_sampling_constraints (:553-561)*/
+/* that RejectionSampler.forward (:195-196) runs before it.                               */
+/*                                                                                        */
+/* Request i is greedy iff all_greedy != 0 or temperature[i] == 0 (:469-473).            */
+/* Random requests need exp_noise (one Exp(1) row per request, :648-655) unless           */
+/* recovered_token_ids is given; uniform_probs is fp64 [P] (:600-624).                    */
+/* ------------------------------------------------------------------------------------ */
+typedef struct mvsd_rejection_args {
+  /* output [batch_size, max_spec_len + 1] int32, row stride out_stride elements */
+  int32_t* output_token_ids;
+  int64_t out_stride;
+
+  /* target logits: verify row j is at target_logits + target_rows[j] * target_stride
+   * (target_rows == NULL means row j).  dtype F32, BF16 or F16; upcast to fp32 in-kernel. */
+  const void* target_logits;
+  int target_dtype;
+  int64_t target_stride;
+  const int32_t* target_rows;
+  int64_t target_num_rows;              /* rows addressable from target_logits (indices are clamped) */
+
+  /* draft probabilities [P, V] (dtype F32, BF16 or F16), or NULL for point-mass drafts
+   * (ngram: q[d] = 1, recovered distribution = p with the draft id removed, :793-795,:891-897) */
+  const void* draft_probs;
+  int draft_dtype;
+  int64_t draft_stride;
+
+  /* Exp(1) noise [batch_size, V] fp32, one row per request; may be NULL when every
+   * request is greedy or recovered_token_ids is given */
+  const float* exp_noise;
+  int64_t noise_stride;
+
+  const double* uniform_probs;          /* [P] fp64; may be NULL when all greedy and not synthetic */
+  const int32_t* draft_token_ids;       /* [P] */
+  const int32_t* cu_num_draft_tokens;   /* [batch_size], no leading 0 */
+  const int32_t* bonus_token_ids;       /* [batch_size] */
+
+  const float* temperature;             /* [batch_size] fp32, or NULL when all_greedy */
+  int all_greedy;
+  int apply_temperature;                /* 1: divide logits by T (T==0 -> 1) in-kernel */
+
+  const int32_t* recovered_token_ids;   /* optional [P] override of the recovered ids */
+  const float* synthetic_conditional_rates; /* optional [>= max_spec_len]; enables synthetic mode */
+
+  int64_t batch_size;
+  int64_t num_tokens;                   /* P */
+  int64_t vocab_size;                   /* V */
+  int64_t max_spec_len;                 /* <= 128 */
+
+  void* workspace;                      /* >= mvsd_rejection_workspace_bytes(...) bytes */
+  int64_t workspace_bytes;
+} mvsd_rejection_args;
+
+int64_t mvsd_rejection_workspace_bytes(int64_t batch_size, int64_t num_tokens,
+                                       int64_t vocab_size, int target_dtype,
+                                       int64_t max_spec_len);
+int mvsd_rejection_sample(const mvsd_rejection_args* args, mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* softmax_rows — probs[j, :] = softmax(logits[row_j, :] / t_j) in fp32.                 */
+/* Replaces: target_logits.softmax(dim=-1, dtype=float32),                               */
+/*           minivllm/sample/rejection_sampler.py:502.  temperature may be NULL (t = 1);  */
+/* otherwise t_j = temperature[j] with 0 -> 1.                                            */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_softmax_rows(float* probs, int64_t probs_stride, const void* logits, int dtype,
+                      int64_t logits_stride, const float* temperature, int64_t num_rows,
+                      int64_t vocab_size, mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* sample_recovered_tokens — argmax_v max(p - q, 0) * (1 / E[req, v]) per verify row.    */
+/* Replaces: sample_recovered_tokens + sample_recovered_tokens_kernel,                   */
+/*           minivllm/sample/rejection_sampler.py:627-670 and :850-928 (noise supplied). */
+/* draft_probs == NULL selects the point-mass form (p with the draft id masked).          */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_sample_recovered_tokens(int32_t* recovered_token_ids, const int32_t* cu_num_draft_tokens,
+                                 const int32_t* draft_token_ids, const float* draft_probs,
+                                 int64_t draft_stride, const float* target_probs,
+                                 int64_t target_stride, const float* exp_noise,
+                                 int64_t noise_stride, int64_t batch_size, int64_t num_tokens,
+                                 int64_t vocab_size, int64_t max_spec_len, mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* ngram_propose — prompt-lookup drafts for a batch of int32 token histories.            */
+/* Replaces: NgramGPUKernel._find_first_and_extract_all_n_parallel + forward             */
+/*           (minivllm/spec_decode/ngram_proposer_gpu.py:56-148) with the in-place       */
+/*           history scatter of NgramProposerGPU.propose (:222-241) when new_tokens is   */
+/*           given; and, with cap_by_model_len != 0, the CPU matcher                     */
+/*           _find_longest_matched_ngram_and_propose_tokens                              */
+/*           (minivllm/spec_decode/ngram_proposer.py:41-99) used by batch_propose        */
+/*           (:152-184).                                                                  */
+/*                                                                                        */
+/* token_ids [num_reqs, row_stride] int32 (written in place when new_tokens != NULL).     */
+/* num_tokens [num_reqs] int32 lengths (read only).  Row i is matched on length           */
+/* L_i = num_tokens[i] + new_counts[i] (new_counts NULL -> 0), clamped to max_seq_len.    */
+/* active [num_reqs] uint8 (NULL = all active): inactive rows get drafts of -1.          */
+/* gate_on_new_counts != 0 additionally deactivates rows with new_counts[i] == 0 or       */
+/* L_i < min_n (the combined_mask of NgramProposerGPU.propose, :239-241).                 */
+/* GPU form (cap_by_model_len == 0): drafts [num_reqs, k] -1 padded, num_valid = count of */
+/* leading valid drafts.  CPU form (cap_by_model_len != 0): k_i = min(k, max_model_len -  */
+/* L_i); rows with L_i < min_n or k_i <= 0 give no drafts; num_valid = drafts copied.     */
+/* Limits: 1 <= min_n <= max_n <= 32, 1 <= k <= 256, max_seq_len <= row_stride < 2^31.   */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_ngram_propose(int32_t* drafts, int32_t* num_valid, int32_t* token_ids,
+                       int64_t row_stride, int64_t max_seq_len, const int32_t* num_tokens,
+                       const int32_t* new_tokens, int64_t new_tokens_stride,
+                       int64_t max_new_tokens, const int32_t* new_counts,
+                       const uint8_t* active, int gate_on_new_counts, int64_t num_reqs,
+                       int32_t min_n, int32_t max_n, int32_t k, int cap_by_model_len,
+                       int64_t max_model_len, mvsd_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MVSD_H_ */

@@ -1,0 +1,330 @@
+"""GPU parity of the fused rejection sampler (libmvsd.so through the C ABI) against the
+reference's KATs and the CPU oracle, on the benchmark configurations at full size.
+
+Bar: greedy ids bit-exact; random ids bit-exact except accept/reject flips where
+|u - p/q| < 1e-6 and recovered-token flips whose top-2 scores tie within 1e-5 relative — both
+counted and printed (probabilities differ from torch's softmax by rounding only).
+"""
+
+import json
+from dataclasses import replace
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from mvsd.outputs import SamplerOutput
+from mvsd.sample import rejection_sampler as rs
+from mvsd.sample.metadata import SamplingMetadata
+from mvsd.testing import configs
+from mvsd.testing.spec_metadata import make_metadata
+from oracle import rejection as orc
+
+pytestmark = pytest.mark.gpu
+
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+
+
+def sm_for(temps, drafts, device, generators=None):
+    all_greedy = all(t < 1e-5 for t in temps)
+    n = len(temps)
+    return SamplingMetadata(
+        temperature=None if all_greedy else torch.tensor(temps, dtype=torch.float32,
+                                                         device=device),
+        all_greedy=all_greedy, all_random=all(t >= 1e-5 for t in temps), top_k=None,
+        top_p=None, generators=dict(generators or {}), prompt_token_ids=[[] for _ in range(n)],
+        output_token_ids=[[] for _ in range(n)], min_tokens=[0] * n,
+        stop_token_ids=[[] for _ in range(n)], spec_token_ids=[list(d) for d in drafts])
+
+
+def compact_logits(case):
+    """[P+B, V] compact logits of a KAT: each request's verify rows then its bonus row."""
+    rows = []
+    if case["kind"] == "argmax":
+        V = case["vocab"]
+        for target, bonus in zip(case["targets"], case["bonus"]):
+            for t in list(target) + [bonus]:
+                row = [0.01] * V
+                row[t] = 0.9
+                rows.append(row)
+    else:
+        start = 0
+        V = len(case["p_rows"][0])
+        for draft, bonus in zip(case["drafts"], case["bonus"]):
+            rows.extend(case["p_rows"][start:start + len(draft)])
+            onehot = [0.0] * V
+            onehot[bonus] = 1.0
+            rows.append(onehot)
+            start += len(draft)
+    return torch.tensor(rows, dtype=torch.float32).log()
+
+
+def run_kat(case, device, monkeypatch, fused):
+    drafts = case["drafts"]
+    meta = make_metadata(drafts, device=device)
+    logits = compact_logits(case).to(device)
+    q = None
+    if case["kind"] == "probs" and case["q_rows"] is not None:
+        q = torch.tensor(case["q_rows"], dtype=torch.float32, device=device)
+    bonus = torch.tensor(case["bonus"], dtype=torch.int32, device=device).view(-1, 1)
+    sm = sm_for(case["temperature"], drafts, device)
+    if "uniforms" in case:
+        u = torch.tensor(case["uniforms"], dtype=torch.float64, device=device)
+        monkeypatch.setattr(rs, "generate_uniform_probs", lambda *a, **k: u)
+    if "recovered" in case:
+        r = torch.tensor(case["recovered"], dtype=torch.int32, device=device)
+        monkeypatch.setattr(rs, "sample_recovered_tokens", lambda *a, **k: r)
+    if fused:
+        return rs.rejection_sample(meta.draft_token_ids, meta.num_draft_tokens,
+                                   meta.max_spec_len, meta.cu_num_draft_tokens, q, logits, bonus,
+                                   sm, target_rows=meta.target_logits_indices,
+                                   apply_temperature=True)
+    target = logits[meta.target_logits_indices.long()]
+    return rs.rejection_sample(meta.draft_token_ids, meta.num_draft_tokens, meta.max_spec_len,
+                               meta.cu_num_draft_tokens, q, target, bonus, sm)
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["reference_signature", "fused_gather"])
+@pytest.mark.parametrize("case", KATS["rejection"], ids=lambda c: c["name"])
+def test_reference_kats(case, fused, device, monkeypatch):
+    out = run_kat(case, device, monkeypatch, fused)
+    assert out.dtype == torch.int32
+    assert out.cpu().tolist() == case["expected"]
+
+
+class ArgmaxBonusSampler:
+    """Test stand-in for the caller's bonus sampler: argmax of the bonus rows."""
+
+    logprobs_mode = "raw_logprobs"
+
+    def forward(self, logits, sampling_metadata, predict_bonus_token=False,
+                logprobs_mode_override=None):
+        return SamplerOutput(sampled_token_ids=logits.argmax(-1).to(torch.int32).view(-1, 1))
+
+
+@pytest.mark.parametrize("case", [c for c in KATS["rejection"] if c["kind"] == "argmax"],
+                         ids=lambda c: c["name"])
+def test_rejection_sampler_forward_greedy_kats(case, device):
+    meta = make_metadata(case["drafts"], device=device)
+    logits = compact_logits(case).to(device)
+    sm = sm_for(case["temperature"], case["drafts"], device)
+    out = rs.RejectionSampler(ArgmaxBonusSampler())(meta, None, logits, sm)
+    assert out.sampled_token_ids.cpu().tolist() == case["expected"]
+    parsed, _ = rs.RejectionSampler.parse_output(out.sampled_token_ids, case["vocab"])
+    assert parsed == [[t for t in row if t != -1] for row in case["expected"]]
+
+
+def test_expand_kats(device):
+    for case in KATS["expand"]:
+        x = torch.tensor(case["x"], device=device)
+        cu = torch.tensor(case["cu"], dtype=torch.int32, device=device)
+        out = rs.expand_batch_to_tokens(x, cu, case["num_tokens"], case["replace_from"],
+                                        case["replace_to"])
+        assert out.cpu().tolist() == case["expected"]
+    k = torch.tensor([5, 50, 7], dtype=torch.int64, device=device)
+    out = rs.expand_batch_to_tokens(k, torch.tensor([2, 2, 5], dtype=torch.int32, device=device), 5)
+    assert out.cpu().tolist() == [5, 5, 7, 7, 7]
+
+
+# --------------------------------------------------------------------------- oracle parity
+
+
+def run_workload(w: configs.Workload, *, draft_none=False, synthetic=None):
+    sm = SamplingMetadata(temperature=w.temperature, all_greedy=w.all_greedy,
+                          all_random=w.all_random, top_k=None, top_p=None)
+    return rs.rejection_sample(
+        w.draft_token_ids, w.num_draft_tokens, w.max_spec_len, w.cu_num_draft_tokens,
+        None if draft_none else w.draft_probs, w.target_logits, w.bonus_token_ids, sm,
+        synthetic_mode=synthetic is not None, synthetic_conditional_rates=synthetic,
+        uniform_probs=w.uniforms, exp_noise=w.exp_noise, target_rows=w.target_rows,
+        apply_temperature=w.apply_temperature)
+
+
+def oracle_for(w: configs.Workload, *, draft_none=False, synthetic=None, rows=None):
+    """Oracle on the verify rows (optionally on a subset of requests)."""
+    logits = w.target_logits if w.target_rows is None else w.target_logits[w.target_rows.long()]
+    return orc.rejection_sample(
+        w.draft_token_ids.cpu(), w.num_draft_tokens, w.max_spec_len,
+        None if (draft_none or w.draft_probs is None) else w.draft_probs.cpu(), logits.cpu(),
+        w.bonus_token_ids.cpu(), temperature=None if w.temperature is None else w.temperature.cpu(),
+        all_greedy=w.all_greedy, uniforms=None if w.uniforms is None else w.uniforms.cpu(),
+        exp_noise=None if w.exp_noise is None else w.exp_noise.cpu(),
+        apply_temperature=w.apply_temperature,
+        synthetic_rates=None if synthetic is None else synthetic.cpu())
+
+
+def check_parity(w, out, ref, label, **kw):
+    rep = orc.compare(out.cpu().numpy(), ref, w.draft_token_ids.cpu(), w.num_draft_tokens, **kw)
+    print(f"[{label}] requests={rep.requests} mismatched={rep.mismatched} "
+          f"accept_flips={rep.accept_flips} recovered_flips={rep.recovered_flips}", flush=True)
+    assert not rep.unexplained, rep.unexplained[:5]
+    return rep
+
+
+def test_c1_greedy_bit_exact(device):
+    w = configs.greedy_c1(device)
+    out = run_workload(w)
+    ref = oracle_for(w)
+    assert np.array_equal(out.cpu().numpy(), ref.output_token_ids)
+
+
+def test_c1_greedy_larger_batch_bit_exact(device):
+    w = configs.greedy_c1(device, B=64, k=6, seed=77)
+    out = run_workload(w)
+    ref = oracle_for(w)
+    assert np.array_equal(out.cpu().numpy(), ref.output_token_ids)
+
+
+def test_c2_random_parity(device):
+    w = configs.random_c2(device)
+    rep = check_parity(w, run_workload(w), oracle_for(w), "c2")
+    assert rep.mismatched <= 2
+
+
+def test_headline_parity_full_size(device):
+    w = configs.headline(device)
+    rep = check_parity(w, run_workload(w), oracle_for(w), "headline B=256 k=4")
+    assert rep.mismatched <= 4
+
+
+def test_point_mass_drafts_parity(device):
+    w = configs.random_c2(device, B=32, k=4, seed=4242)
+    check_parity(w, run_workload(w, draft_none=True), oracle_for(w, draft_none=True),
+                 "point-mass")
+
+
+def test_bf16_ragged_mixed_parity(device):
+    """c4's ragged mixed greedy/random bf16 batch (without its top-k/top-p quartiles)."""
+    w = configs.ragged_c4(device, B=128)
+    check_parity(w, run_workload(w), oracle_for(w), "c4-recipe B=128 no top-k/p")
+
+
+def test_eagle_c5_recipe_subset_parity(device):
+    w = configs.eagle_c5(device, B=48)
+    check_parity(w, run_workload(w), oracle_for(w), "c5-recipe B=48")
+
+
+def test_synthetic_mode_parity(device):
+    w = configs.random_c2(device, B=32, k=4, seed=99)
+    rates = torch.tensor([0.9, 0.6, 0.5, 0.3], device=device)
+    out = run_workload(w, synthetic=rates)
+    ref = oracle_for(w, synthetic=rates)
+    # synthetic acceptance never looks at p/q: accept/reject is exact, recovered ids may tie
+    check_parity(w, out, ref, "synthetic")
+
+
+@pytest.mark.parametrize("V", [5, 1001, 4097, 8193])
+def test_odd_vocab_sizes(device, V):
+    """Unaligned rows (scalar loads) and partial last chunks."""
+    w = configs.random_c2(device, B=16, k=3, V=V, seed=V)
+    check_parity(w, run_workload(w), oracle_for(w), f"V={V}")
+    g = configs.greedy_c1(device, B=16, k=3, V=V, seed=V + 1)
+    assert np.array_equal(run_workload(g).cpu().numpy(), oracle_for(g).output_token_ids)
+
+
+def test_repeated_calls_are_identical(device):
+    w = configs.random_c2(device, B=32, k=4, seed=5)
+    a = run_workload(w)
+    b = run_workload(w)
+    c = run_workload(configs.greedy_c1(device, B=3, k=2, seed=6))
+    d = run_workload(w)
+    assert torch.equal(a, b) and torch.equal(a, d) and c.shape == (3, 3)
+
+
+def test_no_host_synchronisation(device):
+    w = configs.random_c2(device, B=16, k=4, seed=8)
+    run_workload(w)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        run_workload(w)
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+
+
+def test_output_distribution_equals_target(device):
+    case = KATS["distribution"][0]
+    n = case["samples"]
+    drafts = [[int(t)] for t in np.random.default_rng(0).choice(3, size=n, p=case["q"])]
+    meta = make_metadata(drafts, device=device)
+    target = torch.tensor([case["p"]], dtype=torch.float32, device=device).log().repeat(n, 1)
+    q = torch.tensor([case["q"]], dtype=torch.float32, device=device).repeat(n, 1)
+    bonus = torch.full((n, 1), 2, dtype=torch.int32, device=device)
+    torch.manual_seed(0)
+    out = rs.rejection_sample(meta.draft_token_ids, meta.num_draft_tokens, 1,
+                              meta.cu_num_draft_tokens, q, target, bonus,
+                              sm_for([1.0] * n, drafts, device))[:, 0].cpu().numpy()
+    freq = np.bincount(out, minlength=3) / n
+    assert np.all(np.abs(freq - np.array(case["p"])) < case["threshold"]), freq
+
+
+def test_recovered_distribution_standalone(device):
+    case = KATS["distribution"][1]
+    n = case["samples"]
+    meta = make_metadata([[0]] * n, device=device)
+    p = torch.tensor([case["p"]], dtype=torch.float32, device=device).repeat(n, 1)
+    q = torch.tensor([case["q"]], dtype=torch.float32, device=device).repeat(n, 1)
+    torch.manual_seed(1)
+    rec = rs.sample_recovered_tokens(1, meta.num_draft_tokens, meta.cu_num_draft_tokens,
+                                     meta.draft_token_ids, q, p, sm_for([1.0] * n, [[0]] * n,
+                                                                        device), device)
+    freq = np.bincount(rec.cpu().numpy(), minlength=3) / n
+    assert freq[0] == 0.0
+    assert np.all(np.abs(freq - np.array(case["expected"])) < case["threshold"]), freq
+
+
+def test_standalone_recovered_matches_oracle(device):
+    w = configs.random_c2(device, B=16, k=4, seed=21)
+    probs = orc.target_probs(w.target_logits.cpu(), orc.row_temperatures(
+        w.temperature.cpu(), w.num_draft_tokens, False, True))
+    rec = rs.sample_recovered_tokens(w.max_spec_len, w.num_draft_tokens, w.cu_num_draft_tokens,
+                                     w.draft_token_ids, w.draft_probs, probs.to(device), None,
+                                     device, exp_noise=w.exp_noise)
+    scores = orc.recovered_scores(probs, w.draft_probs.cpu(), w.draft_token_ids.cpu(),
+                                  w.exp_noise.cpu(), w.num_draft_tokens)
+    assert torch.equal(rec.cpu(), orc.recovered_token_ids(scores))
+
+
+def test_seeded_generators_do_not_depend_on_batch(device):
+    """K=0 requests consume no randomness (tests/step59/test_rejection.py:466-485)."""
+    gen = torch.Generator(device=device).manual_seed(7)
+    p = [0.5, 0.5]
+    meta = make_metadata([[1], []], device=device)
+    logits = torch.tensor([p], dtype=torch.float32, device=device).log().repeat(3, 1)
+    q = torch.tensor([p], dtype=torch.float32, device=device)
+    bonus = torch.tensor([[0], [1]], dtype=torch.int32, device=device)
+    torch.manual_seed(11)
+    a = rs.rejection_sample(meta.draft_token_ids, meta.num_draft_tokens, 1,
+                            meta.cu_num_draft_tokens, q, logits[meta.target_logits_indices.long()],
+                            bonus, sm_for([1.0, 1.0], [[1], []], device, {0: gen})).cpu()
+    gen.manual_seed(7)
+    meta2 = make_metadata([[1]], device=device)
+    torch.manual_seed(11)
+    b = rs.rejection_sample(meta2.draft_token_ids, [1], 1, meta2.cu_num_draft_tokens, q,
+                            logits[:1], bonus[:1], sm_for([1.0], [[1]], device, {0: gen})).cpu()
+    assert a[0].tolist() == b[0].tolist()
+
+
+def test_forward_fast_path_matches_processed_path(device):
+    """RejectionSampler.forward folds gather + temperature into the kernel; the reference's
+    explicit gather + fp32 + div_ followed by rejection_sample must give the same ids."""
+    w = configs.random_c2(device, B=24, k=3, seed=31)
+    drafts = w.draft_token_ids.cpu().view(24, 3).tolist()
+    meta = make_metadata(drafts, device=device)
+    B, k, V = 24, 3, w.vocab_size
+    compact = torch.zeros((B * (k + 1), V), device=device)
+    compact[meta.target_logits_indices.long()] = w.target_logits
+    sm = replace(sm_for([0.8] * B, drafts, device), temperature=w.temperature)
+    u, e = w.uniforms, w.exp_noise
+    a = rs.rejection_sample(meta.draft_token_ids, meta.num_draft_tokens, k,
+                            meta.cu_num_draft_tokens, w.draft_probs, compact, w.bonus_token_ids,
+                            sm, uniform_probs=u, exp_noise=e,
+                            target_rows=meta.target_logits_indices, apply_temperature=True)
+    processed = rs.apply_sampling_constraints(compact[meta.target_logits_indices.long()].clone(),
+                                              meta.cu_num_draft_tokens, sm)
+    b = rs.rejection_sample(meta.draft_token_ids, meta.num_draft_tokens, k,
+                            meta.cu_num_draft_tokens, w.draft_probs, processed, w.bonus_token_ids,
+                            sm, uniform_probs=u, exp_noise=e)
+    assert torch.equal(a, b)

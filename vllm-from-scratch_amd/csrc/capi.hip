@@ -1,0 +1,292 @@
+// extern "C" entry points of libmvsd.so (declared in include/mvsd.h).
+//
+// Every function validates its arguments on the host, enqueues on the caller's stream and
+// returns a status code; nothing here synchronises the host or allocates device memory.
+#include <stdint.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "mvsd_device.h"
+#include "rows.h"
+#include "verify.h"
+
+namespace {
+
+thread_local int g_last_hip_error = 0;
+
+int hip_status(hipError_t err) {
+  if (err == hipSuccess) return MVSD_OK;
+  g_last_hip_error = (int)err;
+  return MVSD_E_HIP;
+}
+
+bool aligned16(const void* ptr, int64_t stride_bytes) {
+  return ((uintptr_t)ptr % 16 == 0) && (stride_bytes % 16 == 0);
+}
+
+int elem_size(int dtype) {
+  switch (dtype) {
+    case MVSD_F32: return 4;
+    case MVSD_BF16: return 2;
+    case MVSD_F16: return 2;
+    case MVSD_F64: return 8;
+    case MVSD_I32: return 4;
+    case MVSD_I64: return 8;
+    case MVSD_U8: return 1;
+    default: return 0;
+  }
+}
+
+constexpr int kMaxDevices = 64;
+
+// Resident-workgroup capacity of the verify kernel per device and dtype (CUs x occupancy).
+int verify_capacity(int device, int dtype) {
+  static std::mutex mu;
+  static int cache[kMaxDevices][3];
+  if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[device][dtype] > 0) return cache[device][dtype];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    return 0;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mvsd::verify_kernel_ptr(dtype),
+                                                   mvsd::kThreads, 0) != hipSuccess)
+    return 0;
+  if (per_cu < 1) per_cu = 1;
+  cache[device][dtype] = cus * per_cu;
+  return cache[device][dtype];
+}
+
+int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+struct WorkspaceLayout {
+  int64_t ctrl, grp_off, grp_cnt, req_cnt, stats, argv, argi, total;
+};
+
+WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
+  WorkspaceLayout l;
+  int64_t off = 0;
+  l.ctrl = off;
+  off = align_up(off + 2 * 4, 256);
+  l.grp_off = off;
+  off = align_up(off + (B + 1) * 4, 256);
+  l.grp_cnt = off;
+  off = align_up(off + (P > 0 ? P : 1) * 4, 256);
+  l.req_cnt = off;
+  off = align_up(off + (B > 0 ? B : 1) * 4, 256);
+  l.stats = off;
+  off = align_up(off + P * nc * 8, 256);
+  l.argv = off;
+  off = align_up(off + P * nc * 4, 256);
+  l.argi = off;
+  off = align_up(off + P * nc * 4, 256);
+  l.total = off;
+  return l;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mvsd_version(void) { return (0 << 16) | (1 << 8) | 0; }
+
+const char* mvsd_status_string(int status) {
+  switch (status) {
+    case MVSD_OK: return "ok";
+    case MVSD_E_INVALID: return "invalid argument";
+    case MVSD_E_ALIGN: return "misaligned pointer or stride";
+    case MVSD_E_WORKSPACE: return "workspace missing or too small";
+    case MVSD_E_HIP: return "HIP runtime error";
+    case MVSD_E_RANGE: return "size outside the supported range";
+    default: return "unknown status";
+  }
+}
+
+int mvsd_last_hip_error(void) { return g_last_hip_error; }
+
+int mvsd_expand_batch_to_tokens(void* out, const void* x, int dtype, const int32_t* cu_num_tokens,
+                                int64_t batch_size, int64_t num_tokens, double replace_from,
+                                double replace_to, mvsd_stream_t stream) {
+  if (batch_size < 0 || num_tokens < 0 || elem_size(dtype) == 0 || dtype == MVSD_BF16 ||
+      dtype == MVSD_F16)
+    return MVSD_E_INVALID;
+  if (batch_size == 0) return MVSD_OK;
+  if (!out || !x || !cu_num_tokens) return MVSD_E_INVALID;
+  if (batch_size > 0x7fffffff) return MVSD_E_RANGE;
+  return hip_status(mvsd::launch_expand(out, x, dtype, cu_num_tokens, batch_size, num_tokens,
+                                        replace_from, replace_to, (hipStream_t)stream));
+}
+
+int64_t mvsd_rejection_workspace_bytes(int64_t batch_size, int64_t num_tokens, int64_t vocab_size,
+                                       int target_dtype, int64_t max_spec_len) {
+  (void)max_spec_len;
+  if (batch_size < 0 || num_tokens < 0 || vocab_size <= 0) return -1;
+  const mvsd::VerifyPlan plan = mvsd::verify_plan(target_dtype, vocab_size);
+  return verify_layout(batch_size, num_tokens, plan.nc).total;
+}
+
+int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
+  if (!a) return MVSD_E_INVALID;
+  const int64_t B = a->batch_size, P = a->num_tokens, V = a->vocab_size;
+  if (B < 0 || P < 0 || V <= 0 || a->max_spec_len < 0) return MVSD_E_INVALID;
+  if (a->max_spec_len > mvsd::kMaxSpecLen) return MVSD_E_RANGE;
+  if (B > 0x7fffffff || P > 0x7fffffff || V > 0x7fffffff) return MVSD_E_RANGE;
+  if (B == 0) return MVSD_OK;
+  if (!a->output_token_ids || a->out_stride < a->max_spec_len + 1) return MVSD_E_INVALID;
+  if (!a->cu_num_draft_tokens || !a->bonus_token_ids) return MVSD_E_INVALID;
+  if (P > 0 && (!a->target_logits || !a->draft_token_ids)) return MVSD_E_INVALID;
+  if (a->target_dtype != MVSD_F32 && a->target_dtype != MVSD_BF16 && a->target_dtype != MVSD_F16)
+    return MVSD_E_INVALID;
+  if (a->draft_probs && a->draft_dtype != MVSD_F32) return MVSD_E_INVALID;
+  if (!a->all_greedy && !a->temperature) return MVSD_E_INVALID;
+  if (P > 0 && a->target_stride < V) return MVSD_E_INVALID;
+  if (P > 0 && a->target_rows && a->target_num_rows < 1) return MVSD_E_INVALID;
+  if (a->draft_probs && a->draft_stride < V) return MVSD_E_INVALID;
+  const bool need_uniforms = !a->all_greedy || a->synthetic_conditional_rates;
+  if (P > 0 && need_uniforms && !a->uniform_probs) return MVSD_E_INVALID;
+  const bool need_noise = !a->all_greedy && !a->recovered_token_ids;
+  if (P > 0 && need_noise && (!a->exp_noise || a->noise_stride < V)) return MVSD_E_INVALID;
+
+  const mvsd::VerifyPlan plan = mvsd::verify_plan(a->target_dtype, V);
+  const WorkspaceLayout lay = verify_layout(B, P, plan.nc);
+  if (!a->workspace || a->workspace_bytes < lay.total) return MVSD_E_WORKSPACE;
+  if ((uintptr_t)a->workspace % 256 != 0) return MVSD_E_ALIGN;
+
+  char* ws = static_cast<char*>(a->workspace);
+  mvsd::VerifyParams p;
+  memset(&p, 0, sizeof(p));
+  p.out = a->output_token_ids;
+  p.out_stride = a->out_stride;
+  p.target = a->target_logits;
+  p.target_stride = a->target_stride;
+  p.target_rows = a->target_rows;
+  p.target_num_rows = a->target_num_rows;
+  p.draft = static_cast<const float*>(a->draft_probs);
+  p.draft_stride = a->draft_stride;
+  p.noise = a->exp_noise;
+  p.noise_stride = a->noise_stride;
+  p.uniforms = a->uniform_probs;
+  p.draft_ids = a->draft_token_ids;
+  p.cu = a->cu_num_draft_tokens;
+  p.bonus = a->bonus_token_ids;
+  p.temperature = a->temperature;
+  p.recovered = a->recovered_token_ids;
+  p.synth = a->synthetic_conditional_rates;
+  p.target_dtype = a->target_dtype;
+  p.all_greedy = a->all_greedy ? 1 : 0;
+  p.apply_temperature = a->apply_temperature ? 1 : 0;
+  p.B = (int)B;
+  p.P = (int)P;
+  p.V = (int)V;
+  p.max_spec_len = (int)a->max_spec_len;
+  p.chunk = plan.chunk;
+  p.nc = plan.nc;
+  p.G = plan.g;
+  const int esz = elem_size(a->target_dtype);
+  p.target_aligned = aligned16(a->target_logits, a->target_stride * esz);
+  p.draft_aligned = a->draft_probs ? aligned16(a->draft_probs, a->draft_stride * 4) : false;
+  p.noise_aligned = a->exp_noise ? aligned16(a->exp_noise, a->noise_stride * 4) : false;
+  p.ctrl = reinterpret_cast<int*>(ws + lay.ctrl);
+  p.grp_off = reinterpret_cast<int*>(ws + lay.grp_off);
+  p.grp_cnt = reinterpret_cast<int*>(ws + lay.grp_cnt);
+  p.req_cnt = reinterpret_cast<int*>(ws + lay.req_cnt);
+  p.stats = reinterpret_cast<float2*>(ws + lay.stats);
+  p.argv = reinterpret_cast<float*>(ws + lay.argv);
+  p.argi = reinterpret_cast<int*>(ws + lay.argi);
+
+  int grid = 0;
+  if (P > 0) {
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return hip_status(err);
+    const int cap = verify_capacity(device, a->target_dtype);
+    if (cap <= 0) return hip_status(hipErrorInvalidDevice);
+    // Upper bound on tasks: groups <= min(P, B * ceil(max_spec_len / G)).
+    int64_t groups = B * ((a->max_spec_len + plan.g - 1) / plan.g);
+    if (groups > P) groups = P;
+    int64_t tasks = groups * plan.nc;
+    grid = (int)(tasks < cap ? tasks : cap);
+    if (grid < plan.nc) grid = plan.nc;
+  }
+  return hip_status(mvsd::launch_verify(p, a->target_dtype, grid, (hipStream_t)stream));
+}
+
+int mvsd_softmax_rows(float* probs, int64_t probs_stride, const void* logits, int dtype,
+                      int64_t logits_stride, const float* temperature, int64_t num_rows,
+                      int64_t vocab_size, mvsd_stream_t stream) {
+  if (num_rows < 0 || vocab_size <= 0) return MVSD_E_INVALID;
+  if (num_rows == 0) return MVSD_OK;
+  if (!probs || !logits || probs_stride < vocab_size || logits_stride < vocab_size)
+    return MVSD_E_INVALID;
+  if (dtype != MVSD_F32 && dtype != MVSD_BF16 && dtype != MVSD_F16) return MVSD_E_INVALID;
+  if (num_rows > 0x7fffffff) return MVSD_E_RANGE;
+  return hip_status(mvsd::launch_softmax_rows(probs, probs_stride, logits, dtype, logits_stride,
+                                              temperature, num_rows, vocab_size,
+                                              (hipStream_t)stream));
+}
+
+int mvsd_sample_recovered_tokens(int32_t* recovered_token_ids, const int32_t* cu_num_draft_tokens,
+                                 const int32_t* draft_token_ids, const float* draft_probs,
+                                 int64_t draft_stride, const float* target_probs,
+                                 int64_t target_stride, const float* exp_noise,
+                                 int64_t noise_stride, int64_t batch_size, int64_t num_tokens,
+                                 int64_t vocab_size, int64_t max_spec_len, mvsd_stream_t stream) {
+  if (batch_size < 0 || num_tokens < 0 || vocab_size <= 0 || max_spec_len < 0)
+    return MVSD_E_INVALID;
+  if (batch_size == 0 || num_tokens == 0 || max_spec_len == 0) return MVSD_OK;
+  if (!recovered_token_ids || !cu_num_draft_tokens || !draft_token_ids || !target_probs ||
+      !exp_noise)
+    return MVSD_E_INVALID;
+  if (target_stride < vocab_size || noise_stride < vocab_size ||
+      (draft_probs && draft_stride < vocab_size))
+    return MVSD_E_INVALID;
+  if (batch_size > 65535 * 1024LL || max_spec_len > 65535 || vocab_size > 0x7fffffff)
+    return MVSD_E_RANGE;
+  return hip_status(mvsd::launch_recovered(recovered_token_ids, cu_num_draft_tokens,
+                                           draft_token_ids, draft_probs, draft_stride,
+                                           target_probs, target_stride, exp_noise, noise_stride,
+                                           batch_size, max_spec_len, vocab_size, num_tokens,
+                                           (hipStream_t)stream));
+}
+
+int mvsd_ngram_propose(int32_t* drafts, int32_t* num_valid, int32_t* token_ids,
+                       int64_t row_stride, int64_t max_seq_len, const int32_t* num_tokens,
+                       const int32_t* new_tokens, int64_t new_tokens_stride,
+                       int64_t max_new_tokens, const int32_t* new_counts,
+                       const uint8_t* active, int gate_on_new_counts, int64_t num_reqs,
+                       int32_t min_n, int32_t max_n, int32_t k, int cap_by_model_len,
+                       int64_t max_model_len, mvsd_stream_t stream) {
+  if (num_reqs < 0) return MVSD_E_INVALID;
+  if (min_n < 1 || max_n < min_n || k < 1) return MVSD_E_INVALID;
+  if (max_n > mvsd::kNgramMaxN || k > 256) return MVSD_E_RANGE;
+  if (num_reqs == 0) return MVSD_OK;
+  if (!drafts || !num_valid || !token_ids || !num_tokens) return MVSD_E_INVALID;
+  if (max_seq_len < 0 || row_stride < max_seq_len) return MVSD_E_INVALID;
+  if (row_stride > 0x7fffffff || num_reqs > 0x7fffffff) return MVSD_E_RANGE;
+  if (new_tokens && (max_new_tokens < 0 || new_tokens_stride < max_new_tokens))
+    return MVSD_E_INVALID;
+  if (gate_on_new_counts && !new_counts) return MVSD_E_INVALID;
+  mvsd::NgramParams p;
+  p.drafts = drafts;
+  p.num_valid = num_valid;
+  p.tokens = token_ids;
+  p.row_stride = row_stride;
+  p.max_seq_len = max_seq_len;
+  p.num_tokens = num_tokens;
+  p.new_tokens = new_tokens;
+  p.new_stride = new_tokens_stride;
+  p.max_new = new_tokens ? max_new_tokens : 0;
+  p.new_counts = new_counts;
+  p.active = active;
+  p.gate_on_new_counts = gate_on_new_counts ? 1 : 0;
+  p.min_n = min_n;
+  p.max_n = max_n;
+  p.k = k;
+  p.cap_by_model_len = cap_by_model_len ? 1 : 0;
+  p.max_model_len = max_model_len;
+  return hip_status(mvsd::launch_ngram(p, num_reqs, (hipStream_t)stream));
+}
+
+}  // extern "C"

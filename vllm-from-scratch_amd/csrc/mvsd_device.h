@@ -1,0 +1,202 @@
+// Device-side helpers shared by the mvsd kernels (gfx950, wave64).
+//
+// Conventions used throughout:
+//   * workgroups are 256 threads = 4 wavefronts of 64 lanes;
+//   * streaming loads are 16-byte vector loads (4 x fp32 or 8 x bf16/fp16) laid out so
+//     that consecutive lanes touch consecutive 16-byte segments (fully coalesced);
+//   * argmax ties resolve to the lowest index and NaN ranks above every number, which is
+//     torch.argmax's rule and the first-index rule of the reference's Triton reduction
+//     (minivllm/sample/rejection_sampler.py:921-925).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mvsd.h"
+
+namespace mvsd {
+
+constexpr int kWave = 64;
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+// ------------------------------------------------------------------ element types ----
+
+template <int DT>
+struct Elem;
+
+template <>
+struct Elem<MVSD_F32> {
+  using storage = float;
+  static constexpr int kVec = 4;  // elements per 16-byte load
+  __device__ static inline float cvt(float v) { return v; }
+};
+
+template <>
+struct Elem<MVSD_BF16> {
+  using storage = uint16_t;
+  static constexpr int kVec = 8;
+  __device__ static inline float cvt(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
+};
+
+template <>
+struct Elem<MVSD_F16> {
+  using storage = _Float16;
+  static constexpr int kVec = 8;
+  __device__ static inline float cvt(_Float16 v) { return static_cast<float>(v); }
+};
+
+// Load kVec consecutive elements starting at p[idx] and convert them to fp32.  Elements at
+// or beyond `limit` are replaced by `fill`.  `aligned` (wave-uniform) says p + idx is 16-byte
+// aligned whenever idx is a multiple of kVec; otherwise scalar loads are used.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ inline void load_vec(const typename Elem<DT>::storage* __restrict__ p, int64_t idx,
+                                int64_t limit, bool aligned, float fill,
+                                float (&out)[Elem<DT>::kVec]) {
+  constexpr int V = Elem<DT>::kVec;
+  using S = typename Elem<DT>::storage;
+  if (aligned && idx + V <= limit) {
+    const u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + idx));
+    const S* s = reinterpret_cast<const S*>(&raw);
+#pragma unroll
+    for (int j = 0; j < V; ++j) out[j] = Elem<DT>::cvt(s[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) out[j] = (idx + j < limit) ? Elem<DT>::cvt(p[idx + j]) : fill;
+  }
+}
+
+// ------------------------------------------------------------------ comparisons ------
+
+// True when (a, ia) ranks above (b, ib): NaN above numbers, larger value, then lower index.
+__device__ inline bool argmax_better(float a, int ia, float b, int ib) {
+  const bool an = a != a;
+  const bool bn = b != b;
+  if (an | bn) return an && (!bn || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+
+// ------------------------------------------------------------------ wave reductions --
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ inline void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, kWave);
+    const int oi = __shfl_xor(i, o, kWave);
+    if (argmax_better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+__device__ inline int lane_id() { return threadIdx.x & (kWave - 1); }
+__device__ inline int wave_id() { return threadIdx.x / kWave; }
+
+// ------------------------------------------------------------------ block reductions -
+// Reduce N independent values across the 256-thread block.  `scratch` must hold
+// kWaves * N entries; every thread receives the results.  Two barriers.
+
+template <int N>
+__device__ inline void block_max(float (&v)[N], float* scratch) {
+#pragma unroll
+  for (int g = 0; g < N; ++g) v[g] = wave_max(v[g]);
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int g = 0; g < N; ++g) scratch[g * kWaves + wave_id()] = v[g];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < N; ++g) {
+    float m = scratch[g * kWaves];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) m = fmaxf(m, scratch[g * kWaves + w]);
+    v[g] = m;
+  }
+  __syncthreads();
+}
+
+template <int N>
+__device__ inline void block_sum(float (&v)[N], float* scratch) {
+#pragma unroll
+  for (int g = 0; g < N; ++g) v[g] = wave_sum(v[g]);
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int g = 0; g < N; ++g) scratch[g * kWaves + wave_id()] = v[g];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < N; ++g) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += scratch[g * kWaves + w];
+    v[g] = s;
+  }
+  __syncthreads();
+}
+
+template <int N>
+__device__ inline void block_argmax(float (&v)[N], int (&i)[N], float* sv, int* si) {
+#pragma unroll
+  for (int g = 0; g < N; ++g) wave_argmax(v[g], i[g]);
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int g = 0; g < N; ++g) {
+      sv[g * kWaves + wave_id()] = v[g];
+      si[g * kWaves + wave_id()] = i[g];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < N; ++g) {
+    float bv = sv[g * kWaves];
+    int bi = si[g * kWaves];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      if (argmax_better(sv[g * kWaves + w], si[g * kWaves + w], bv, bi)) {
+        bv = sv[g * kWaves + w];
+        bi = si[g * kWaves + w];
+      }
+    }
+    v[g] = bv;
+    i[g] = bi;
+  }
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------ atomics ----------
+// Agent-scope acquire/release on plain device memory; see the AMDGPU memory model for
+// gfx942/gfx950 (release writes back L2, acquire invalidates stale L1/L2 lines), which
+// makes partial results written by a workgroup on one XCD visible to another XCD.
+
+__device__ inline int atomic_add_release(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline int atomic_add_acq_rel(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline int atomic_add_relaxed(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline int atomic_load_acquire(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void atomic_store_relaxed(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace mvsd

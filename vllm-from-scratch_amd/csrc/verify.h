@@ -1,0 +1,66 @@
+// Host/device interface of the fused verification kernel (verify.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mvsd {
+
+constexpr int kMaxSpecLen = 128;  // reference MAX_SPEC_LEN, rejection_sampler.py:83
+
+// Kernel parameters, passed by value.  Pointers are device pointers; strides are in
+// elements.  The workspace pointers are carved by the host from one caller buffer.
+struct VerifyParams {
+  int32_t* out;
+  int64_t out_stride;
+  const void* target;
+  int64_t target_stride;
+  const int32_t* target_rows;
+  int64_t target_num_rows;
+  const float* draft;
+  int64_t draft_stride;
+  const float* noise;
+  int64_t noise_stride;
+  const double* uniforms;
+  const int32_t* draft_ids;
+  const int32_t* cu;
+  const int32_t* bonus;
+  const float* temperature;
+  const int32_t* recovered;
+  const float* synth;
+  int target_dtype;
+  int all_greedy;
+  int apply_temperature;
+  int B;
+  int P;
+  int V;
+  int max_spec_len;
+  int chunk;  // vocab columns per task
+  int nc;     // chunks per row
+  int G;      // rows per group
+  bool target_aligned;
+  bool draft_aligned;
+  bool noise_aligned;
+  // workspace
+  int* ctrl;      // [0] ticket, [1] spin-limit error flag
+  int* grp_off;   // [B + 1] exclusive scan of groups per request
+  int* grp_cnt;   // [P] published chunk stats per group
+  int* req_cnt;   // [B] finished tasks per request
+  float2* stats;  // [P * nc] (chunk max, chunk sumexp)
+  float* argv;    // [P * nc] chunk argmax value
+  int* argi;      // [P * nc] chunk argmax index
+};
+
+struct VerifyPlan {
+  int ept;    // elements per thread per row
+  int g;      // rows per group
+  int chunk;  // 256 * ept
+  int nc;     // ceil(V / chunk)
+};
+
+VerifyPlan verify_plan(int target_dtype, int64_t vocab_size);
+const void* verify_kernel_ptr(int target_dtype);
+hipError_t launch_verify(const VerifyParams& params, int target_dtype, int grid,
+                         hipStream_t stream);
+
+}  // namespace mvsd

@@ -1,0 +1,75 @@
+"""Build recipe for libmvsd.so (the HIP kernels + C ABI declared in include/mvsd.h).
+
+Compiles every ``csrc/*.hip`` for gfx950 with hipcc into one shared library next to this
+file.  Flags:
+  * ``-fhip-fp32-correctly-rounded-divide-sqrt``: IEEE fp32 division, so the temperature
+    divide and ``p / q`` round like the reference's fp32 arithmetic;
+  * ``-Xclang -target-feature -Xclang -packed-fp32-ops``: no packed-FP32 VALU instructions;
+  * no fast-math.
+
+Run ``python -m mvsd.build`` (from ``vllm-from-scratch_amd/``) or call :func:`build`.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+CSRC_DIR = PACKAGE_DIR.parent / "csrc"
+INCLUDE_DIR = PACKAGE_DIR.parent.parent / "include"
+LIB_NAME = "libmvsd.so"
+LIB_PATH = PACKAGE_DIR / LIB_NAME
+
+OFFLOAD_ARCH = os.environ.get("MVSD_OFFLOAD_ARCH", "gfx950")
+
+HIPCC_FLAGS = [
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    for candidate in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if candidate and Path(candidate).exists():
+            return candidate
+    raise RuntimeError("hipcc not found: set HIPCC or install ROCm under /opt/rocm")
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC_DIR.glob("*.hip"))
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile libmvsd.so in place (always rebuilds) and return its path."""
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-o", str(tmp), *map(str, srcs)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature; that is expected.
+    noise = "packed-fp32-ops"
+    stderr = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{stderr}")
+    if verbose and stderr.strip():
+        print(stderr, file=sys.stderr)
+    tmp.replace(LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,468 @@
+"""Speculative-decoding verification on MI355X (drop-in for minivllm/sample/rejection_sampler.py).
+
+Same public names, signatures, dtypes and error behaviour as the reference module:
+
+    RejectionSampler(sampler, spec_config=None, device=None)      (:86-406)
+    rejection_sample(draft_token_ids, num_draft_tokens, max_spec_len, cu_num_draft_tokens,
+                     draft_probs, target_logits, bonus_token_ids, sampling_metadata,
+                     synthetic_mode=False, synthetic_conditional_rates=None)   (:414-534)
+    apply_sampling_constraints / expand_batch_to_tokens / generate_uniform_probs /
+    sample_recovered_tokens, PLACEHOLDER_TOKEN_ID, GREEDY_TEMPERATURE, MAX_SPEC_LEN
+
+The arithmetic is one fused HIP launch (``mvsd_rejection_sample`` in include/mvsd.h): target
+softmax statistics, greedy argmax, exponential-race recovered tokens, acceptance chain and
+bonus emission, reading each target / draft / noise element once.  ``RejectionSampler.forward``
+also folds the gather of verify rows and the temperature divide into that launch when no
+logits processor or top-k/top-p needs the processed logits.
+
+Randomness is drawn by the same seams as the reference, and both stay monkeypatchable:
+``generate_uniform_probs`` (fp64 [P]) and the exponential noise of
+``sample_recovered_tokens`` (one Exp(1) row per request, drawn by
+``generate_exponential_noise``).  Callers may also pass them explicitly
+(``uniform_probs=``, ``exp_noise=``).  When a test replaces ``sample_recovered_tokens``
+the fused kernel takes its result as the recovered ids, as the reference's random kernel
+does.
+
+Differences from the reference, all on inputs the reference does not define:
+  * a draft id >= V is rejected (the reference reads out of bounds);
+  * acceptance compares the fp32 ratio p/q with the fp64 uniform using IEEE fp32 division
+    (the reference's Triton kernel uses its compiler's fp32 divide).
+"""
+
+from __future__ import annotations
+
+from dataclasses import replace
+from typing import TYPE_CHECKING
+
+import torch
+
+from .. import _native as nat
+from .metadata import SamplingMetadata
+from .ops.topk_topp_sampler import apply_top_k_top_p
+
+if TYPE_CHECKING:
+    from ..spec_decode.metadata import SpecDecodeMetadata
+
+PLACEHOLDER_TOKEN_ID = -1
+GREEDY_TEMPERATURE = 0
+MAX_SPEC_LEN = 128
+
+PROCESSED_LOGPROBS_MODES = ("processed_logits", "processed_logprobs")
+
+
+class RejectionSampler:
+    """Batch verifier with the reference's constructor and call protocol (:86-225).
+
+    ``sampler`` samples the bonus token from each request's bonus row exactly as in the
+    reference (:169-181); it is the caller's sampler object.
+    """
+
+    def __init__(self, sampler, spec_config=None, device: torch.device | None = None) -> None:
+        self.sampler = sampler
+        self.logprobs_mode = getattr(sampler, "logprobs_mode", "raw_logprobs")
+        self.is_processed_logprobs_mode = self.logprobs_mode in PROCESSED_LOGPROBS_MODES
+        self.is_logits_logprobs_mode = self.logprobs_mode in ("raw_logits", "processed_logits")
+        method = getattr(spec_config, "rejection_sample_method", "standard")
+        self.synthetic_conditional_rates: torch.Tensor | None = None
+        if spec_config is not None and method == "synthetic":
+            from ..spec_decode.utils import unconditional_to_conditional_rates
+
+            assert spec_config.synthetic_acceptance_rates is not None
+            self.synthetic_conditional_rates = torch.tensor(
+                unconditional_to_conditional_rates(spec_config.synthetic_acceptance_rates),
+                dtype=torch.float32, device=device)
+        self.synthetic_mode = self.synthetic_conditional_rates is not None
+        if method == "block":
+            raise NotImplementedError(
+                "rejection_sample_method='block' (block verification) exists only for the V2 "
+                "model runner; the V1 rejection sampler implements 'standard' and 'synthetic'")
+
+    def __call__(self, metadata: "SpecDecodeMetadata", draft_probs: torch.Tensor | None,
+                 logits: torch.Tensor, sampling_metadata: SamplingMetadata):
+        return self.forward(metadata, draft_probs, logits, sampling_metadata)
+
+    def forward(self, metadata: "SpecDecodeMetadata", draft_probs: torch.Tensor | None,
+                logits: torch.Tensor, sampling_metadata: SamplingMetadata):
+        """``logits`` is the compact ``[P + B, V]`` tensor in metadata row order (:153-225)."""
+        from ..outputs import SamplerOutput
+
+        assert metadata.max_spec_len <= MAX_SPEC_LEN
+        if len(sampling_metadata.prompt_token_ids) != len(metadata.num_draft_tokens):
+            raise ValueError(
+                f"sampling metadata has {len(sampling_metadata.prompt_token_ids)} rows but the "
+                f"spec metadata has {len(metadata.num_draft_tokens)} requests: they must match "
+                "request for request, in the same order")
+        if sampling_metadata.max_num_logprobs is not None:
+            raise NotImplementedError("speculative logprobs are not provided by this build")
+
+        # 1) bonus tokens from the bonus rows with the regular sampler (:169-181)
+        bonus_logits = logits[metadata.bonus_logits_indices]
+        bonus_out = self.sampler.forward(
+            bonus_logits, replace(sampling_metadata, max_num_logprobs=-1),
+            predict_bonus_token=True,
+            logprobs_mode_override=("processed_logits" if self.is_processed_logprobs_mode
+                                    else "raw_logits"))
+        bonus_token_ids = bonus_out.sampled_token_ids
+
+        needs_processing = (not sampling_metadata.no_penalties
+                            or _has_active_min_tokens(sampling_metadata)
+                            or sampling_metadata.top_k is not None
+                            or sampling_metadata.top_p is not None)
+        if not needs_processing:
+            # 2+3 fused: gather, fp32 upcast and temperature divide happen in the kernel
+            output_token_ids = rejection_sample(
+                metadata.draft_token_ids, metadata.num_draft_tokens, metadata.max_spec_len,
+                metadata.cu_num_draft_tokens, draft_probs, logits, bonus_token_ids,
+                sampling_metadata, synthetic_mode=self.synthetic_mode,
+                synthetic_conditional_rates=self.synthetic_conditional_rates,
+                target_rows=metadata.target_logits_indices, apply_temperature=True)
+        else:
+            target_logits = logits[metadata.target_logits_indices].to(torch.float32)
+            target_logits = self.apply_logits_processors(target_logits, sampling_metadata,
+                                                         metadata)
+            target_logits = apply_sampling_constraints(
+                target_logits, metadata.cu_num_draft_tokens, sampling_metadata)
+            output_token_ids = rejection_sample(
+                metadata.draft_token_ids, metadata.num_draft_tokens, metadata.max_spec_len,
+                metadata.cu_num_draft_tokens, draft_probs, target_logits, bonus_token_ids,
+                sampling_metadata, synthetic_mode=self.synthetic_mode,
+                synthetic_conditional_rates=self.synthetic_conditional_rates)
+        return SamplerOutput(sampled_token_ids=output_token_ids, logprobs_tensors=None)
+
+    def apply_logits_processors(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata,
+                                metadata: "SpecDecodeMetadata") -> torch.Tensor:
+        """Penalties and min_tokens over the hypothetical draft-prefix history (:338-356)."""
+        if not sampling_metadata.no_penalties or _has_active_min_tokens(sampling_metadata):
+            raise NotImplementedError(
+                "penalties and min_tokens on verify rows are not provided by this build")
+        return logits
+
+    @staticmethod
+    def parse_output(output_token_ids: torch.Tensor, vocab_size: int, discard_req_indices=(),
+                     logprobs_tensors=None):
+        """``[B, max_spec_len + 1]`` -> ``list[list[int]]``; the path's only D2H (:304-334)."""
+        if logprobs_tensors is not None:
+            raise NotImplementedError("speculative logprobs are not provided by this build")
+        out = output_token_ids.cpu().numpy()
+        valid = (out != PLACEHOLDER_TOKEN_ID) & (out < vocab_size)
+        if len(discard_req_indices) > 0:
+            valid[list(discard_req_indices)] = False
+        return [row[valid[i]].tolist() for i, row in enumerate(out)], None
+
+
+def _has_active_min_tokens(sm: SamplingMetadata) -> bool:
+    """True when some row still has to mask stop tokens (min_tokens not yet reached)."""
+    for index, min_tokens in enumerate(sm.min_tokens):
+        if min_tokens and index < len(sm.stop_token_ids) and sm.stop_token_ids[index]:
+            produced = len(sm.output_token_ids[index]) if index < len(sm.output_token_ids) else 0
+            if produced < min_tokens:
+                return True
+    return False
+
+
+# --------------------------------------------------------------------------- batch entry
+
+
+def rejection_sample(
+    draft_token_ids: torch.Tensor,
+    num_draft_tokens: list[int],
+    max_spec_len: int,
+    cu_num_draft_tokens: torch.Tensor,
+    draft_probs: torch.Tensor | None,
+    target_logits: torch.Tensor,
+    bonus_token_ids: torch.Tensor,
+    sampling_metadata: SamplingMetadata,
+    synthetic_mode: bool = False,
+    synthetic_conditional_rates: torch.Tensor | None = None,
+    *,
+    uniform_probs: torch.Tensor | None = None,
+    exp_noise: torch.Tensor | None = None,
+    target_rows: torch.Tensor | None = None,
+    apply_temperature: bool = False,
+) -> torch.Tensor:
+    """Verify a batch of drafts; returns ``[B, max_spec_len + 1]`` int32, -1 padded.
+
+    Reference signature and semantics (:414-534).  ``target_logits`` is ``[P, V]`` with the
+    temperature / top-k / top-p already applied, as in the reference.  Extensions:
+      * ``uniform_probs`` [P] fp64 and ``exp_noise`` [B, V] fp32 supply the randomness;
+      * ``target_rows`` [P] int32 selects verify row j as ``target_logits[target_rows[j]]``
+        (no gather copy), and ``apply_temperature`` divides by the request temperature in the
+        kernel (greedy T = 0 -> 1), which together replace the gather + ``div_`` that
+        RejectionSampler.forward runs before this function.
+    """
+    assert draft_token_ids.ndim == 1
+    assert draft_probs is None or draft_probs.ndim == 2
+    assert cu_num_draft_tokens.ndim == 1
+    assert target_logits.ndim == 2
+    nat.require_device_tensor(target_logits, "target_logits")
+
+    batch_size = len(num_draft_tokens)
+    num_tokens = draft_token_ids.shape[0]
+    vocab_size = target_logits.shape[-1]
+    device = target_logits.device
+    assert draft_token_ids.is_contiguous()
+    assert draft_probs is None or draft_probs.is_contiguous()
+    assert bonus_token_ids.is_contiguous()
+    if target_rows is None:
+        assert target_logits.shape == (num_tokens, vocab_size)
+    else:
+        assert target_rows.shape == (num_tokens,)
+    assert max_spec_len <= MAX_SPEC_LEN
+    assert cu_num_draft_tokens.shape[0] == batch_size
+
+    output_token_ids = torch.empty((batch_size, max_spec_len + 1), dtype=torch.int32,
+                                   device=device)
+    if batch_size == 0:
+        return output_token_ids
+
+    all_greedy = bool(sampling_metadata.all_greedy)
+    temperature = None
+    if not all_greedy:
+        temperature = _as(sampling_metadata.temperature, torch.float32, device)
+
+    if uniform_probs is None and (synthetic_mode or not all_greedy):
+        uniform_probs = generate_uniform_probs(num_tokens, num_draft_tokens,
+                                               sampling_metadata.generators, device)
+    recovered_token_ids = None
+    if not all_greedy and num_tokens > 0:
+        if sample_recovered_tokens is not _SAMPLE_RECOVERED_TOKENS:
+            # a caller replaced the seam: give it materialised probabilities, as the
+            # reference does, and use the ids it returns
+            target_probs = _softmax_rows(target_logits, target_rows,
+                                         _expand_temperature(temperature, cu_num_draft_tokens,
+                                                             num_tokens)
+                                         if apply_temperature else None)
+            recovered_token_ids = sample_recovered_tokens(
+                max_spec_len, num_draft_tokens, cu_num_draft_tokens, draft_token_ids,
+                draft_probs, target_probs, sampling_metadata, device)
+        elif exp_noise is None:
+            exp_noise = generate_exponential_noise(batch_size, vocab_size, num_draft_tokens,
+                                                   sampling_metadata.generators, device)
+
+    rates = None
+    if synthetic_mode:
+        assert synthetic_conditional_rates is not None
+        rates = _as(synthetic_conditional_rates, torch.float32, device)
+        if rates.shape[0] < max_spec_len:
+            raise ValueError(f"synthetic_conditional_rates has {rates.shape[0]} entries but "
+                             f"max_spec_len is {max_spec_len}")
+
+    draft_ids = _as(draft_token_ids, torch.int32, device)
+    cu = _as(cu_num_draft_tokens, torch.int32, device)
+    bonus = _as(bonus_token_ids.reshape(-1), torch.int32, device)
+    rows = None if target_rows is None else _as(target_rows, torch.int32, device)
+    if uniform_probs is not None:
+        uniform_probs = _as(uniform_probs, torch.float64, device)
+    if recovered_token_ids is not None:
+        recovered_token_ids = _as(recovered_token_ids, torch.int32, device)
+    if draft_probs is not None:
+        nat.require_device_tensor(draft_probs, "draft_probs")
+        if draft_probs.dtype != torch.float32:
+            raise TypeError(f"draft_probs must be float32, got {draft_probs.dtype}")
+        assert draft_probs.shape == (num_tokens, vocab_size)
+    if exp_noise is not None:
+        exp_noise = _as(exp_noise, torch.float32, device)
+        assert exp_noise.shape == (batch_size, vocab_size) and exp_noise.stride(1) == 1
+    if target_logits.stride(1) != 1:
+        target_logits = target_logits.contiguous()
+
+    dtype = nat.dtype_code(target_logits.dtype)
+    handle = nat.lib()
+    ws_bytes = handle.mvsd_rejection_workspace_bytes(batch_size, num_tokens, vocab_size, dtype,
+                                                     max_spec_len)
+    workspace = torch.empty(max(int(ws_bytes), 256), dtype=torch.uint8, device=device)
+    args = nat.RejectionArgs(
+        output_token_ids=output_token_ids.data_ptr(),
+        out_stride=output_token_ids.stride(0),
+        target_logits=target_logits.data_ptr(),
+        target_dtype=dtype,
+        target_stride=target_logits.stride(0),
+        target_rows=nat.ptr(rows),
+        target_num_rows=target_logits.shape[0],
+        draft_probs=nat.ptr(draft_probs),
+        draft_dtype=nat.F32,
+        draft_stride=draft_probs.stride(0) if draft_probs is not None else 0,
+        exp_noise=nat.ptr(exp_noise),
+        noise_stride=exp_noise.stride(0) if exp_noise is not None else 0,
+        uniform_probs=nat.ptr(uniform_probs),
+        draft_token_ids=draft_ids.data_ptr(),
+        cu_num_draft_tokens=cu.data_ptr(),
+        bonus_token_ids=bonus.data_ptr(),
+        temperature=nat.ptr(temperature),
+        all_greedy=int(all_greedy),
+        apply_temperature=int(bool(apply_temperature)),
+        recovered_token_ids=nat.ptr(recovered_token_ids),
+        synthetic_conditional_rates=nat.ptr(rates),
+        batch_size=batch_size,
+        num_tokens=num_tokens,
+        vocab_size=vocab_size,
+        max_spec_len=max_spec_len,
+        workspace=workspace.data_ptr(),
+        workspace_bytes=workspace.numel(),
+    )
+    nat.check(handle.mvsd_rejection_sample(args, nat.stream_of(device)), "mvsd_rejection_sample")
+    return output_token_ids
+
+
+def apply_sampling_constraints(
+    logits: torch.Tensor,               # [num_tokens, vocab_size]
+    cu_num_draft_tokens: torch.Tensor,  # [batch_size]
+    sampling_metadata: SamplingMetadata,
+) -> torch.Tensor:
+    """Per-row temperature divide (greedy T=0 -> 1) then top-k/top-p, in place (:537-571)."""
+    assert logits.ndim == 2
+    assert cu_num_draft_tokens.ndim == 1
+    if sampling_metadata.all_greedy:
+        return logits
+    num_tokens = logits.shape[0]
+    temperature = expand_batch_to_tokens(sampling_metadata.temperature, cu_num_draft_tokens,
+                                         num_tokens, replace_from=GREEDY_TEMPERATURE,
+                                         replace_to=1)
+    logits.div_(temperature.unsqueeze(-1))
+    top_k = None
+    if sampling_metadata.top_k is not None:
+        top_k = expand_batch_to_tokens(sampling_metadata.top_k, cu_num_draft_tokens, num_tokens)
+    top_p = None
+    if sampling_metadata.top_p is not None:
+        top_p = expand_batch_to_tokens(sampling_metadata.top_p, cu_num_draft_tokens, num_tokens)
+    return apply_top_k_top_p(logits, top_k, top_p)
+
+
+def expand_batch_to_tokens(
+    x: torch.Tensor,              # [batch_size]
+    cu_num_tokens: torch.Tensor,  # [batch_size]
+    num_tokens: int,
+    replace_from: int = 0,
+    replace_to: int = 0,
+) -> torch.Tensor:
+    """``[B] -> [num_tokens]``: request i's value repeated over its rows (:574-597)."""
+    batch_size = x.shape[0]
+    assert cu_num_tokens.shape[0] == batch_size
+    expanded = x.new_empty(num_tokens)
+    if batch_size == 0:
+        return expanded
+    nat.require_device_tensor(x, "x")
+    src = x.contiguous()
+    cu = _as(cu_num_tokens, torch.int32, x.device)
+    code = nat.dtype_code(src.dtype)
+    nat.check(nat.lib().mvsd_expand_batch_to_tokens(
+        expanded.data_ptr(), src.data_ptr(), code, cu.data_ptr(), batch_size, num_tokens,
+        float(replace_from), float(replace_to), nat.stream_of(x.device)),
+        "mvsd_expand_batch_to_tokens")
+    return expanded
+
+
+def generate_uniform_probs(
+    num_tokens: int,
+    num_draft_tokens: list[int],
+    generators: dict[int, torch.Generator],
+    device: torch.device,
+) -> torch.Tensor:
+    """One fp64 uniform per verify row; seeded requests draw from their own generator and
+    requests without drafts consume nothing (:600-624)."""
+    uniform_probs = torch.rand((num_tokens,), dtype=torch.float64, device=device)
+    start = 0
+    for req_idx, n in enumerate(num_draft_tokens):
+        if n == 0:
+            continue
+        generator = generators.get(req_idx)
+        if generator is not None:
+            uniform_probs[start:start + n].uniform_(generator=generator)
+        start += n
+    return uniform_probs
+
+
+def generate_exponential_noise(
+    batch_size: int,
+    vocab_size: int,
+    num_draft_tokens: list[int],
+    generators: dict[int, torch.Generator],
+    device: torch.device,
+) -> torch.Tensor:
+    """One Exp(1) row per request, seeded rows from their generator, requests without
+    drafts leaving their generator untouched (:646-653)."""
+    noise = torch.empty((batch_size, vocab_size), dtype=torch.float32, device=device)
+    noise.exponential_()
+    for index, generator in generators.items():
+        if num_draft_tokens[index] > 0:
+            noise[index].exponential_(generator=generator)
+    return noise
+
+
+def sample_recovered_tokens(
+    max_spec_len: int,
+    num_draft_tokens: list[int],
+    cu_num_draft_tokens: torch.Tensor,  # [batch_size]
+    draft_token_ids: torch.Tensor,      # [num_tokens]
+    draft_probs: torch.Tensor | None,   # [num_tokens, vocab_size]
+    target_probs: torch.Tensor,         # [num_tokens, vocab_size]
+    sampling_metadata: SamplingMetadata,
+    device: torch.device,
+    *,
+    exp_noise: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Recovered ids ``argmax_v max(p - q, 0) * (1 / E[req, v])`` from materialised
+    probabilities (:627-670); ``draft_probs=None`` is the point-mass form."""
+    batch_size = len(num_draft_tokens)
+    vocab_size = target_probs.shape[-1]
+    nat.require_device_tensor(target_probs, "target_probs")
+    if exp_noise is None:
+        exp_noise = generate_exponential_noise(batch_size, vocab_size, num_draft_tokens,
+                                               sampling_metadata.generators, device)
+    recovered = torch.empty_like(draft_token_ids)
+    if draft_token_ids.shape[0] == 0 or max_spec_len == 0:
+        return recovered
+    out32 = recovered if recovered.dtype == torch.int32 else torch.empty(
+        recovered.shape, dtype=torch.int32, device=device)
+    cu = _as(cu_num_draft_tokens, torch.int32, device)
+    ids = _as(draft_token_ids, torch.int32, device)
+    tp = _as(target_probs, torch.float32, device)
+    dp = None if draft_probs is None else _as(draft_probs, torch.float32, device)
+    noise = _as(exp_noise, torch.float32, device)
+    nat.check(nat.lib().mvsd_sample_recovered_tokens(
+        out32.data_ptr(), cu.data_ptr(), ids.data_ptr(), nat.ptr(dp),
+        dp.stride(0) if dp is not None else 0, tp.data_ptr(), tp.stride(0), noise.data_ptr(),
+        noise.stride(0), batch_size, draft_token_ids.shape[0], vocab_size, max_spec_len,
+        nat.stream_of(device)), "mvsd_sample_recovered_tokens")
+    if out32 is not recovered:
+        recovered.copy_(out32)
+    return recovered
+
+
+_SAMPLE_RECOVERED_TOKENS = sample_recovered_tokens
+
+
+# --------------------------------------------------------------------------- helpers
+
+
+def _as(t: torch.Tensor, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """Contiguous tensor of ``dtype`` on ``device`` (no copy when it already is one)."""
+    if t.device != device:
+        t = t.to(device)
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    return t.contiguous()
+
+
+def _expand_temperature(temperature: torch.Tensor | None, cu: torch.Tensor,
+                        num_tokens: int) -> torch.Tensor | None:
+    if temperature is None:
+        return None
+    return expand_batch_to_tokens(temperature, cu, num_tokens, replace_from=GREEDY_TEMPERATURE,
+                                  replace_to=1)
+
+
+def _softmax_rows(logits: torch.Tensor, rows: torch.Tensor | None,
+                  row_temperature: torch.Tensor | None) -> torch.Tensor:
+    """fp32 probabilities of the verify rows (HIP kernel ``mvsd_softmax_rows``)."""
+    src = logits if rows is None else logits[rows.long()]
+    src = src.contiguous()
+    probs = torch.empty(src.shape, dtype=torch.float32, device=src.device)
+    if src.shape[0] == 0:
+        return probs
+    temp = None if row_temperature is None else _as(row_temperature, torch.float32, src.device)
+    nat.check(nat.lib().mvsd_softmax_rows(
+        probs.data_ptr(), probs.stride(0), src.data_ptr(), nat.dtype_code(src.dtype),
+        src.stride(0), nat.ptr(temp), src.shape[0], src.shape[1], nat.stream_of(src.device)),
+        "mvsd_softmax_rows")
+    return probs
