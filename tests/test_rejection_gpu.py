@@ -115,6 +115,33 @@ def test_rejection_sampler_forward_greedy_kats(case, device):
     assert parsed == [[t for t in row if t != -1] for row in case["expected"]]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("V", [5, 64, 4096 + 8, 151936])
+def test_greedy_argmax_at_every_position(device, dtype, V):
+    """One row per argmax position (vector-lane 0..7, thread boundaries, chunk boundaries,
+    last column), plus ties that must resolve to the first index."""
+    positions = sorted({p for p in [0, 1, 2, 3, 4, 7, 8, 9, 1023, 1024, 4095, 4096, 4097,
+                                    8191, 8192, V - 2, V - 1] if 0 <= p < V})
+    P = len(positions)
+    logits = torch.randn((P, V), device=device).clamp(-3, 3).to(dtype)
+    for r, pos in enumerate(positions):
+        logits[r, pos] = 10.0
+    tie = torch.full((2, V), -1.0, device=device, dtype=dtype)
+    tie[0, [V - 1, max(V - 3, 0)]] = 5.0
+    tie[1, :] = 2.0
+    logits = torch.cat([logits, tie])
+    drafts = [[0] for _ in range(P + 2)]
+    meta = make_metadata(drafts, device=device)
+    out = rs.rejection_sample(meta.draft_token_ids, meta.num_draft_tokens, 1,
+                              meta.cu_num_draft_tokens, None, logits,
+                              torch.full((P + 2, 1), 7, dtype=torch.int32, device=device),
+                              sm_for([0.0] * (P + 2), drafts, device))
+    expect = positions + [max(V - 3, 0), 0]
+    got = out[:, 0].cpu().tolist()
+    assert got == expect
+    assert got == logits.float().argmax(-1).cpu().tolist()
+
+
 def test_expand_kats(device):
     for case in KATS["expand"]:
         x = torch.tensor(case["x"], device=device)

@@ -71,11 +71,22 @@ __device__ inline void load_vec(const typename Elem<DT>::storage* __restrict__ p
 // ------------------------------------------------------------------ comparisons ------
 
 // True when (a, ia) ranks above (b, ib): NaN above numbers, larger value, then lower index.
+// Written branch-free (bitwise logic only): the short-circuit form was lowered by the gfx950
+// backend into a control-flow diamond whose phi moves dropped the update for the first
+// element of an unrolled argmax loop.
 __device__ inline bool argmax_better(float a, int ia, float b, int ib) {
   const bool an = a != a;
   const bool bn = b != b;
-  if (an | bn) return an && (!bn || ia < ib);
-  return a > b || (a == b && ia < ib);
+  const bool lower = ia < ib;
+  const bool num = (a > b) | ((a == b) & lower);
+  return (an & (!bn | lower)) | (!an & !bn & num);
+}
+
+// (bv, bi) <- (v, i) when (v, i) ranks above it and `valid`; branch-free select.
+__device__ inline void argmax_update(float& bv, int& bi, float v, int i, bool valid) {
+  const bool take = valid & argmax_better(v, i, bv, bi);
+  bv = take ? v : bv;
+  bi = take ? i : bi;
 }
 
 // ------------------------------------------------------------------ wave reductions --
@@ -97,10 +108,7 @@ __device__ inline void wave_argmax(float& v, int& i) {
   for (int o = kWave / 2; o > 0; o >>= 1) {
     const float ov = __shfl_xor(v, o, kWave);
     const int oi = __shfl_xor(i, o, kWave);
-    if (argmax_better(ov, oi, v, i)) {
-      v = ov;
-      i = oi;
-    }
+    argmax_update(v, i, ov, oi, true);
   }
 }
 
@@ -166,12 +174,7 @@ __device__ inline void block_argmax(float (&v)[N], int (&i)[N], float* sv, int* 
     float bv = sv[g * kWaves];
     int bi = si[g * kWaves];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) {
-      if (argmax_better(sv[g * kWaves + w], si[g * kWaves + w], bv, bi)) {
-        bv = sv[g * kWaves + w];
-        bi = si[g * kWaves + w];
-      }
-    }
+    for (int w = 1; w < kWaves; ++w) argmax_update(bv, bi, sv[g * kWaves + w], si[g * kWaves + w], true);
     v[g] = bv;
     i[g] = bi;
   }

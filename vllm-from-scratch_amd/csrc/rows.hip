@@ -144,10 +144,7 @@ __global__ __launch_bounds__(kThreads) void recovered_kernel(
     const float prob = tp[v];
     const float w = dp ? fmaxf(prob - dp[v], 0.f) : (v == d ? 0.f : prob);
     const float score = w * (1.0f / np[v]);
-    if (argmax_better(score, (int)v, bv, bi)) {
-      bv = score;
-      bi = (int)v;
-    }
+    argmax_update(bv, bi, score, (int)v, true);
   }
   float vv[1] = {bv};
   int ii[1] = {bi};

@@ -127,12 +127,7 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
       float bv = -INFINITY;
       int bi = INT_MAX;
       for (int c = lane; c < nc; c += kWave) {
-        const float v = p.argv[row * nc + c];
-        const int i = p.argi[row * nc + c];
-        if (argmax_better(v, i, bv, bi)) {
-          bv = v;
-          bi = i;
-        }
+        argmax_update(bv, bi, p.argv[row * nc + c], p.argi[row * nc + c], true);
       }
       wave_argmax(bv, bi);
       if (lane == 0) s_tok[k] = full ? min(bi, p.V - 1) : bi;
@@ -292,11 +287,7 @@ __global__ __launch_bounds__(kThreads) void verify_kernel(VerifyParams p) {
 #pragma unroll
           for (int j = 0; j < VEC; ++j) {
             const int idx = (int)(v0 + ((int64_t)i * kThreads + tid) * VEC + j);
-            const float v = x[g][i * VEC + j];
-            if (idx < vend && argmax_better(v, idx, bv[g], bi[g])) {
-              bv[g] = v;
-              bi[g] = idx;
-            }
+            argmax_update(bv[g], bi[g], x[g][i * VEC + j], idx, idx < vend);
           }
         }
       }
@@ -419,10 +410,7 @@ __global__ __launch_bounds__(kThreads) void verify_kernel(VerifyParams p) {
                   const float prob = x[g][i * VEC + h + j] * f;
                   const float w = dbase ? fmaxf(prob - q[j], 0.f) : (idx == d ? 0.f : prob);
                   const float score = w * inv[i * VEC + h + j];
-                  if (idx < vend && argmax_better(score, idx, bv[g], bi[g])) {
-                    bv[g] = score;
-                    bi[g] = idx;
-                  }
+                  argmax_update(bv[g], bi[g], score, idx, idx < vend);
                 }
               }
             }
