@@ -127,9 +127,17 @@ typedef struct mvsd_rejection_args {
   int64_t workspace_bytes;
 } mvsd_rejection_args;
 
+/* Workspace contract: zero-filled before its first use (mvsd_rejection_workspace_init, or
+ * any zeroed allocation); every call leaves it zero-filled again except for the int at
+ * byte offset 4, a sticky flag that becomes non-zero if a wait inside the kernel ever hit
+ * its spin bound (results of that call are then unreliable).  One workspace must not be used by two
+ * calls that can run concurrently (different streams).  Sizes: the query below is monotone
+ * in every argument, so a workspace sized for the largest batch serves smaller ones. */
 int64_t mvsd_rejection_workspace_bytes(int64_t batch_size, int64_t num_tokens,
                                        int64_t vocab_size, int target_dtype,
                                        int64_t max_spec_len);
+/* Zero-fill a workspace on `stream` with a kernel (no hipMemsetAsync). */
+int mvsd_rejection_workspace_init(void* workspace, int64_t workspace_bytes, mvsd_stream_t stream);
 int mvsd_rejection_sample(const mvsd_rejection_args* args, mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */

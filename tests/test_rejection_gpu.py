@@ -259,6 +259,26 @@ def test_repeated_calls_are_identical(device):
     assert torch.equal(a, b) and torch.equal(a, d) and c.shape == (3, 3)
 
 
+def test_workspace_is_left_zeroed_across_shapes(device):
+    """Calls of different shapes share one cached workspace; each must leave it zeroed (only
+    the sticky spin flag may differ, and it must stay clear)."""
+    big = configs.random_c2(device, B=96, k=4, seed=41)
+    small = configs.random_c2(device, B=8, k=2, seed=42)
+    greedy = configs.greedy_c1(device, B=40, k=5, seed=43)
+    expect = {id(w): oracle_for(w).output_token_ids for w in (big, small, greedy)}
+    for w in (big, small, greedy, small, big, greedy, big):
+        out = run_workload(w).cpu().numpy()
+        rep = orc.compare(out, orc.OracleResult(expect[id(w)], *([np.full(w.num_tokens, np.nan)] * 4),
+                                                np.zeros(w.num_tokens, bool)),
+                          w.draft_token_ids.cpu(), w.num_draft_tokens)
+        assert rep.mismatched == 0, (w.name, rep)
+    torch.cuda.synchronize()
+    assert rs.workspace_error_flag(device) == 0
+    for ws in rs._WORKSPACES.values():
+        words = ws.view(torch.int32)
+        assert int(words[0]) == 0 and int(words[2:].abs().sum()) == 0
+
+
 def test_no_host_synchronisation(device):
     w = configs.random_c2(device, B=16, k=4, seed=8)
     run_workload(w)

@@ -52,7 +52,7 @@ int verify_capacity(int device, int dtype) {
     return 0;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mvsd::verify_kernel_ptr(dtype),
-                                                   mvsd::kThreads, 0) != hipSuccess)
+                                                   mvsd::kVThreads, 0) != hipSuccess)
     return 0;
   if (per_cu < 1) per_cu = 1;
   cache[device][dtype] = cus * per_cu;
@@ -61,27 +61,24 @@ int verify_capacity(int device, int dtype) {
 
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
+// Workspace layout.  ctrl = {ticket, sticky spin-limit flag (byte offset 4), exit counter}.
 struct WorkspaceLayout {
-  int64_t ctrl, grp_off, grp_cnt, req_cnt, stats, argv, argi, total;
+  int64_t ctrl, grp_off, req_cnt, stat_slots, arg_slots, total;
 };
 
 WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
   WorkspaceLayout l;
   int64_t off = 0;
   l.ctrl = off;
-  off = align_up(off + 2 * 4, 256);
+  off = align_up(off + 3 * 4, 256);
   l.grp_off = off;
   off = align_up(off + (B + 1) * 4, 256);
-  l.grp_cnt = off;
-  off = align_up(off + (P > 0 ? P : 1) * 4, 256);
   l.req_cnt = off;
   off = align_up(off + (B > 0 ? B : 1) * 4, 256);
-  l.stats = off;
+  l.stat_slots = off;
   off = align_up(off + P * nc * 8, 256);
-  l.argv = off;
-  off = align_up(off + P * nc * 4, 256);
-  l.argi = off;
-  off = align_up(off + P * nc * 4, 256);
+  l.arg_slots = off;
+  off = align_up(off + P * nc * 8, 256);
   l.total = off;
   return l;
 }
@@ -125,6 +122,12 @@ int64_t mvsd_rejection_workspace_bytes(int64_t batch_size, int64_t num_tokens, i
   if (batch_size < 0 || num_tokens < 0 || vocab_size <= 0) return -1;
   const mvsd::VerifyPlan plan = mvsd::verify_plan(target_dtype, vocab_size);
   return verify_layout(batch_size, num_tokens, plan.nc).total;
+}
+
+int mvsd_rejection_workspace_init(void* workspace, int64_t workspace_bytes, mvsd_stream_t stream) {
+  if (!workspace || workspace_bytes < 0) return MVSD_E_INVALID;
+  if ((uintptr_t)workspace % 256 != 0) return MVSD_E_ALIGN;
+  return hip_status(mvsd::launch_zero_fill(workspace, workspace_bytes, (hipStream_t)stream));
 }
 
 int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
@@ -190,11 +193,9 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   p.noise_aligned = a->exp_noise ? aligned16(a->exp_noise, a->noise_stride * 4) : false;
   p.ctrl = reinterpret_cast<int*>(ws + lay.ctrl);
   p.grp_off = reinterpret_cast<int*>(ws + lay.grp_off);
-  p.grp_cnt = reinterpret_cast<int*>(ws + lay.grp_cnt);
   p.req_cnt = reinterpret_cast<int*>(ws + lay.req_cnt);
-  p.stats = reinterpret_cast<float2*>(ws + lay.stats);
-  p.argv = reinterpret_cast<float*>(ws + lay.argv);
-  p.argi = reinterpret_cast<int*>(ws + lay.argi);
+  p.stat_slots = reinterpret_cast<uint64_t*>(ws + lay.stat_slots);
+  p.arg_slots = reinterpret_cast<uint64_t*>(ws + lay.arg_slots);
 
   int grid = 0;
   if (P > 0) {

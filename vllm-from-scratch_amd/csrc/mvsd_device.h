@@ -116,65 +116,66 @@ __device__ inline int lane_id() { return threadIdx.x & (kWave - 1); }
 __device__ inline int wave_id() { return threadIdx.x / kWave; }
 
 // ------------------------------------------------------------------ block reductions -
-// Reduce N independent values across the 256-thread block.  `scratch` must hold
-// kWaves * N entries; every thread receives the results.  Two barriers.
+// Reduce N independent values across a block of NW wavefronts (default: the 256-thread
+// block).  `scratch` must hold NW * N entries; every thread receives the results.  Two
+// barriers.
 
-template <int N>
+template <int N, int NW = kWaves>
 __device__ inline void block_max(float (&v)[N], float* scratch) {
 #pragma unroll
   for (int g = 0; g < N; ++g) v[g] = wave_max(v[g]);
   if (lane_id() == 0) {
 #pragma unroll
-    for (int g = 0; g < N; ++g) scratch[g * kWaves + wave_id()] = v[g];
+    for (int g = 0; g < N; ++g) scratch[g * NW + wave_id()] = v[g];
   }
   __syncthreads();
 #pragma unroll
   for (int g = 0; g < N; ++g) {
-    float m = scratch[g * kWaves];
+    float m = scratch[g * NW];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) m = fmaxf(m, scratch[g * kWaves + w]);
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, scratch[g * NW + w]);
     v[g] = m;
   }
   __syncthreads();
 }
 
-template <int N>
+template <int N, int NW = kWaves>
 __device__ inline void block_sum(float (&v)[N], float* scratch) {
 #pragma unroll
   for (int g = 0; g < N; ++g) v[g] = wave_sum(v[g]);
   if (lane_id() == 0) {
 #pragma unroll
-    for (int g = 0; g < N; ++g) scratch[g * kWaves + wave_id()] = v[g];
+    for (int g = 0; g < N; ++g) scratch[g * NW + wave_id()] = v[g];
   }
   __syncthreads();
 #pragma unroll
   for (int g = 0; g < N; ++g) {
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) s += scratch[g * kWaves + w];
+    for (int w = 0; w < NW; ++w) s += scratch[g * NW + w];
     v[g] = s;
   }
   __syncthreads();
 }
 
-template <int N>
+template <int N, int NW = kWaves>
 __device__ inline void block_argmax(float (&v)[N], int (&i)[N], float* sv, int* si) {
 #pragma unroll
   for (int g = 0; g < N; ++g) wave_argmax(v[g], i[g]);
   if (lane_id() == 0) {
 #pragma unroll
     for (int g = 0; g < N; ++g) {
-      sv[g * kWaves + wave_id()] = v[g];
-      si[g * kWaves + wave_id()] = i[g];
+      sv[g * NW + wave_id()] = v[g];
+      si[g * NW + wave_id()] = i[g];
     }
   }
   __syncthreads();
 #pragma unroll
   for (int g = 0; g < N; ++g) {
-    float bv = sv[g * kWaves];
-    int bi = si[g * kWaves];
+    float bv = sv[g * NW];
+    int bi = si[g * NW];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) argmax_update(bv, bi, sv[g * kWaves + w], si[g * kWaves + w], true);
+    for (int w = 1; w < NW; ++w) argmax_update(bv, bi, sv[g * NW + w], si[g * NW + w], true);
     v[g] = bv;
     i[g] = bi;
   }
@@ -200,6 +201,50 @@ __device__ inline int atomic_load_acquire(const int* p) {
 }
 __device__ inline void atomic_store_relaxed(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------------ partial slots ----
+// 64-bit self-describing slots exchanged between workgroups with relaxed agent-scope atomics
+// (coherent across XCDs without any fence, hence without L2 write-back or invalidation).  An
+// empty slot holds 0 and no written slot can be 0, so a reader polls the data itself.
+
+__device__ inline void slot_store(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t slot_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// (chunk max, chunk sumexp): s >= 1 whenever m is finite and m = -inf has a non-zero bit
+// pattern, so a written stats slot is never 0.  NaN maxima are stored canonically.
+__device__ inline uint64_t pack_stats(float m, float s) {
+  const uint32_t mb = (m != m) ? 0x7fc00000u : __float_as_uint(m);
+  return (uint64_t)mb | ((uint64_t)__float_as_uint(s) << 32);
+}
+__device__ inline float2 unpack_stats(uint64_t v) {
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
+
+// (value, index): the index is stored + 1 so that a written slot is never 0.
+__device__ inline uint64_t pack_arg(float v, int idx) {
+  return (uint64_t)__float_as_uint(v) | ((uint64_t)(uint32_t)(idx + 1) << 32);
+}
+__device__ inline void unpack_arg(uint64_t s, float& v, int& idx) {
+  v = __uint_as_float((uint32_t)s);
+  idx = (int)(uint32_t)(s >> 32) - 1;
+}
+
+// One wavefront waits until the n slots at `slots` are all written.  Returns false when the
+// bounded spin runs out (the caller flags the error and carries on, so every wave exits).
+__device__ inline bool wave_wait_slots(const uint64_t* slots, int n, int spin_limit) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int spins = 0;; ++spins) {
+    int ready = 1;
+    for (int c = lane; c < n; c += kWave) ready &= slot_load(slots + c) != 0;
+    if (__all(ready)) return true;
+    if (spins >= spin_limit) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
 }
 
 }  // namespace mvsd

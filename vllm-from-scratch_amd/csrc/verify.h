@@ -7,6 +7,8 @@
 namespace mvsd {
 
 constexpr int kMaxSpecLen = 128;  // reference MAX_SPEC_LEN, rejection_sampler.py:83
+constexpr int kVThreads = 512;   // verify-kernel workgroup size (8 wavefronts)
+constexpr int kVWaves = kVThreads / 64;
 
 // Kernel parameters, passed by value.  Pointers are device pointers; strides are in
 // elements.  The workspace pointers are carved by the host from one caller buffer.
@@ -42,13 +44,11 @@ struct VerifyParams {
   bool draft_aligned;
   bool noise_aligned;
   // workspace
-  int* ctrl;      // [0] ticket, [1] spin-limit error flag
-  int* grp_off;   // [B + 1] exclusive scan of groups per request
-  int* grp_cnt;   // [P] published chunk stats per group
-  int* req_cnt;   // [B] finished tasks per request
-  float2* stats;  // [P * nc] (chunk max, chunk sumexp)
-  float* argv;    // [P * nc] chunk argmax value
-  int* argi;      // [P * nc] chunk argmax index
+  int* ctrl;             // [0] ticket, [1] sticky spin-limit flag, [2] exit counter
+  int* grp_off;          // [B + 1] exclusive scan of groups per request
+  int* req_cnt;          // [B] finished tasks per request (zero between calls)
+  uint64_t* stat_slots;  // [P * nc] packed (chunk max, chunk sumexp); 0 = empty
+  uint64_t* arg_slots;   // [P * nc] packed (chunk argmax value, index + 1); 0 = empty
 };
 
 struct VerifyPlan {
@@ -60,6 +60,7 @@ struct VerifyPlan {
 
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size);
 const void* verify_kernel_ptr(int target_dtype);
+hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream);
 hipError_t launch_verify(const VerifyParams& params, int target_dtype, int grid,
                          hipStream_t stream);
 

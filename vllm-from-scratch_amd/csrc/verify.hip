@@ -14,15 +14,24 @@
 //     Tasks are handed out by an atomic ticket in group-major order, so the NC chunk
 //     tasks of a group hold consecutive tickets.
 //   * Phase 1 loads the group's target slice into registers, reduces a per-chunk
-//     (max, sumexp) for each row and publishes it (release).  Random rows then wait until
-//     all NC chunk tasks of the group have published; those tasks were claimed earlier (or
-//     are being claimed by running workgroups), never wait themselves before publishing,
-//     and therefore finish: the wait cannot deadlock.  A spin bound still ends every wave.
-//   * Phase 2 combines the NC partials into the row's (M, S), streams the request's noise
-//     chunk once and each row's draft chunk once, and scores p_v = e_v * exp(m_c - M) / S
-//     straight from the registers, keeping a chunk-local argmax per row.
-//   * The last task to finish a request (acq_rel counter) reduces the chunk argmaxes and
-//     runs the sequential accept/reject chain, writing [B, max_spec_len + 1].
+//     (max, sumexp) for each row and publishes it into that row's stats slot.  Random rows
+//     then wait until all NC slots of their rows are written; the tasks writing them were
+//     claimed earlier (or are being claimed by running workgroups), never wait before
+//     publishing, and therefore finish: the wait cannot deadlock.  A spin bound still ends
+//     every wave.  The request's noise chunk is loaded before the wait and the first draft
+//     chunk right after it, so the wait overlaps with HBM traffic.
+//   * Phase 2 combines the NC partials into the row's (M, S) and scores
+//     p_v = e_v * exp(m_c - M) / S straight from the registers, keeping a chunk-local argmax
+//     that goes into the row's argmax slot.
+//   * The last task to finish a request reduces the argmax slots, decides every position in
+//     parallel, writes [B, max_spec_len + 1] and clears the request's slots and counter.
+//   * Slots are 64-bit values exchanged with relaxed agent-scope atomics; 0 means empty and
+//     no written slot is 0, so readers poll the data itself and no fence (no L2 write-back or
+//     invalidation) is needed.  Every call leaves the workspace zeroed for the next one.
+//
+// Full, 16-byte-aligned chunks take a fast path with unconditional vector loads (all of a
+// task's loads in flight together); the last chunk of a row and unaligned rows take a
+// bounds-checked path.
 #include <float.h>
 
 #include "mvsd_device.h"
@@ -62,18 +71,106 @@ __device__ inline float req_temperature(const VerifyParams& p, int r) {
   return t == 0.f ? 1.f : t;
 }
 
-__device__ inline float2 load_stats(const float2* s) {
-  return *s;
+// x / t, correctly rounded, given rt = 1 / t correctly rounded (Markstein's correction:
+// q0 = x * rt is within an ulp, the FMA residual x - q0 * t is exact, and q0 + residual * rt
+// rounds to the IEEE quotient).  Three VALU ops instead of the ten of the IEEE sequence.
+__device__ inline float div_by(float x, float t, float rt) {
+  const float q0 = x * rt;
+  return fmaf(fmaf(-q0, t, x), rt, q0);
+}
+
+// exp(d) for d <= 0 (or -inf): 2^(d log2 e) with the product split into a rounded head and
+// an FMA-recovered tail so large |d| keeps full accuracy; ~1.5 ulp.
+__device__ inline float exp_le0(float d) {
+  constexpr float kLog2e = 1.44269502925872802734375f;      // RN(log2 e)
+  constexpr float kLog2eLo = 1.925963033500011079e-08f;     // log2 e - kLog2e
+  constexpr float kLn2 = 0.693147180559945309f;
+  d = fmaxf(d, -200.f);  // exp(-200) underflows to 0; keeps the tail finite for -inf
+  const float t = d * kLog2e;
+  const float lo = fmaf(d, kLog2eLo, fmaf(d, kLog2e, -t));
+  const float e = __builtin_amdgcn_exp2f(t);
+  return fmaf(e, lo * kLn2, e);
+}
+
+// ------------------------------------------------------------------ loads ------------
+// EPT consecutive-by-lane elements of one row chunk into fp32 registers.  FAST: full,
+// aligned chunk, unconditional 16-byte loads.  Otherwise bounds-checked, `fill` beyond vend.
+template <int DT, int EPT, bool FAST>
+__device__ inline void load_chunk(const typename Elem<DT>::storage* __restrict__ base, int64_t v0,
+                                  int64_t vend, bool aligned, float fill, float (&out)[EPT]) {
+  using S = typename Elem<DT>::storage;
+  constexpr int VEC = Elem<DT>::kVec;
+  constexpr int NV = EPT / VEC;
+  const int tid = threadIdx.x;
+  if constexpr (FAST) {
+    u32x4 raw[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      raw[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(base + v0 + ((int64_t)i * kVThreads + tid) * VEC));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const S* s = reinterpret_cast<const S*>(&raw[i]);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) out[i * VEC + j] = Elem<DT>::cvt(s[j]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float tmp[VEC];
+      load_vec<DT>(base, v0 + ((int64_t)i * kVThreads + tid) * VEC, vend, aligned, fill, tmp);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) out[i * VEC + j] = tmp[j];
+    }
+  }
+}
+
+// fp32 chunk whose lane layout follows a DT row (VEC elements of DT per 16-byte group).
+template <int DT, int EPT, bool FAST>
+__device__ inline void load_chunk_f32(const float* __restrict__ base, int64_t v0, int64_t vend,
+                                      bool aligned, float fill, float (&out)[EPT]) {
+  constexpr int VEC = Elem<DT>::kVec;
+  constexpr int NV = EPT / VEC;
+  const int tid = threadIdx.x;
+  if constexpr (FAST) {
+    u32x4 raw[EPT / 4];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int h = 0; h < VEC / 4; ++h)
+        raw[i * (VEC / 4) + h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            base + v0 + ((int64_t)i * kVThreads + tid) * VEC + h * 4));
+#pragma unroll
+    for (int k = 0; k < EPT / 4; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[k * 4 + j] = __uint_as_float(raw[k][j]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int h = 0; h < VEC; h += 4) {
+        float tmp[4];
+        load_vec<MVSD_F32>(base, v0 + ((int64_t)i * kVThreads + tid) * VEC + h, vend, aligned,
+                           fill, tmp);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[i * VEC + h + j] = tmp[j];
+      }
+  }
+}
+
+template <int DT, int EPT>
+__device__ inline int elem_index(int64_t v0, int k) {
+  constexpr int VEC = Elem<DT>::kVec;
+  return (int)(v0 + ((int64_t)(k / VEC) * kVThreads + threadIdx.x) * VEC + (k % VEC));
 }
 
 // ------------------------------------------------------------------ init kernel ------
-// One 1024-thread block: zero the ticket / counters, fill the output with -1 (bonus in
-// column 0 for requests without drafts), and exclusive-scan the per-request group counts.
+// One 1024-thread block: fill the output with -1 (bonus in column 0 for requests without
+// drafts) and exclusive-scan the per-request group counts.  Everything else in the workspace
+// is already zero (every call clears what it used); the spin-limit flag ctrl[1] is sticky
+// so that a timed-out call stays detectable.
 __global__ __launch_bounds__(1024) void verify_init_kernel(VerifyParams p) {
   const int tid = threadIdx.x;
-  if (tid < 2) p.ctrl[tid] = 0;
-  for (int i = tid; i < p.P; i += 1024) p.grp_cnt[i] = 0;
-  for (int i = tid; i < p.B; i += 1024) p.req_cnt[i] = 0;
   const int width = p.max_spec_len + 1;
   const int64_t n_out = (int64_t)p.B * width;
   for (int64_t i = tid; i < n_out; i += 1024) {
@@ -114,61 +211,79 @@ __global__ __launch_bounds__(1024) void verify_init_kernel(VerifyParams p) {
 }
 
 // ------------------------------------------------------------------ finalisation -----
+struct FinalizeSmem {
+  int tok[kMaxSpecLen];
+  float M[kMaxSpecLen];
+  float S[kMaxSpecLen];
+  int out_tok[kMaxSpecLen];
+  int accepted[kMaxSpecLen];
+  int first_reject;
+};
+
 // Executed by the whole block that completed request r's last task.
 __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool full,
-                                 int* s_tok, float* s_M, float* s_S) {
+                                 FinalizeSmem& sm) {
   int begin, K;
   req_range(p, r, begin, K);
   const int lane = lane_id();
   const int nc = p.nc;
-  for (int k = wave_id(); k < K; k += kWaves) {
+  for (int k = wave_id(); k < K; k += kVWaves) {
     const int64_t row = begin + k;
+    uint64_t* aslots = p.arg_slots + row * nc;
+    uint64_t* sslots = p.stat_slots + row * nc;
     if (greedy || full) {
+      if (!wave_wait_slots(aslots, nc, kSpinLimit) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
       float bv = -INFINITY;
       int bi = INT_MAX;
       for (int c = lane; c < nc; c += kWave) {
-        argmax_update(bv, bi, p.argv[row * nc + c], p.argi[row * nc + c], true);
+        float v;
+        int i;
+        unpack_arg(slot_load(aslots + c), v, i);
+        argmax_update(bv, bi, v, i, true);
       }
       wave_argmax(bv, bi);
-      if (lane == 0) s_tok[k] = full ? min(bi, p.V - 1) : bi;
+      if (lane == 0) sm.tok[k] = min(max(bi, 0), p.V - 1);
+      for (int c = lane; c < nc; c += kWave) slot_store(aslots + c, 0);
     } else if (lane == 0) {
-      s_tok[k] = p.recovered[row];
+      sm.tok[k] = p.recovered[row];
     }
     if (!greedy) {
+      if (!full && !wave_wait_slots(sslots, nc, kSpinLimit) && lane == 0)
+        atomic_store_relaxed(&p.ctrl[1], 1);
       float m = -INFINITY;
-      for (int c = lane; c < nc; c += kWave) m = fmaxf(m, load_stats(&p.stats[row * nc + c]).x);
+      for (int c = lane; c < nc; c += kWave) m = fmaxf(m, unpack_stats(slot_load(sslots + c)).x);
       m = wave_max(m);
       float s = 0.f;
       for (int c = lane; c < nc; c += kWave) {
-        const float2 st = load_stats(&p.stats[row * nc + c]);
+        const float2 st = unpack_stats(slot_load(sslots + c));
         if (st.x != -INFINITY) s += st.y * expf(st.x - m);
       }
       s = wave_sum(s);
       if (lane == 0) {
-        s_M[k] = m;
-        s_S[k] = s;
+        sm.M[k] = m;
+        sm.S[k] = s;
       }
+      for (int c = lane; c < nc; c += kWave) slot_store(sslots + c, 0);
     }
   }
+  if (threadIdx.x == 0) atomic_store_relaxed(&p.req_cnt[r], 0);
   __syncthreads();
-  if (threadIdx.x != 0) return;
 
-  int32_t* out = p.out + (int64_t)r * p.out_stride;
+  // every position's decision in parallel; the chain keeps the prefix up to the first reject
+  const int tid = threadIdx.x;
   const bool synthetic = p.synth != nullptr;
-  const float temp = req_temperature(p, r);
-  bool rejected = false;
-  for (int pos = 0; pos < K; ++pos) {
+  for (int pos = tid; pos < K; pos += kVThreads) {
     const int64_t row = begin + pos;
     const int d = p.draft_ids[row];
-    int token;
     bool accepted;
+    int token;
     if (greedy) {
       // rejection_sampler.py:715-732
       if (synthetic) {
         accepted = p.uniforms[row] < (double)p.synth[pos] && d >= 0;
-        token = accepted ? d : s_tok[pos];
+        token = accepted ? d : sm.tok[pos];
       } else {
-        token = s_tok[pos];
+        token = sm.tok[pos];
         accepted = d == token;
       }
     } else {
@@ -191,37 +306,243 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
         } else {
           x = Elem<MVSD_F16>::cvt(static_cast<const _Float16*>(p.target)[trow * p.target_stride + d]);
         }
+        const float temp = req_temperature(p, r);
         if (temp != 1.f) x = x / temp;
-        const float pd = expf(x - s_M[pos]) / s_S[pos];
+        const float pd = expf(x - sm.M[pos]) / sm.S[pos];
         accepted = q > 0.f && (double)(pd / q) >= u;
       }
-      token = accepted ? d : s_tok[pos];
+      token = accepted ? d : sm.tok[pos];
     }
-    out[pos] = token;
-    if (!accepted) {
-      rejected = true;
-      break;
+    sm.accepted[pos] = accepted;
+    sm.out_tok[pos] = token;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int first = K;
+    for (int pos = 0; pos < K; ++pos) {
+      if (!sm.accepted[pos]) {
+        first = pos;
+        break;
+      }
+    }
+    sm.first_reject = first;
+  }
+  __syncthreads();
+  const int first = sm.first_reject;
+  int32_t* out = p.out + (int64_t)r * p.out_stride;
+  for (int pos = tid; pos <= K; pos += kVThreads) {
+    if (pos < K && pos <= first) out[pos] = sm.out_tok[pos];
+    else if (pos == K && first == K) out[K] = p.bonus[r];
+  }
+}
+
+// ------------------------------------------------------------------ one task ---------
+template <int DT, int EPT, int G, bool FAST>
+__device__ inline void run_task(const VerifyParams& p, int gi, int c, int r, int row0, int nrows,
+                                int ngr, bool greedy, bool full, int64_t v0, int64_t vend,
+                                float* s_red, int* s_redi, float* s_f, int& s_last,
+                                FinalizeSmem& fsm) {
+  using S = typename Elem<DT>::storage;
+  const int tid = threadIdx.x;
+  const int nc = p.nc;
+
+  // ---- the group's target slice into registers (-inf beyond V) ----
+  float x[G][EPT];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (g < nrows) {
+      const S* base = static_cast<const S*>(p.target) + target_row(p, row0 + g) * p.target_stride;
+      load_chunk<DT, EPT, FAST>(base, v0, vend, p.target_aligned, -INFINITY, x[g]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) x[g][k] = -INFINITY;
     }
   }
-  if (!rejected) out[K] = p.bonus[r];
+
+  if (greedy) {
+    // ---- chunk-local argmax of the raw logits (NaN ranks first, lowest index wins) ----
+    float bv[G];
+    int bi[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      bv[g] = -INFINITY;
+      bi[g] = INT_MAX;
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) {
+        const int idx = elem_index<DT, EPT>(v0, k);
+        argmax_update(bv[g], bi[g], x[g][k], idx, FAST || idx < vend);
+      }
+    }
+    block_argmax<G, kVWaves>(bv, bi, s_red, s_redi);
+    if (tid < nrows) {
+      float v = bv[0];
+      int i = bi[0];
+#pragma unroll
+      for (int g = 1; g < G; ++g) {
+        v = tid == g ? bv[g] : v;
+        i = tid == g ? bi[g] : i;
+      }
+      slot_store(p.arg_slots + (int64_t)(row0 + tid) * nc + c, pack_arg(v, i));
+    }
+  } else {
+    // ---- phase 1: temperature, chunk max, exp, chunk sum ----
+    const float temp = req_temperature(p, r);
+    if (temp != 1.f) {
+      const float rt = 1.0f / temp;
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) x[g][k] = div_by(x[g][k], temp, rt);
+    }
+    float m[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mm = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) mm = fmaxf(mm, x[g][k]);
+      m[g] = mm;
+    }
+    block_max<G, kVWaves>(m, s_red);
+    float s[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float ss = 0.f;
+      const float mg = m[g] == -INFINITY ? 0.f : m[g];
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) {
+        const float e = exp_le0(x[g][k] - mg);
+        x[g][k] = e;
+        ss += e;
+      }
+      s[g] = ss;
+    }
+    block_sum<G, kVWaves>(s, s_red);
+    if (tid < nrows) {
+      float mv = m[0], sv = s[0];
+#pragma unroll
+      for (int g = 1; g < G; ++g) {
+        mv = tid == g ? m[g] : mv;
+        sv = tid == g ? s[g] : sv;
+      }
+      slot_store(p.stat_slots + (int64_t)(row0 + tid) * nc + c, pack_stats(mv, sv));
+    }
+
+    if (full) {
+      // ---- the request's noise chunk, in flight during the wait ----
+      float inv[EPT];
+      load_chunk_f32<DT, EPT, FAST>(p.noise + (int64_t)r * p.noise_stride, v0, vend,
+                                    p.noise_aligned, 1.f, inv);
+      // ---- wait until every chunk of the group's rows has published its stats ----
+      if (wave_id() < nrows &&
+          !wave_wait_slots(p.stat_slots + (int64_t)(row0 + wave_id()) * nc, nc, kSpinLimit) &&
+          lane_id() == 0)
+        atomic_store_relaxed(&p.ctrl[1], 1);
+      __syncthreads();
+      // ---- first row's draft chunk in flight while the partial stats are combined ----
+      float q[EPT];
+      if (p.draft) {
+        load_chunk_f32<DT, EPT, FAST>(p.draft + (int64_t)row0 * p.draft_stride, v0, vend,
+                                      p.draft_aligned, 0.f, q);
+      }
+      const int lane = lane_id();
+      for (int g = wave_id(); g < nrows; g += kVWaves) {
+        const int64_t row = row0 + g;
+        const uint64_t* sslots = p.stat_slots + row * nc;
+        float mm = -INFINITY;
+        for (int cc = lane; cc < nc; cc += kWave) mm = fmaxf(mm, unpack_stats(slot_load(sslots + cc)).x);
+        mm = wave_max(mm);
+        float ss = 0.f;
+        for (int cc = lane; cc < nc; cc += kWave) {
+          const float2 st = unpack_stats(slot_load(sslots + cc));
+          if (st.x != -INFINITY) ss += st.y * expf(st.x - mm);
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) {
+          float mine = -INFINITY;
+#pragma unroll
+          for (int gg = 0; gg < G; ++gg) mine = gg == g ? m[gg] : mine;
+          s_f[g] = (mine == -INFINITY) ? 0.f : expf(mine - mm) / ss;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) inv[k] = 1.0f / inv[k];
+      __syncthreads();
+
+      // ---- phase 2: score p - q against the noise, chunk-local argmax per row ----
+      float bv[G];
+      int bi[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        bv[g] = -INFINITY;
+        bi[g] = INT_MAX;
+        if (g < nrows) {
+          if (g > 0 && p.draft) {
+            load_chunk_f32<DT, EPT, FAST>(p.draft + (int64_t)(row0 + g) * p.draft_stride, v0,
+                                          vend, p.draft_aligned, 0.f, q);
+          }
+          const float f = s_f[g];
+          const int d = p.draft ? -1 : p.draft_ids[row0 + g];
+#pragma unroll
+          for (int k = 0; k < EPT; ++k) {
+            const int idx = elem_index<DT, EPT>(v0, k);
+            const float prob = x[g][k] * f;
+            const float w = p.draft ? fmaxf(prob - q[k], 0.f) : (idx == d ? 0.f : prob);
+            const float score = w * inv[k];
+            // indices rise along k, so a strict compare keeps the first maximum
+            const bool take = (score > bv[g]) & (FAST || idx < vend);
+            bv[g] = take ? score : bv[g];
+            bi[g] = take ? idx : bi[g];
+          }
+        }
+      }
+      block_argmax<G, kVWaves>(bv, bi, s_red, s_redi);
+      if (tid < nrows) {
+        float v = bv[0];
+        int i = bi[0];
+#pragma unroll
+        for (int g = 1; g < G; ++g) {
+          v = tid == g ? bv[g] : v;
+          i = tid == g ? bi[g] : i;
+        }
+        slot_store(p.arg_slots + (int64_t)(row0 + tid) * nc + c,
+                   pack_arg(v, i == INT_MAX ? (int)v0 : i));
+      }
+    }
+  }
+
+  // ---- request completion: the last task runs the accept/reject chain ----
+  if (tid == 0) {
+    const int old = atomic_add_relaxed(&p.req_cnt[r], 1);
+    s_last = old == ngr * nc - 1;
+  }
+  __syncthreads();
+  if (s_last) finalize_request(p, r, greedy, full, fsm);
 }
 
 // ------------------------------------------------------------------ main kernel ------
-template <int DT, int EPT, int G>
-__global__ __launch_bounds__(kThreads) void verify_kernel(VerifyParams p) {
-  using S = typename Elem<DT>::storage;
-  constexpr int VEC = Elem<DT>::kVec;
-  constexpr int NV = EPT / VEC;
-  static_assert(EPT % VEC == 0, "EPT must be a multiple of the vector width");
+// Tunables (compile-time): elements per thread per row, and an optional cap on waves per SIMD
+// that bounds the register budget (0 = let the compiler choose).
+#ifndef MVSD_VERIFY_EPT
+#define MVSD_VERIFY_EPT 8
+#endif
+#ifndef MVSD_VERIFY_WAVES_PER_EU
+#define MVSD_VERIFY_WAVES_PER_EU 0
+#endif
+#if MVSD_VERIFY_WAVES_PER_EU > 0
+#define MVSD_VERIFY_ATTRS __attribute__((amdgpu_waves_per_eu(MVSD_VERIFY_WAVES_PER_EU, 8)))
+#else
+#define MVSD_VERIFY_ATTRS
+#endif
 
-  __shared__ float s_red[G * kWaves];
-  __shared__ int s_redi[G * kWaves];
+template <int DT, int EPT, int G>
+__global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(VerifyParams p) {
+  static_assert(EPT % Elem<DT>::kVec == 0, "EPT must be a multiple of the vector width");
+  __shared__ float s_red[G * kVWaves];
+  __shared__ int s_redi[G * kVWaves];
   __shared__ float s_f[G];
   __shared__ int s_task;
   __shared__ int s_last;
-  __shared__ int s_tok[kMaxSpecLen];
-  __shared__ float s_M[kMaxSpecLen];
-  __shared__ float s_S[kMaxSpecLen];
+  __shared__ FinalizeSmem fsm;
 
   const int tid = threadIdx.x;
   const int nc = p.nc;
@@ -252,215 +573,66 @@ __global__ __launch_bounds__(kThreads) void verify_kernel(VerifyParams p) {
     const bool full = !greedy && p.recovered == nullptr;
     const int64_t v0 = (int64_t)c * p.chunk;
     const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
-
-    // ---- load the group's target slice (fp32 in registers; -inf beyond V) ----
-    float x[G][EPT];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if (g < nrows) {
-        const int64_t trow = target_row(p, row0 + g);
-        const S* base = static_cast<const S*>(p.target) + trow * p.target_stride;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          float tmp[VEC];
-          load_vec<DT>(base, v0 + ((int64_t)i * kThreads + tid) * VEC, vend, p.target_aligned,
-                       -INFINITY, tmp);
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) x[g][i * VEC + j] = tmp[j];
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < EPT; ++k) x[g][k] = -INFINITY;
-      }
-    }
-
-    if (greedy) {
-      // ---- chunk-local argmax of the raw logits ----
-      float bv[G];
-      int bi[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        bv[g] = -INFINITY;
-        bi[g] = INT_MAX;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) {
-            const int idx = (int)(v0 + ((int64_t)i * kThreads + tid) * VEC + j);
-            argmax_update(bv[g], bi[g], x[g][i * VEC + j], idx, idx < vend);
-          }
-        }
-      }
-      block_argmax<G>(bv, bi, s_red, s_redi);
-      if (tid == 0) {
-        for (int g = 0; g < nrows; ++g) {
-          p.argv[(int64_t)(row0 + g) * nc + c] = bv[g];
-          p.argi[(int64_t)(row0 + g) * nc + c] = bi[g];
-        }
-      }
+    const bool fast = p.target_aligned && vend - v0 == p.chunk &&
+                      (!full || (p.noise_aligned && (p.draft_aligned || !p.draft)));
+    if (fast) {
+      run_task<DT, EPT, G, true>(p, gi, c, r, row0, nrows, ngr, greedy, full, v0, vend, s_red,
+                                 s_redi, s_f, s_last, fsm);
     } else {
-      // ---- phase 1: temperature, chunk max, exp, chunk sum ----
-      const float temp = req_temperature(p, r);
-      if (temp != 1.f) {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int k = 0; k < EPT; ++k) x[g][k] = x[g][k] / temp;
-      }
-      float m[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float mm = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < EPT; ++k) mm = fmaxf(mm, x[g][k]);
-        m[g] = mm;
-      }
-      block_max<G>(m, s_red);
-      float s[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float ss = 0.f;
-        const bool dead = m[g] == -INFINITY;
-#pragma unroll
-        for (int k = 0; k < EPT; ++k) {
-          const float e = dead ? 0.f : expf(x[g][k] - m[g]);
-          x[g][k] = e;
-          ss += e;
-        }
-        s[g] = ss;
-      }
-      block_sum<G>(s, s_red);
-      if (tid == 0) {
-        for (int g = 0; g < nrows; ++g) p.stats[(int64_t)(row0 + g) * nc + c] = make_float2(m[g], s[g]);
-      }
-
-      if (full) {
-        // ---- publish, then wait for the group's other chunk tasks ----
-        if (tid == 0) {
-          atomic_add_release(&p.grp_cnt[gi], 1);
-          int spins = 0;
-          while (atomic_load_acquire(&p.grp_cnt[gi]) < nc) {
-            __builtin_amdgcn_s_sleep(2);
-            if (++spins > kSpinLimit) {
-              atomic_store_relaxed(&p.ctrl[1], 1);
-              break;
-            }
-          }
-        }
-        __syncthreads();
-        // ---- combine partials: row (M, S) and this chunk's scale exp(m_c - M) / S ----
-        const int lane = lane_id();
-        for (int g = wave_id(); g < nrows; g += kWaves) {
-          const int64_t row = row0 + g;
-          float mm = -INFINITY;
-          for (int cc = lane; cc < nc; cc += kWave) mm = fmaxf(mm, load_stats(&p.stats[row * nc + cc]).x);
-          mm = wave_max(mm);
-          float ss = 0.f;
-          for (int cc = lane; cc < nc; cc += kWave) {
-            const float2 st = load_stats(&p.stats[row * nc + cc]);
-            if (st.x != -INFINITY) ss += st.y * expf(st.x - mm);
-          }
-          ss = wave_sum(ss);
-          if (lane == 0) {
-            float mine = -INFINITY;
-#pragma unroll
-            for (int gg = 0; gg < G; ++gg) if (gg == g) mine = m[gg];
-            s_f[g] = (mine == -INFINITY) ? 0.f : expf(mine - mm) / ss;
-          }
-        }
-        __syncthreads();
-
-        // ---- phase 2: noise chunk once, then each row's draft chunk ----
-        float inv[EPT];
-        {
-          const float* nbase = p.noise + (int64_t)r * p.noise_stride;
-#pragma unroll
-          for (int i = 0; i < NV; ++i) {
-#pragma unroll
-            for (int h = 0; h < VEC; h += 4) {
-              float tmp[4];
-              load_vec<MVSD_F32>(nbase, v0 + ((int64_t)i * kThreads + tid) * VEC + h, vend,
-                                 p.noise_aligned, 1.f, tmp);
-#pragma unroll
-              for (int j = 0; j < 4; ++j) inv[i * VEC + h + j] = 1.0f / tmp[j];
-            }
-          }
-        }
-        float bv[G];
-        int bi[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          bv[g] = -INFINITY;
-          bi[g] = INT_MAX;
-          if (g < nrows) {
-            const int row = row0 + g;
-            const float f = s_f[g];
-            const int d = p.draft_ids[row];
-            const float* dbase = p.draft ? p.draft + (int64_t)row * p.draft_stride : nullptr;
-#pragma unroll
-            for (int i = 0; i < NV; ++i) {
-#pragma unroll
-              for (int h = 0; h < VEC; h += 4) {
-                const int64_t idx0 = v0 + ((int64_t)i * kThreads + tid) * VEC + h;
-                float q[4] = {0.f, 0.f, 0.f, 0.f};
-                if (dbase) load_vec<MVSD_F32>(dbase, idx0, vend, p.draft_aligned, 0.f, q);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                  const int idx = (int)(idx0 + j);
-                  const float prob = x[g][i * VEC + h + j] * f;
-                  const float w = dbase ? fmaxf(prob - q[j], 0.f) : (idx == d ? 0.f : prob);
-                  const float score = w * inv[i * VEC + h + j];
-                  argmax_update(bv[g], bi[g], score, idx, idx < vend);
-                }
-              }
-            }
-          }
-        }
-        block_argmax<G>(bv, bi, s_red, s_redi);
-        if (tid == 0) {
-          for (int g = 0; g < nrows; ++g) {
-            p.argv[(int64_t)(row0 + g) * nc + c] = bv[g];
-            p.argi[(int64_t)(row0 + g) * nc + c] = bi[g];
-          }
-        }
-      }
-    }
-
-    // ---- request completion: the last task runs the accept/reject chain ----
-    if (tid == 0) {
-      const int old = atomic_add_acq_rel(&p.req_cnt[r], 1);
-      s_last = old == ngr * nc - 1;
-    }
-    __syncthreads();
-    if (s_last) {
-      finalize_request(p, r, greedy, full, s_tok, s_M, s_S);
+      run_task<DT, EPT, G, false>(p, gi, c, r, row0, nrows, ngr, greedy, full, v0, vend, s_red,
+                                  s_redi, s_f, s_last, fsm);
     }
     __syncthreads();
   }
+
+  // The last workgroup out (every other one has made its final claim and finished reading
+  // grp_off) returns the group offsets, ticket and exit counter to zero, so the whole
+  // workspace is zero again whatever layout the next call uses.
+  if (tid == 0) s_last = atomic_add_relaxed(&p.ctrl[2], 1) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (s_last) {
+    for (int i = tid; i <= p.B; i += kVThreads) p.grp_off[i] = 0;
+    if (tid == 0) {
+      atomic_store_relaxed(&p.ctrl[0], 0);
+      atomic_store_relaxed(&p.ctrl[2], 0);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ workspace init ---
+__global__ __launch_bounds__(256) void zero_fill_kernel(uint64_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    p[i] = 0;
+}
+
+hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream) {
+  const int64_t n = bytes / 8;
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256),
+                     0, stream, static_cast<uint64_t*>(p), n);
+  return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ dispatch ---------
+constexpr int kEpt = MVSD_VERIFY_EPT;
+constexpr int kGroup = 4;
 
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size) {
   VerifyPlan plan;
-  plan.ept = 16;
-  plan.g = 4;
-  plan.chunk = kThreads * plan.ept;
+  plan.ept = kEpt;
+  plan.g = kGroup;
+  plan.chunk = kVThreads * plan.ept;
   plan.nc = (int)((vocab_size + plan.chunk - 1) / plan.chunk);
   (void)target_dtype;
   return plan;
 }
 
-template <int DT>
-static const void* kernel_for() {
-  return reinterpret_cast<const void*>(&verify_kernel<DT, 16, 4>);
-}
-
 const void* verify_kernel_ptr(int target_dtype) {
   switch (target_dtype) {
-    case MVSD_F32: return kernel_for<MVSD_F32>();
-    case MVSD_BF16: return kernel_for<MVSD_BF16>();
-    case MVSD_F16: return kernel_for<MVSD_F16>();
+    case MVSD_F32: return reinterpret_cast<const void*>(&verify_kernel<MVSD_F32, kEpt, kGroup>);
+    case MVSD_BF16: return reinterpret_cast<const void*>(&verify_kernel<MVSD_BF16, kEpt, kGroup>);
+    case MVSD_F16: return reinterpret_cast<const void*>(&verify_kernel<MVSD_F16, kEpt, kGroup>);
     default: return nullptr;
   }
 }
@@ -472,13 +644,16 @@ hipError_t launch_verify(const VerifyParams& params, int target_dtype, int grid,
   if (err != hipSuccess || params.P == 0) return err;
   switch (target_dtype) {
     case MVSD_F32:
-      hipLaunchKernelGGL((verify_kernel<MVSD_F32, 16, 4>), dim3(grid), dim3(kThreads), 0, stream, params);
+      hipLaunchKernelGGL((verify_kernel<MVSD_F32, kEpt, kGroup>), dim3(grid), dim3(kVThreads), 0,
+                         stream, params);
       break;
     case MVSD_BF16:
-      hipLaunchKernelGGL((verify_kernel<MVSD_BF16, 16, 4>), dim3(grid), dim3(kThreads), 0, stream, params);
+      hipLaunchKernelGGL((verify_kernel<MVSD_BF16, kEpt, kGroup>), dim3(grid), dim3(kVThreads), 0,
+                         stream, params);
       break;
     case MVSD_F16:
-      hipLaunchKernelGGL((verify_kernel<MVSD_F16, 16, 4>), dim3(grid), dim3(kThreads), 0, stream, params);
+      hipLaunchKernelGGL((verify_kernel<MVSD_F16, kEpt, kGroup>), dim3(grid), dim3(kVThreads), 0,
+                         stream, params);
       break;
     default:
       return hipErrorInvalidValue;

@@ -76,6 +76,7 @@ SIGNATURES = {
     "mvsd_expand_batch_to_tokens": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int64,
                                             c_double, c_double, c_void_p]),
     "mvsd_rejection_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int, c_int64]),
+    "mvsd_rejection_workspace_init": (c_int, [c_void_p, c_int64, c_void_p]),
     "mvsd_rejection_sample": (c_int, [ctypes.POINTER(RejectionArgs), c_void_p]),
     "mvsd_softmax_rows": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int64, c_void_p, c_int64,
                                   c_int64, c_void_p]),

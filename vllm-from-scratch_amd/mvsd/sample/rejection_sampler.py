@@ -270,7 +270,7 @@ def rejection_sample(
     handle = nat.lib()
     ws_bytes = handle.mvsd_rejection_workspace_bytes(batch_size, num_tokens, vocab_size, dtype,
                                                      max_spec_len)
-    workspace = torch.empty(max(int(ws_bytes), 256), dtype=torch.uint8, device=device)
+    workspace = _workspace(device, int(ws_bytes))
     args = nat.RejectionArgs(
         output_token_ids=output_token_ids.data_ptr(),
         out_stride=output_token_ids.stride(0),
@@ -433,6 +433,33 @@ _SAMPLE_RECOVERED_TOKENS = sample_recovered_tokens
 
 
 # --------------------------------------------------------------------------- helpers
+
+# One zero-initialised verification workspace per (device, stream).  The kernel leaves it
+# zeroed after every call (include/mvsd.h), so it is reused without clearing; it only grows.
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    stream = nat.stream_of(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 1 << 16)
+        if ws is not None:
+            size = max(size, 2 * ws.numel())
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
+        nat.check(nat.lib().mvsd_rejection_workspace_init(ws.data_ptr(), ws.numel(), stream),
+                  "mvsd_rejection_workspace_init")
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def workspace_error_flag(device: torch.device) -> int:
+    """The sticky spin-limit flag of this stream's workspace (synchronises; diagnostics)."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           nat.stream_of(device))
+    ws = _WORKSPACES.get(key)
+    return 0 if ws is None else int(ws[4:8].view(torch.int32).item())
 
 
 def _as(t: torch.Tensor, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
