@@ -3,6 +3,7 @@
 // Every function validates its arguments on the host, enqueues on the caller's stream and
 // returns a status code; nothing here synchronises the host or allocates device memory.
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -63,7 +64,7 @@ int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 // Workspace layout.  ctrl = {ticket, sticky spin-limit flag (byte offset 4), exit counter}.
 struct WorkspaceLayout {
-  int64_t ctrl, grp_off, req_cnt, stat_slots, arg_slots, total;
+  int64_t ctrl, grp_off, grp_req, req_cnt, stat_slots, arg_slots, total;
 };
 
 WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
@@ -73,6 +74,8 @@ WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
   off = align_up(off + 3 * 4, 256);
   l.grp_off = off;
   off = align_up(off + (B + 1) * 4, 256);
+  l.grp_req = off;
+  off = align_up(off + (P > 0 ? P : 1) * 4, 256);
   l.req_cnt = off;
   off = align_up(off + (B > 0 ? B : 1) * 4, 256);
   l.stat_slots = off;
@@ -193,6 +196,7 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   p.noise_aligned = a->exp_noise ? aligned16(a->exp_noise, a->noise_stride * 4) : false;
   p.ctrl = reinterpret_cast<int*>(ws + lay.ctrl);
   p.grp_off = reinterpret_cast<int*>(ws + lay.grp_off);
+  p.grp_req = reinterpret_cast<int*>(ws + lay.grp_req);
   p.req_cnt = reinterpret_cast<int*>(ws + lay.req_cnt);
   p.stat_slots = reinterpret_cast<uint64_t*>(ws + lay.stat_slots);
   p.arg_slots = reinterpret_cast<uint64_t*>(ws + lay.arg_slots);
@@ -207,9 +211,16 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
     // Upper bound on tasks: groups <= min(P, B * ceil(max_spec_len / G)).
     int64_t groups = B * ((a->max_spec_len + plan.g - 1) / plan.g);
     if (groups > P) groups = P;
-    int64_t tasks = groups * plan.nc;
+    // B-chunks of a group are claimed `lag` groups after its A-chunks, far enough that the
+    // resident workgroups have finished the A-chunks (no waiting in the common case) and
+    // close enough that the re-read target slice is still in the Infinity Cache.
+    p.two_phase = (!a->all_greedy && !a->recovered_token_ids) ? 1 : 0;
+    int lag = cap / (2 * plan.nc) + 4;
+    if (const char* env = getenv("MVSD_VERIFY_LAG")) lag = atoi(env);
+    p.lag = lag < 1 ? 1 : (lag > 256 ? 256 : lag);
+    const int64_t step = p.two_phase ? 2 * plan.nc : plan.nc;
+    const int64_t tasks = (groups + (p.two_phase ? p.lag : 0)) * step;
     grid = (int)(tasks < cap ? tasks : cap);
-    if (grid < plan.nc) grid = plan.nc;
   }
   return hip_status(mvsd::launch_verify(p, a->target_dtype, grid, (hipStream_t)stream));
 }

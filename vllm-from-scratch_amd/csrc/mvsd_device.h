@@ -182,6 +182,74 @@ __device__ inline void block_argmax(float (&v)[N], int (&i)[N], float* sv, int* 
   __syncthreads();
 }
 
+// ------------------------------------------------------------------ argmax keys ------
+// An (value, index) pair as one 64-bit key whose unsigned maximum is the argmax under the
+// rule above: the high word orders floats (NaN mapped above +inf), the low word is
+// 0xffffffff - index so that equal values prefer the lower index.  Key 0 is below every
+// real pair (the smallest float, -inf, maps to 0x007fffff).
+
+__device__ inline uint32_t ordered_bits(float x) {
+  const uint32_t b = __float_as_uint(x);
+  const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (x != x) ? 0xffffffffu : o;
+}
+
+__device__ inline uint64_t argmax_key(float v, int idx) {
+  return ((uint64_t)ordered_bits(v) << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+}
+
+__device__ inline int key_index(uint64_t key) { return (int)(0xffffffffu - (uint32_t)key); }
+
+__device__ inline uint64_t wave_max_u64(uint64_t k) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), o, kWave) << 32) |
+                           (uint32_t)__shfl_xor((int)(uint32_t)k, o, kWave);
+    k = other > k ? other : k;
+  }
+  return k;
+}
+
+// Per-row maximum of N keys over a block of NW wavefronts; only thread g (< N) receives row
+// g's result (returned; other threads get 0).  `scratch` holds N * NW keys.  One barrier.
+template <int N, int NW>
+__device__ inline uint64_t block_max_key_to_row_thread(const uint64_t (&k)[N], uint64_t* scratch) {
+#pragma unroll
+  for (int g = 0; g < N; ++g) {
+    const uint64_t w = wave_max_u64(k[g]);
+    if (lane_id() == 0) scratch[g * NW + wave_id()] = w;
+  }
+  __syncthreads();
+  uint64_t best = 0;
+  const int t = threadIdx.x;
+  if (t < N) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint64_t v = scratch[t * NW + w];
+      best = v > best ? v : best;
+    }
+  }
+  return best;
+}
+
+// Per-row sums of N values; only thread g (< N) receives row g's sum.  One barrier.
+template <int N, int NW>
+__device__ inline float block_sum_to_row_thread(const float (&v)[N], float* scratch) {
+#pragma unroll
+  for (int g = 0; g < N; ++g) {
+    const float w = wave_sum(v[g]);
+    if (lane_id() == 0) scratch[g * NW + wave_id()] = w;
+  }
+  __syncthreads();
+  float s = 0.f;
+  const int t = threadIdx.x;
+  if (t < N) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) s += scratch[t * NW + w];
+  }
+  return s;
+}
+
 // ------------------------------------------------------------------ atomics ----------
 // Agent-scope acquire/release on plain device memory; see the AMDGPU memory model for
 // gfx942/gfx950 (release writes back L2, acquire invalidates stale L1/L2 lines), which

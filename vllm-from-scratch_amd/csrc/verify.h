@@ -40,12 +40,15 @@ struct VerifyParams {
   int chunk;  // vocab columns per task
   int nc;     // chunks per row
   int G;      // rows per group
+  int lag;        // groups between a group's A-chunks and its B-chunks in ticket order
+  int two_phase;  // the batch has random requests that need B-chunks
   bool target_aligned;
   bool draft_aligned;
   bool noise_aligned;
   // workspace
   int* ctrl;             // [0] ticket, [1] sticky spin-limit flag, [2] exit counter
   int* grp_off;          // [B + 1] exclusive scan of groups per request
+  int* grp_req;          // [P] request of each group
   int* req_cnt;          // [B] finished tasks per request (zero between calls)
   uint64_t* stat_slots;  // [P * nc] packed (chunk max, chunk sumexp); 0 = empty
   uint64_t* arg_slots;   // [P * nc] packed (chunk argmax value, index + 1); 0 = empty

@@ -202,12 +202,70 @@ __global__ __launch_bounds__(1024) void verify_init_kernel(VerifyParams p) {
       __syncthreads();
     }
     const int carry = s_carry;
-    if (r < p.B) p.grp_off[r] = carry + s_scan[tid] - ng;
+    if (r < p.B) {
+      const int first = carry + s_scan[tid] - ng;
+      p.grp_off[r] = first;
+      for (int g = 0; g < ng; ++g) p.grp_req[first + g] = r;
+    }
     __syncthreads();
     if (tid == 1023) s_carry = carry + s_scan[1023];
     __syncthreads();
   }
   if (tid == 0) p.grp_off[p.B] = s_carry;
+}
+
+// ------------------------------------------------------------------ row statistics ---
+// Softmax statistics travel as (raw chunk max mx, sum of exp2((x - mx) * c1)) with
+// c1 = log2(e) / T: for T > 0 the max of x / T is the max of x divided by T, so no per-element
+// division is needed, and p = exp((x - MX) / T) / S = exp2(fma(x - MX, c1, -log2 S)).
+
+// log2(e) / T rounded once from double.
+__device__ inline float exp2_scale(float temp) {
+  return (float)(1.4426950408889634074 / (double)temp);
+}
+
+// One wavefront: wait until the n stats slots of a row are written, then combine them into
+// the row's raw max MX and S = sum_c s_c * 2^((mx_c - MX) * c1).  Up to 4 * 64 slots are kept
+// in registers from the last poll.
+__device__ inline bool wave_row_stats(const uint64_t* slots, int n, float c1, float& MX, float& S) {
+  const int lane = lane_id();
+  constexpr int R = 4;
+  uint64_t v[R];
+  bool ok = true;
+  for (int spins = 0;; ++spins) {
+    int ready = 1;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int c = lane + j * kWave;
+      v[j] = c < n ? slot_load(slots + c) : 0;
+      ready &= (c >= n) | (v[j] != 0);
+    }
+    for (int c = lane + R * kWave; c < n; c += kWave) ready &= slot_load(slots + c) != 0;
+    if (__all(ready)) break;
+    if (spins >= kSpinLimit) {
+      ok = false;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (lane + j * kWave < n) m = fmaxf(m, unpack_stats(v[j]).x);
+  for (int c = lane + R * kWave; c < n; c += kWave) m = fmaxf(m, unpack_stats(slot_load(slots + c)).x);
+  MX = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const float2 st = unpack_stats(v[j]);
+    if (lane + j * kWave < n && st.x != -INFINITY) s += st.y * exp2f((st.x - MX) * c1);
+  }
+  for (int c = lane + R * kWave; c < n; c += kWave) {
+    const float2 st = unpack_stats(slot_load(slots + c));
+    if (st.x != -INFINITY) s += st.y * exp2f((st.x - MX) * c1);
+  }
+  S = wave_sum(s);
+  return ok;
 }
 
 // ------------------------------------------------------------------ finalisation -----
@@ -233,35 +291,24 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
     uint64_t* sslots = p.stat_slots + row * nc;
     if (greedy || full) {
       if (!wave_wait_slots(aslots, nc, kSpinLimit) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
-      float bv = -INFINITY;
-      int bi = INT_MAX;
+      uint64_t best = 0;
       for (int c = lane; c < nc; c += kWave) {
-        float v;
-        int i;
-        unpack_arg(slot_load(aslots + c), v, i);
-        argmax_update(bv, bi, v, i, true);
+        const uint64_t k = slot_load(aslots + c);
+        best = k > best ? k : best;
       }
-      wave_argmax(bv, bi);
-      if (lane == 0) sm.tok[k] = min(max(bi, 0), p.V - 1);
+      best = wave_max_u64(best);
+      if (lane == 0) sm.tok[k] = min(max(key_index(best), 0), p.V - 1);
       for (int c = lane; c < nc; c += kWave) slot_store(aslots + c, 0);
     } else if (lane == 0) {
       sm.tok[k] = p.recovered[row];
     }
     if (!greedy) {
-      if (!full && !wave_wait_slots(sslots, nc, kSpinLimit) && lane == 0)
-        atomic_store_relaxed(&p.ctrl[1], 1);
-      float m = -INFINITY;
-      for (int c = lane; c < nc; c += kWave) m = fmaxf(m, unpack_stats(slot_load(sslots + c)).x);
-      m = wave_max(m);
-      float s = 0.f;
-      for (int c = lane; c < nc; c += kWave) {
-        const float2 st = unpack_stats(slot_load(sslots + c));
-        if (st.x != -INFINITY) s += st.y * expf(st.x - m);
-      }
-      s = wave_sum(s);
+      const float c1 = exp2_scale(req_temperature(p, r));
+      float MX, S;
+      if (!wave_row_stats(sslots, nc, c1, MX, S) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
       if (lane == 0) {
-        sm.M[k] = m;
-        sm.S[k] = s;
+        sm.M[k] = MX;
+        sm.S[k] = S;
       }
       for (int c = lane; c < nc; c += kWave) slot_store(sslots + c, 0);
     }
@@ -307,8 +354,7 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
           x = Elem<MVSD_F16>::cvt(static_cast<const _Float16*>(p.target)[trow * p.target_stride + d]);
         }
         const float temp = req_temperature(p, r);
-        if (temp != 1.f) x = x / temp;
-        const float pd = expf(x - sm.M[pos]) / sm.S[pos];
+        const float pd = expf(x / temp - sm.M[pos] / temp) / sm.S[pos];
         accepted = q > 0.f && (double)(pd / q) >= u;
       }
       token = accepted ? d : sm.tok[pos];
@@ -336,18 +382,13 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
   }
 }
 
-// ------------------------------------------------------------------ one task ---------
-template <int DT, int EPT, int G, bool FAST>
-__device__ inline void run_task(const VerifyParams& p, int gi, int c, int r, int row0, int nrows,
-                                int ngr, bool greedy, bool full, int64_t v0, int64_t vend,
-                                float* s_red, int* s_redi, float* s_f, int& s_last,
-                                FinalizeSmem& fsm) {
-  using S = typename Elem<DT>::storage;
-  const int tid = threadIdx.x;
-  const int nc = p.nc;
+// ------------------------------------------------------------------ tasks ------------
 
-  // ---- the group's target slice into registers (-inf beyond V) ----
-  float x[G][EPT];
+// The group's target slice into registers (-inf beyond V and for rows >= nrows).
+template <int DT, int EPT, int G, bool FAST>
+__device__ inline void load_rows(const VerifyParams& p, int row0, int nrows, int64_t v0,
+                                 int64_t vend, float (&x)[G][EPT]) {
+  using S = typename Elem<DT>::storage;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     if (g < nrows) {
@@ -358,165 +399,138 @@ __device__ inline void run_task(const VerifyParams& p, int gi, int c, int r, int
       for (int k = 0; k < EPT; ++k) x[g][k] = -INFINITY;
     }
   }
+}
 
-  if (greedy) {
-    // ---- chunk-local argmax of the raw logits (NaN ranks first, lowest index wins) ----
-    float bv[G];
-    int bi[G];
+// Value of a per-row register array for row = this thread's index (threads < G).
+template <int G, typename T>
+__device__ inline T row_of_thread(const T (&a)[G]) {
+  T v = a[0];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      bv[g] = -INFINITY;
-      bi[g] = INT_MAX;
+  for (int g = 1; g < G; ++g) v = (int)threadIdx.x == g ? a[g] : v;
+  return v;
+}
+
+// Greedy task: chunk-local argmax of the raw logits (NaN first, lowest index wins).
+template <int DT, int EPT, int G, bool FAST>
+__device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int nrows, int64_t v0,
+                                   int64_t vend, uint64_t* s_key) {
+  float x[G][EPT];
+  load_rows<DT, EPT, G, FAST>(p, row0, nrows, v0, vend, x);
+  uint64_t key[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float bv = -INFINITY;
+    int bi = (int)v0;
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int idx = elem_index<DT, EPT>(v0, k);
+      const float v = x[g][k];
+      // indices rise along k: a strict compare keeps the first maximum; a NaN beats numbers
+      const bool take = ((v > bv) | ((v != v) & (bv == bv))) & (FAST || idx < vend);
+      bv = take ? v : bv;
+      bi = take ? idx : bi;
+    }
+    key[g] = argmax_key(bv, bi);
+  }
+  const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
+  if ((int)threadIdx.x < nrows) slot_store(p.arg_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c, best);
+}
+
+// A-task: per row of the group, the chunk's raw max and sum of exp2((x - mx) * c1).
+template <int DT, int EPT, int G, bool FAST>
+__device__ inline void task_stats(const VerifyParams& p, int c, int r, int row0, int nrows,
+                                  int64_t v0, int64_t vend, float* s_red) {
+  float x[G][EPT];
+  load_rows<DT, EPT, G, FAST>(p, row0, nrows, v0, vend, x);
+  const float c1 = exp2_scale(req_temperature(p, r));
+  float m[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) mm = fmaxf(mm, x[g][k]);
+    m[g] = mm;
+  }
+  block_max<G, kVWaves>(m, s_red);
+  float s[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float mg = m[g] == -INFINITY ? 0.f : m[g];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) ss += __builtin_amdgcn_exp2f((x[g][k] - mg) * c1);
+    s[g] = ss;
+  }
+  const float srow = block_sum_to_row_thread<G, kVWaves>(s, s_red);
+  if ((int)threadIdx.x < nrows) {
+    const float mrow = row_of_thread<G>(m);
+    slot_store(p.stat_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c,
+               pack_stats(mrow, mrow == -INFINITY ? 0.f : srow));
+  }
+}
+
+// B-task: per row of the group, the chunk-local argmax of max(p - q, 0) * (1 / E).  All of
+// the task's loads (the target slice again, noise chunk, draft chunks) are issued up front;
+// the group's stats were published by A-tasks holding lower tickets.
+template <int DT, int EPT, int G, bool FAST>
+__device__ inline void task_scores(const VerifyParams& p, int c, int r, int row0, int nrows,
+                                   int64_t v0, int64_t vend, uint64_t* s_key, float* s_M,
+                                   float* s_L) {
+  float x[G][EPT];
+  load_rows<DT, EPT, G, FAST>(p, row0, nrows, v0, vend, x);
+  float inv[EPT];
+  load_chunk_f32<DT, EPT, FAST>(p.noise + (int64_t)r * p.noise_stride, v0, vend, p.noise_aligned,
+                                1.f, inv);
+  float q[G][EPT];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (p.draft && g < nrows) {
+      load_chunk_f32<DT, EPT, FAST>(p.draft + (int64_t)(row0 + g) * p.draft_stride, v0, vend,
+                                    p.draft_aligned, 0.f, q[g]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) q[g][k] = 0.f;
+    }
+  }
+  const float c1 = exp2_scale(req_temperature(p, r));
+  if (wave_id() < nrows) {
+    float MX, S;
+    if (!wave_row_stats(p.stat_slots + (int64_t)(row0 + wave_id()) * p.nc, p.nc, c1, MX, S) &&
+        lane_id() == 0)
+      atomic_store_relaxed(&p.ctrl[1], 1);
+    if (lane_id() == 0) {
+      s_M[wave_id()] = MX;
+      s_L[wave_id()] = (float)(-log2((double)S));
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) inv[k] = 1.0f / inv[k];
+  uint64_t key[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float bv = -INFINITY;
+    int bi = (int)v0;
+    if (g < nrows) {
+      const float MX = s_M[g];
+      const float nl = s_L[g];
+      const int d = p.draft ? -1 : p.draft_ids[row0 + g];
 #pragma unroll
       for (int k = 0; k < EPT; ++k) {
         const int idx = elem_index<DT, EPT>(v0, k);
-        argmax_update(bv[g], bi[g], x[g][k], idx, FAST || idx < vend);
+        const float prob = __builtin_amdgcn_exp2f(fmaf(x[g][k] - MX, c1, nl));  // softmax
+        const float w = p.draft ? fmaxf(prob - q[g][k], 0.f) : (idx == d ? 0.f : prob);
+        const float score = w * inv[k];
+        // indices rise along k, so a strict compare keeps the first maximum
+        const bool take = (score > bv) & (FAST || idx < vend);
+        bv = take ? score : bv;
+        bi = take ? idx : bi;
       }
     }
-    block_argmax<G, kVWaves>(bv, bi, s_red, s_redi);
-    if (tid < nrows) {
-      float v = bv[0];
-      int i = bi[0];
-#pragma unroll
-      for (int g = 1; g < G; ++g) {
-        v = tid == g ? bv[g] : v;
-        i = tid == g ? bi[g] : i;
-      }
-      slot_store(p.arg_slots + (int64_t)(row0 + tid) * nc + c, pack_arg(v, i));
-    }
-  } else {
-    // ---- phase 1: temperature, chunk max, exp, chunk sum ----
-    const float temp = req_temperature(p, r);
-    if (temp != 1.f) {
-      const float rt = 1.0f / temp;
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int k = 0; k < EPT; ++k) x[g][k] = div_by(x[g][k], temp, rt);
-    }
-    float m[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mm = -INFINITY;
-#pragma unroll
-      for (int k = 0; k < EPT; ++k) mm = fmaxf(mm, x[g][k]);
-      m[g] = mm;
-    }
-    block_max<G, kVWaves>(m, s_red);
-    float s[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float ss = 0.f;
-      const float mg = m[g] == -INFINITY ? 0.f : m[g];
-#pragma unroll
-      for (int k = 0; k < EPT; ++k) {
-        const float e = exp_le0(x[g][k] - mg);
-        x[g][k] = e;
-        ss += e;
-      }
-      s[g] = ss;
-    }
-    block_sum<G, kVWaves>(s, s_red);
-    if (tid < nrows) {
-      float mv = m[0], sv = s[0];
-#pragma unroll
-      for (int g = 1; g < G; ++g) {
-        mv = tid == g ? m[g] : mv;
-        sv = tid == g ? s[g] : sv;
-      }
-      slot_store(p.stat_slots + (int64_t)(row0 + tid) * nc + c, pack_stats(mv, sv));
-    }
-
-    if (full) {
-      // ---- the request's noise chunk, in flight during the wait ----
-      float inv[EPT];
-      load_chunk_f32<DT, EPT, FAST>(p.noise + (int64_t)r * p.noise_stride, v0, vend,
-                                    p.noise_aligned, 1.f, inv);
-      // ---- wait until every chunk of the group's rows has published its stats ----
-      if (wave_id() < nrows &&
-          !wave_wait_slots(p.stat_slots + (int64_t)(row0 + wave_id()) * nc, nc, kSpinLimit) &&
-          lane_id() == 0)
-        atomic_store_relaxed(&p.ctrl[1], 1);
-      __syncthreads();
-      // ---- first row's draft chunk in flight while the partial stats are combined ----
-      float q[EPT];
-      if (p.draft) {
-        load_chunk_f32<DT, EPT, FAST>(p.draft + (int64_t)row0 * p.draft_stride, v0, vend,
-                                      p.draft_aligned, 0.f, q);
-      }
-      const int lane = lane_id();
-      for (int g = wave_id(); g < nrows; g += kVWaves) {
-        const int64_t row = row0 + g;
-        const uint64_t* sslots = p.stat_slots + row * nc;
-        float mm = -INFINITY;
-        for (int cc = lane; cc < nc; cc += kWave) mm = fmaxf(mm, unpack_stats(slot_load(sslots + cc)).x);
-        mm = wave_max(mm);
-        float ss = 0.f;
-        for (int cc = lane; cc < nc; cc += kWave) {
-          const float2 st = unpack_stats(slot_load(sslots + cc));
-          if (st.x != -INFINITY) ss += st.y * expf(st.x - mm);
-        }
-        ss = wave_sum(ss);
-        if (lane == 0) {
-          float mine = -INFINITY;
-#pragma unroll
-          for (int gg = 0; gg < G; ++gg) mine = gg == g ? m[gg] : mine;
-          s_f[g] = (mine == -INFINITY) ? 0.f : expf(mine - mm) / ss;
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < EPT; ++k) inv[k] = 1.0f / inv[k];
-      __syncthreads();
-
-      // ---- phase 2: score p - q against the noise, chunk-local argmax per row ----
-      float bv[G];
-      int bi[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        bv[g] = -INFINITY;
-        bi[g] = INT_MAX;
-        if (g < nrows) {
-          if (g > 0 && p.draft) {
-            load_chunk_f32<DT, EPT, FAST>(p.draft + (int64_t)(row0 + g) * p.draft_stride, v0,
-                                          vend, p.draft_aligned, 0.f, q);
-          }
-          const float f = s_f[g];
-          const int d = p.draft ? -1 : p.draft_ids[row0 + g];
-#pragma unroll
-          for (int k = 0; k < EPT; ++k) {
-            const int idx = elem_index<DT, EPT>(v0, k);
-            const float prob = x[g][k] * f;
-            const float w = p.draft ? fmaxf(prob - q[k], 0.f) : (idx == d ? 0.f : prob);
-            const float score = w * inv[k];
-            // indices rise along k, so a strict compare keeps the first maximum
-            const bool take = (score > bv[g]) & (FAST || idx < vend);
-            bv[g] = take ? score : bv[g];
-            bi[g] = take ? idx : bi[g];
-          }
-        }
-      }
-      block_argmax<G, kVWaves>(bv, bi, s_red, s_redi);
-      if (tid < nrows) {
-        float v = bv[0];
-        int i = bi[0];
-#pragma unroll
-        for (int g = 1; g < G; ++g) {
-          v = tid == g ? bv[g] : v;
-          i = tid == g ? bi[g] : i;
-        }
-        slot_store(p.arg_slots + (int64_t)(row0 + tid) * nc + c,
-                   pack_arg(v, i == INT_MAX ? (int)v0 : i));
-      }
-    }
+    key[g] = argmax_key(bv, bi);
   }
-
-  // ---- request completion: the last task runs the accept/reject chain ----
-  if (tid == 0) {
-    const int old = atomic_add_relaxed(&p.req_cnt[r], 1);
-    s_last = old == ngr * nc - 1;
-  }
-  __syncthreads();
-  if (s_last) finalize_request(p, r, greedy, full, fsm);
+  const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
+  if ((int)threadIdx.x < nrows) slot_store(p.arg_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c, best);
 }
 
 // ------------------------------------------------------------------ main kernel ------
@@ -534,19 +548,26 @@ __device__ inline void run_task(const VerifyParams& p, int gi, int c, int r, int
 #define MVSD_VERIFY_ATTRS
 #endif
 
+// Ticket t -> step s = t / steps_size: the first nc tickets of step s are the A-chunks (stats,
+// or the argmax for greedy groups) of group s; when the batch has random requests the next nc
+// are the B-chunks (scores) of group s - lag.  Slots of absent groups are claimed and skipped.
 template <int DT, int EPT, int G>
 __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(VerifyParams p) {
   static_assert(EPT % Elem<DT>::kVec == 0, "EPT must be a multiple of the vector width");
   __shared__ float s_red[G * kVWaves];
-  __shared__ int s_redi[G * kVWaves];
-  __shared__ float s_f[G];
+  __shared__ uint64_t s_key[G * kVWaves];
+  __shared__ float s_M[G];
+  __shared__ float s_L[G];
   __shared__ int s_task;
   __shared__ int s_last;
   __shared__ FinalizeSmem fsm;
 
   const int tid = threadIdx.x;
   const int nc = p.nc;
-  const int total = p.grp_off[p.B] * nc;
+  const int lag = p.lag;
+  const int groups = p.grp_off[p.B];
+  const int step_size = p.two_phase ? 2 * nc : nc;
+  const int total = (groups + (p.two_phase ? lag : 0)) * step_size;
 
   for (;;) {
     if (tid == 0) s_task = atomic_add_relaxed(&p.ctrl[0], 1);
@@ -555,43 +576,54 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
     __syncthreads();
     if (t >= total) break;
 
-    const int gi = t / nc;
-    const int c = t - gi * nc;
-    int lo = 0, hi = p.B;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (p.grp_off[mid] <= gi) lo = mid; else hi = mid;
-    }
-    const int r = lo;
+    const int step = t / step_size;
+    const int w = t - step * step_size;
+    const bool phase_b = w >= nc;
+    const int c = phase_b ? w - nc : w;
+    const int gi = phase_b ? step - lag : step;
+    if (gi < 0 || gi >= groups) continue;
+    const int r = p.grp_req[gi];
     int begin, K;
     req_range(p, r, begin, K);
     const int g0 = gi - p.grp_off[r];
     const int row0 = begin + g0 * G;
     const int nrows = min(G, K - g0 * G);
-    const int ngr = p.grp_off[r + 1] - p.grp_off[r];
+    const int ngr = (K + G - 1) / G;
     const bool greedy = req_is_greedy(p, r);
     const bool full = !greedy && p.recovered == nullptr;
+    if (phase_b && !full) continue;
     const int64_t v0 = (int64_t)c * p.chunk;
     const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
     const bool fast = p.target_aligned && vend - v0 == p.chunk &&
-                      (!full || (p.noise_aligned && (p.draft_aligned || !p.draft)));
-    if (fast) {
-      run_task<DT, EPT, G, true>(p, gi, c, r, row0, nrows, ngr, greedy, full, v0, vend, s_red,
-                                 s_redi, s_f, s_last, fsm);
+                      (!phase_b || (p.noise_aligned && (p.draft_aligned || !p.draft)));
+    if (greedy) {
+      if (fast) task_argmax<DT, EPT, G, true>(p, c, row0, nrows, v0, vend, s_key);
+      else task_argmax<DT, EPT, G, false>(p, c, row0, nrows, v0, vend, s_key);
+    } else if (!phase_b) {
+      if (fast) task_stats<DT, EPT, G, true>(p, c, r, row0, nrows, v0, vend, s_red);
+      else task_stats<DT, EPT, G, false>(p, c, r, row0, nrows, v0, vend, s_red);
     } else {
-      run_task<DT, EPT, G, false>(p, gi, c, r, row0, nrows, ngr, greedy, full, v0, vend, s_red,
-                                  s_redi, s_f, s_last, fsm);
+      if (fast) task_scores<DT, EPT, G, true>(p, c, r, row0, nrows, v0, vend, s_key, s_M, s_L);
+      else task_scores<DT, EPT, G, false>(p, c, r, row0, nrows, v0, vend, s_key, s_M, s_L);
+    }
+    // ---- request completion: the last counted task runs the accept/reject chain ----
+    // (counted: B-tasks of full random requests, A-tasks otherwise)
+    if (full == phase_b) {
+      if (tid == 0) s_last = atomic_add_relaxed(&p.req_cnt[r], 1) == ngr * nc - 1;
+      __syncthreads();
+      if (s_last) finalize_request(p, r, greedy, full, fsm);
     }
     __syncthreads();
   }
 
   // The last workgroup out (every other one has made its final claim and finished reading
-  // grp_off) returns the group offsets, ticket and exit counter to zero, so the whole
+  // grp_off / grp_req) returns the group tables, ticket and exit counter to zero, so the whole
   // workspace is zero again whatever layout the next call uses.
   if (tid == 0) s_last = atomic_add_relaxed(&p.ctrl[2], 1) == (int)gridDim.x - 1;
   __syncthreads();
   if (s_last) {
     for (int i = tid; i <= p.B; i += kVThreads) p.grp_off[i] = 0;
+    for (int i = tid; i < groups; i += kVThreads) p.grp_req[i] = 0;
     if (tid == 0) {
       atomic_store_relaxed(&p.ctrl[0], 0);
       atomic_store_relaxed(&p.ctrl[2], 0);
