@@ -241,6 +241,23 @@ def test_synthetic_mode_parity(device):
     check_parity(w, out, ref, "synthetic")
 
 
+@pytest.mark.parametrize("case", ["c2", "headline", "point_mass", "bf16_ragged", "odd_v"])
+def test_fused_kernel_parity(device, monkeypatch, case):
+    """The single-read kernel (MVSD_VERIFY_MODE=fused; the default is the split kernel).  Odd
+    V (unaligned rows) makes the host fall back to the split kernel."""
+    monkeypatch.setenv("MVSD_VERIFY_MODE", "fused")
+    draft_none = case == "point_mass"
+    w = {"c2": lambda: configs.random_c2(device),
+         "headline": lambda: configs.headline(device),
+         "point_mass": lambda: configs.random_c2(device, B=32, k=4, seed=4243),
+         "bf16_ragged": lambda: configs.ragged_c4(device, B=64),
+         "odd_v": lambda: configs.random_c2(device, B=16, k=3, V=4097, seed=11)}[case]()
+    rep = check_parity(w, run_workload(w, draft_none=draft_none),
+                       oracle_for(w, draft_none=draft_none), f"fused {case}")
+    assert rep.mismatched <= 4
+    assert rs.workspace_error_flag(w.target_logits.device) == 0
+
+
 @pytest.mark.parametrize("V", [5, 1001, 4097, 8193])
 def test_odd_vocab_sizes(device, V):
     """Unaligned rows (scalar loads) and partial last chunks."""

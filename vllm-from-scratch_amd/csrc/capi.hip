@@ -41,30 +41,45 @@ int elem_size(int dtype) {
 
 constexpr int kMaxDevices = 64;
 
-// Resident-workgroup capacity of the verify kernel per device and dtype (CUs x occupancy).
-int verify_capacity(int device, int dtype) {
+// Resident-workgroup capacity of a verify kernel per device, dtype and kernel kind
+// (CUs x occupancy).
+int verify_capacity(int device, int dtype, bool fused, bool has_draft) {
   static std::mutex mu;
-  static int cache[kMaxDevices][3];
+  static int cache[kMaxDevices][3][3];
   if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2) return 0;
   std::lock_guard<std::mutex> lock(mu);
-  if (cache[device][dtype] > 0) return cache[device][dtype];
+  int& slot = cache[device][dtype][fused ? (has_draft ? 2 : 1) : 0];
+  if (slot > 0) return slot;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     return 0;
+  const void* fn = mvsd::verify_kernel_ptr(dtype, fused, has_draft);
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mvsd::verify_kernel_ptr(dtype),
-                                                   mvsd::kVThreads, 0) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, mvsd::kVThreads, 0) != hipSuccess)
     return 0;
-  if (per_cu < 1) per_cu = 1;
-  cache[device][dtype] = cus * per_cu;
-  return cache[device][dtype];
+  // The persistent kernels rely on every launched workgroup being resident, so the runtime's
+  // figure is capped by an LDS estimate with a coarse (2 KiB) allocation granularity.
+  hipFuncAttributes attr;
+  int lds_cu = 0;
+  if (hipFuncGetAttributes(&attr, fn) == hipSuccess &&
+      hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, device) ==
+          hipSuccess &&
+      attr.sharedSizeBytes > 0) {
+    const int64_t granule = 2048;
+    const int64_t per_block = ((int64_t)attr.sharedSizeBytes + granule - 1) / granule * granule;
+    const int by_lds = (int)(lds_cu / per_block);
+    if (by_lds < per_cu) per_cu = by_lds;
+  }
+  if (per_cu < 1) return 0;
+  slot = cus * per_cu;
+  return slot;
 }
 
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 // Workspace layout.  ctrl = {ticket, sticky spin-limit flag (byte offset 4), exit counter}.
 struct WorkspaceLayout {
-  int64_t ctrl, grp_off, grp_req, req_cnt, stat_slots, arg_slots, total;
+  int64_t ctrl, grp_off, grp_desc, req_cnt, stat_slots, arg_slots, total;
 };
 
 WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
@@ -74,8 +89,8 @@ WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
   off = align_up(off + 3 * 4, 256);
   l.grp_off = off;
   off = align_up(off + (B + 1) * 4, 256);
-  l.grp_req = off;
-  off = align_up(off + (P > 0 ? P : 1) * 4, 256);
+  l.grp_desc = off;
+  off = align_up(off + (P > 0 ? P : 1) * 16, 256);
   l.req_cnt = off;
   off = align_up(off + (B > 0 ? B : 1) * 4, 256);
   l.stat_slots = off;
@@ -123,8 +138,8 @@ int64_t mvsd_rejection_workspace_bytes(int64_t batch_size, int64_t num_tokens, i
                                        int target_dtype, int64_t max_spec_len) {
   (void)max_spec_len;
   if (batch_size < 0 || num_tokens < 0 || vocab_size <= 0) return -1;
-  const mvsd::VerifyPlan plan = mvsd::verify_plan(target_dtype, vocab_size);
-  return verify_layout(batch_size, num_tokens, plan.nc).total;
+  const mvsd::VerifyPlan plan = mvsd::verify_plan(target_dtype, vocab_size, 0, 1, 0);
+  return verify_layout(batch_size, num_tokens, plan.nsub).total;
 }
 
 int mvsd_rejection_workspace_init(void* workspace, int64_t workspace_bytes, mvsd_stream_t stream) {
@@ -155,10 +170,48 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   const bool need_noise = !a->all_greedy && !a->recovered_token_ids;
   if (P > 0 && need_noise && (!a->exp_noise || a->noise_stride < V)) return MVSD_E_INVALID;
 
-  const mvsd::VerifyPlan plan = mvsd::verify_plan(a->target_dtype, V);
-  const WorkspaceLayout lay = verify_layout(B, P, plan.nc);
+  // Slot arrays are sized for the most chunks any plan can use (nsub), so the layout does not
+  // depend on the device.
+  const mvsd::VerifyPlan size_plan = mvsd::verify_plan(a->target_dtype, V, 0, 1, 0);
+  const WorkspaceLayout lay = verify_layout(B, P, size_plan.nsub);
   if (!a->workspace || a->workspace_bytes < lay.total) return MVSD_E_WORKSPACE;
   if ((uintptr_t)a->workspace % 256 != 0) return MVSD_E_ALIGN;
+
+  // Kernel choice: the split kernel (stats tasks, then score tasks that re-read the target
+  // chunk) by default.  MVSD_VERIFY_MODE=fused selects the single-read kernel for batches
+  // that need recovered scores, when its progress condition (resident workgroups >= chunks
+  // per row) and its load-width requirements hold.
+  const int two_phase = (!a->all_greedy && !a->recovered_token_ids) ? 1 : 0;
+  int cap = 0;
+  bool fused = false;
+  if (P > 0) {
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return hip_status(err);
+    // The fused kernel issues unconditional 16-byte loads: rows must be 16-byte aligned and
+    // V a multiple of the vector width.
+    const int esz = elem_size(a->target_dtype);
+    const bool vec_ok = aligned16(a->target_logits, a->target_stride * esz) &&
+                        aligned16(a->exp_noise, a->noise_stride * 4) &&
+                        (!a->draft_probs || aligned16(a->draft_probs, a->draft_stride * 4)) &&
+                        V % (16 / esz) == 0;
+    const char* mode = getenv("MVSD_VERIFY_MODE");
+    if (two_phase && vec_ok && mode && strcmp(mode, "fused") == 0) {
+      const int fcap = verify_capacity(device, a->target_dtype, true, a->draft_probs != nullptr);
+      if (fcap >= size_plan.nsub && fcap > 0) {
+        fused = true;
+        cap = fcap;
+      }
+    }
+    if (!fused) cap = verify_capacity(device, a->target_dtype, false, false);
+    if (cap <= 0) return hip_status(hipErrorInvalidDevice);
+  }
+  // Upper bound on groups: min(P, B * ceil(max_spec_len / G)).
+  int64_t groups = B * ((a->max_spec_len + size_plan.g - 1) / size_plan.g);
+  if (groups > P) groups = P;
+  mvsd::VerifyPlan plan = size_plan;
+  if (!fused)
+    plan = mvsd::verify_plan(a->target_dtype, V, groups > 0 ? groups : 1, two_phase ? 2 : 1, cap);
 
   char* ws = static_cast<char*>(a->workspace);
   mvsd::VerifyParams p;
@@ -196,33 +249,31 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   p.noise_aligned = a->exp_noise ? aligned16(a->exp_noise, a->noise_stride * 4) : false;
   p.ctrl = reinterpret_cast<int*>(ws + lay.ctrl);
   p.grp_off = reinterpret_cast<int*>(ws + lay.grp_off);
-  p.grp_req = reinterpret_cast<int*>(ws + lay.grp_req);
+  p.grp_desc = reinterpret_cast<int4*>(ws + lay.grp_desc);
   p.req_cnt = reinterpret_cast<int*>(ws + lay.req_cnt);
   p.stat_slots = reinterpret_cast<uint64_t*>(ws + lay.stat_slots);
   p.arg_slots = reinterpret_cast<uint64_t*>(ws + lay.arg_slots);
 
   int grid = 0;
   if (P > 0) {
-    int device = 0;
-    hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess) return hip_status(err);
-    const int cap = verify_capacity(device, a->target_dtype);
-    if (cap <= 0) return hip_status(hipErrorInvalidDevice);
-    // Upper bound on tasks: groups <= min(P, B * ceil(max_spec_len / G)).
-    int64_t groups = B * ((a->max_spec_len + plan.g - 1) / plan.g);
-    if (groups > P) groups = P;
-    // B-chunks of a group are claimed `lag` groups after its A-chunks, far enough that the
-    // resident workgroups have finished the A-chunks (no waiting in the common case) and
-    // close enough that the re-read target slice is still in the Infinity Cache.
-    p.two_phase = (!a->all_greedy && !a->recovered_token_ids) ? 1 : 0;
-    int lag = cap / (2 * plan.nc) + 4;
-    if (const char* env = getenv("MVSD_VERIFY_LAG")) lag = atoi(env);
-    p.lag = lag < 1 ? 1 : (lag > 256 ? 256 : lag);
-    const int64_t step = p.two_phase ? 2 * plan.nc : plan.nc;
-    const int64_t tasks = (groups + (p.two_phase ? p.lag : 0)) * step;
+    int64_t tasks;
+    if (fused) {
+      tasks = groups * plan.nc;
+    } else {
+      // B-chunks of a group are claimed `lag` groups after its A-chunks: far enough that the
+      // resident workgroups (each holding a current and a prefetched ticket) have finished the
+      // A-chunks, so score tasks rarely wait.
+      p.two_phase = two_phase;
+      int lag = (2 * cap + 2 * plan.nc - 1) / (2 * plan.nc) + 2;
+      if (const char* env = getenv("MVSD_VERIFY_LAG")) lag = atoi(env);
+      p.lag = lag < 1 ? 1 : (lag > 4096 ? 4096 : lag);
+      const int64_t step = p.two_phase ? 2 * plan.nc : plan.nc;
+      tasks = (groups + (p.two_phase ? p.lag : 0)) * step;
+    }
+    if (tasks > 0x7fffffff - 2 * (int64_t)cap) return MVSD_E_RANGE;
     grid = (int)(tasks < cap ? tasks : cap);
   }
-  return hip_status(mvsd::launch_verify(p, a->target_dtype, grid, (hipStream_t)stream));
+  return hip_status(mvsd::launch_verify(p, a->target_dtype, fused, grid, (hipStream_t)stream));
 }
 
 int mvsd_softmax_rows(float* probs, int64_t probs_stride, const void* logits, int dtype,

@@ -30,6 +30,7 @@ struct Elem<MVSD_F32> {
   using storage = float;
   static constexpr int kVec = 4;  // elements per 16-byte load
   __device__ static inline float cvt(float v) { return v; }
+  __device__ static inline float ninf() { return -INFINITY; }
 };
 
 template <>
@@ -37,6 +38,7 @@ struct Elem<MVSD_BF16> {
   using storage = uint16_t;
   static constexpr int kVec = 8;
   __device__ static inline float cvt(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
+  __device__ static inline uint16_t ninf() { return 0xff80; }
 };
 
 template <>
@@ -44,6 +46,7 @@ struct Elem<MVSD_F16> {
   using storage = _Float16;
   static constexpr int kVec = 8;
   __device__ static inline float cvt(_Float16 v) { return static_cast<float>(v); }
+  __device__ static inline _Float16 ninf() { return static_cast<_Float16>(-INFINITY); }
 };
 
 // Load kVec consecutive elements starting at p[idx] and convert them to fp32.  Elements at
@@ -90,26 +93,63 @@ __device__ inline void argmax_update(float& bv, int& bi, float v, int i, bool va
 }
 
 // ------------------------------------------------------------------ wave reductions --
+// Cross-lane steps use DPP row permutations (VALU, no LDS round trip): quad swaps for lane
+// xor 1 and 2, then the half-row and row mirrors, after which every lane of a 16-lane row
+// holds the row's result; the four row results are combined from v_readlane in a fixed
+// order, so every lane gets the same, deterministic value.  All combining operations here
+// are commutative.
+
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8 lanes
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within each row
+
+template <int CTRL>
+__device__ inline int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ inline float dpp_f32(float v) {
+  return __int_as_float(dpp_i32<CTRL>(__float_as_int(v)));
+}
+__device__ inline float readlane_f32(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
 
 __device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  v = fmaxf(v, dpp_f32<kDppXor1>(v));
+  v = fmaxf(v, dpp_f32<kDppXor2>(v));
+  v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f32<kDppMirror>(v));
+  return fmaxf(fmaxf(readlane_f32(v, 0), readlane_f32(v, 16)),
+               fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
 }
 
 __device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  v += dpp_f32<kDppXor1>(v);
+  v += dpp_f32<kDppXor2>(v);
+  v += dpp_f32<kDppHalfMirror>(v);
+  v += dpp_f32<kDppMirror>(v);
+  return (readlane_f32(v, 0) + readlane_f32(v, 16)) + (readlane_f32(v, 32) + readlane_f32(v, 48));
+}
+
+template <int CTRL>
+__device__ inline void argmax_step(float& v, int& i) {
+  argmax_update(v, i, dpp_f32<CTRL>(v), dpp_i32<CTRL>(i), true);
 }
 
 __device__ inline void wave_argmax(float& v, int& i) {
+  argmax_step<kDppXor1>(v, i);
+  argmax_step<kDppXor2>(v, i);
+  argmax_step<kDppHalfMirror>(v, i);
+  argmax_step<kDppMirror>(v, i);
+  float bv = readlane_f32(v, 0);
+  int bi = __builtin_amdgcn_readlane(i, 0);
 #pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(v, o, kWave);
-    const int oi = __shfl_xor(i, o, kWave);
-    argmax_update(v, i, ov, oi, true);
-  }
+  for (int r = 1; r < 4; ++r)
+    argmax_update(bv, bi, readlane_f32(v, 16 * r), __builtin_amdgcn_readlane(i, 16 * r), true);
+  v = bv;
+  i = bi;
 }
 
 __device__ inline int lane_id() { return threadIdx.x & (kWave - 1); }
@@ -200,14 +240,28 @@ __device__ inline uint64_t argmax_key(float v, int idx) {
 
 __device__ inline int key_index(uint64_t key) { return (int)(0xffffffffu - (uint32_t)key); }
 
+template <int CTRL>
+__device__ inline uint64_t dpp_u64(uint64_t k) {
+  const uint32_t lo = (uint32_t)dpp_i32<CTRL>((int)(uint32_t)k);
+  const uint32_t hi = (uint32_t)dpp_i32<CTRL>((int)(uint32_t)(k >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ inline uint64_t readlane_u64(uint64_t k, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ inline uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
 __device__ inline uint64_t wave_max_u64(uint64_t k) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) {
-    const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), o, kWave) << 32) |
-                           (uint32_t)__shfl_xor((int)(uint32_t)k, o, kWave);
-    k = other > k ? other : k;
-  }
-  return k;
+  k = umax64(k, dpp_u64<kDppXor1>(k));
+  k = umax64(k, dpp_u64<kDppXor2>(k));
+  k = umax64(k, dpp_u64<kDppHalfMirror>(k));
+  k = umax64(k, dpp_u64<kDppMirror>(k));
+  return umax64(umax64(readlane_u64(k, 0), readlane_u64(k, 16)),
+                umax64(readlane_u64(k, 32), readlane_u64(k, 48)));
 }
 
 // Per-row maximum of N keys over a block of NW wavefronts; only thread g (< N) receives row
@@ -267,6 +321,9 @@ __device__ inline int atomic_add_relaxed(int* p, int v) {
 __device__ inline int atomic_load_acquire(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ inline int atomic_load_relaxed(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ inline void atomic_store_relaxed(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -304,13 +361,17 @@ __device__ inline void unpack_arg(uint64_t s, float& v, int& idx) {
 
 // One wavefront waits until the n slots at `slots` are all written.  Returns false when the
 // bounded spin runs out (the caller flags the error and carries on, so every wave exits).
-__device__ inline bool wave_wait_slots(const uint64_t* slots, int n, int spin_limit) {
+// Wait until slots[0..n) are all written.  Gives up (returns false) after spin_limit polls,
+// or early once the sticky failure flag *abort is set by any wave, so that one wait that
+// cannot complete ends every other wait quickly instead of each running to its own limit.
+__device__ inline bool wave_wait_slots(const uint64_t* slots, int n, int spin_limit, const int* abort) {
   const int lane = threadIdx.x & (kWave - 1);
   for (int spins = 0;; ++spins) {
     int ready = 1;
     for (int c = lane; c < n; c += kWave) ready &= slot_load(slots + c) != 0;
     if (__all(ready)) return true;
     if (spins >= spin_limit) return false;
+    if ((spins & 255) == 255 && atomic_load_relaxed(abort) != 0) return false;
     __builtin_amdgcn_s_sleep(1);
   }
 }

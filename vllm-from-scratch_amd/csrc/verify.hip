@@ -33,13 +33,18 @@
 // task's loads in flight together); the last chunk of a row and unaligned rows take a
 // bounds-checked path.
 #include <float.h>
+#include <stdlib.h>
+
+#include <type_traits>
 
 #include "mvsd_device.h"
 #include "verify.h"
 
 namespace mvsd {
 
-constexpr int kSpinLimit = 1 << 21;
+// Polls before a wait gives up and sets the sticky flag (ctrl[1]); with a poll every ~1-2 us
+// this is a fraction of a second, far beyond any wait of a healthy run.
+constexpr int kSpinLimit = 1 << 18;
 
 // Request r's verify rows [begin, begin + K), clamped so that inconsistent metadata can
 // produce wrong tokens but never an out-of-bounds access: 0 <= begin <= begin + K <= P and
@@ -92,72 +97,18 @@ __device__ inline float exp_le0(float d) {
   return fmaf(e, lo * kLn2, e);
 }
 
+// log2(e) / T rounded once from double.
+__device__ inline float exp2_scale(float temp) {
+  return (float)(1.4426950408889634074 / (double)temp);
+}
+
+// Group descriptor flags.
+constexpr int kGreedy = 1;
+constexpr int kFull = 2;  // random request whose recovered ids come from in-kernel scores
+
 // ------------------------------------------------------------------ loads ------------
-// EPT consecutive-by-lane elements of one row chunk into fp32 registers.  FAST: full,
-// aligned chunk, unconditional 16-byte loads.  Otherwise bounds-checked, `fill` beyond vend.
-template <int DT, int EPT, bool FAST>
-__device__ inline void load_chunk(const typename Elem<DT>::storage* __restrict__ base, int64_t v0,
-                                  int64_t vend, bool aligned, float fill, float (&out)[EPT]) {
-  using S = typename Elem<DT>::storage;
-  constexpr int VEC = Elem<DT>::kVec;
-  constexpr int NV = EPT / VEC;
-  const int tid = threadIdx.x;
-  if constexpr (FAST) {
-    u32x4 raw[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      raw[i] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(base + v0 + ((int64_t)i * kVThreads + tid) * VEC));
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const S* s = reinterpret_cast<const S*>(&raw[i]);
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) out[i * VEC + j] = Elem<DT>::cvt(s[j]);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      float tmp[VEC];
-      load_vec<DT>(base, v0 + ((int64_t)i * kVThreads + tid) * VEC, vend, aligned, fill, tmp);
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) out[i * VEC + j] = tmp[j];
-    }
-  }
-}
-
-// fp32 chunk whose lane layout follows a DT row (VEC elements of DT per 16-byte group).
-template <int DT, int EPT, bool FAST>
-__device__ inline void load_chunk_f32(const float* __restrict__ base, int64_t v0, int64_t vend,
-                                      bool aligned, float fill, float (&out)[EPT]) {
-  constexpr int VEC = Elem<DT>::kVec;
-  constexpr int NV = EPT / VEC;
-  const int tid = threadIdx.x;
-  if constexpr (FAST) {
-    u32x4 raw[EPT / 4];
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-#pragma unroll
-      for (int h = 0; h < VEC / 4; ++h)
-        raw[i * (VEC / 4) + h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-            base + v0 + ((int64_t)i * kVThreads + tid) * VEC + h * 4));
-#pragma unroll
-    for (int k = 0; k < EPT / 4; ++k)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) out[k * 4 + j] = __uint_as_float(raw[k][j]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-#pragma unroll
-      for (int h = 0; h < VEC; h += 4) {
-        float tmp[4];
-        load_vec<MVSD_F32>(base, v0 + ((int64_t)i * kVThreads + tid) * VEC + h, vend, aligned,
-                           fill, tmp);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) out[i * VEC + h + j] = tmp[j];
-      }
-  }
-}
-
+// Column of element k of this thread in the sub-chunk starting at v0: 16-byte vectors of kVec
+// elements, consecutive lanes on consecutive vectors.
 template <int DT, int EPT>
 __device__ inline int elem_index(int64_t v0, int k) {
   constexpr int VEC = Elem<DT>::kVec;
@@ -205,7 +156,14 @@ __global__ __launch_bounds__(1024) void verify_init_kernel(VerifyParams p) {
     if (r < p.B) {
       const int first = carry + s_scan[tid] - ng;
       p.grp_off[r] = first;
-      for (int g = 0; g < ng; ++g) p.grp_req[first + g] = r;
+      if (ng > 0) {
+        const bool greedy = req_is_greedy(p, r);
+        const int flags = (greedy ? kGreedy : 0) | (!greedy && !p.recovered ? kFull : 0);
+        const int c1 = __float_as_int(exp2_scale(req_temperature(p, r)));
+        for (int g = 0; g < ng; ++g)
+          p.grp_desc[first + g] =
+              make_int4(r, b + g * p.G, min(p.G, k - g * p.G) | ng << 8 | flags << 16, c1);
+      }
     }
     __syncthreads();
     if (tid == 1023) s_carry = carry + s_scan[1023];
@@ -219,15 +177,11 @@ __global__ __launch_bounds__(1024) void verify_init_kernel(VerifyParams p) {
 // c1 = log2(e) / T: for T > 0 the max of x / T is the max of x divided by T, so no per-element
 // division is needed, and p = exp((x - MX) / T) / S = exp2(fma(x - MX, c1, -log2 S)).
 
-// log2(e) / T rounded once from double.
-__device__ inline float exp2_scale(float temp) {
-  return (float)(1.4426950408889634074 / (double)temp);
-}
-
 // One wavefront: wait until the n stats slots of a row are written, then combine them into
 // the row's raw max MX and S = sum_c s_c * 2^((mx_c - MX) * c1).  Up to 4 * 64 slots are kept
 // in registers from the last poll.
-__device__ inline bool wave_row_stats(const uint64_t* slots, int n, float c1, float& MX, float& S) {
+__device__ inline bool wave_row_stats(const uint64_t* slots, int n, float c1, const int* abort,
+                                      float& MX, float& S) {
   const int lane = lane_id();
   constexpr int R = 4;
   uint64_t v[R];
@@ -242,7 +196,7 @@ __device__ inline bool wave_row_stats(const uint64_t* slots, int n, float c1, fl
     }
     for (int c = lane + R * kWave; c < n; c += kWave) ready &= slot_load(slots + c) != 0;
     if (__all(ready)) break;
-    if (spins >= kSpinLimit) {
+    if (spins >= kSpinLimit || ((spins & 255) == 255 && atomic_load_relaxed(abort) != 0)) {
       ok = false;
       break;
     }
@@ -290,7 +244,7 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
     uint64_t* aslots = p.arg_slots + row * nc;
     uint64_t* sslots = p.stat_slots + row * nc;
     if (greedy || full) {
-      if (!wave_wait_slots(aslots, nc, kSpinLimit) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
+      if (!wave_wait_slots(aslots, nc, kSpinLimit, &p.ctrl[1]) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
       uint64_t best = 0;
       for (int c = lane; c < nc; c += kWave) {
         const uint64_t k = slot_load(aslots + c);
@@ -305,7 +259,7 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
     if (!greedy) {
       const float c1 = exp2_scale(req_temperature(p, r));
       float MX, S;
-      if (!wave_row_stats(sslots, nc, c1, MX, S) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
+      if (!wave_row_stats(sslots, nc, c1, &p.ctrl[1], MX, S) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
       if (lane == 0) {
         sm.M[k] = MX;
         sm.S[k] = S;
@@ -384,22 +338,143 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
 
 // ------------------------------------------------------------------ tasks ------------
 
-// The group's target slice into registers (-inf beyond V and for rows >= nrows).
-template <int DT, int EPT, int G, bool FAST>
-__device__ inline void load_rows(const VerifyParams& p, int row0, int nrows, int64_t v0,
-                                 int64_t vend, float (&x)[G][EPT]) {
+// A task covers rows [row0, row0 + nrows) of one group and columns [v0, vend), walked in
+// sub-chunks of kVThreads * EPT columns.  Full, aligned sub-chunks are double-buffered: the
+// loads of sub-chunk j + 1 are issued before sub-chunk j is reduced, so a workgroup keeps HBM
+// requests in flight for the whole task.  Buffers hold the raw 16-byte vectors; elements are
+// converted to fp32 only when they are consumed.
+
+template <bool F>
+using Fast = std::integral_constant<bool, F>;
+
+// Element k (0 <= k < EPT) of a DT row buffer, as fp32.
+template <int DT>
+__device__ inline float raw_elem(const u32x4* raw, int k) {
   using S = typename Elem<DT>::storage;
+  constexpr int VEC = Elem<DT>::kVec;
+  const S* s = reinterpret_cast<const S*>(&raw[k / VEC]);
+  return Elem<DT>::cvt(s[k % VEC]);
+}
+
+// Element k of an fp32 buffer laid out like a DT row (the 4-element vector k / 4 holds
+// elements 4 (k / 4) .. 4 (k / 4) + 3 for every DT, since kVec is a multiple of 4).
+__device__ inline float raw_f32(const u32x4* raw, int k) { return __uint_as_float(raw[k / 4][k % 4]); }
+
+// Column of the first element of 16-byte vector i of this thread (DT layout).
+template <int DT>
+__device__ inline int64_t vec_col(int64_t s0, int i) {
+  constexpr int VEC = Elem<DT>::kVec;
+  return s0 + ((int64_t)i * kVThreads + threadIdx.x) * VEC;
+}
+
+// Target loads: non-temporal unless MVSD_VERIFY_NT_TARGET is 0 (tuning switch).
+#ifndef MVSD_VERIFY_NT_TARGET
+#define MVSD_VERIFY_NT_TARGET 1
+#endif
+__device__ inline u32x4 load_target16(const void* p) {
+  const u32x4* q = static_cast<const u32x4*>(p);
+  if constexpr (MVSD_VERIFY_NT_TARGET) return __builtin_nontemporal_load(q);
+  else return *q;
+}
+
+// DT row sub-chunk, full and aligned.
+template <int DT, int EPT>
+__device__ inline void load_raw(const typename Elem<DT>::storage* __restrict__ base, int64_t s0,
+                                u32x4 (&out)[EPT / Elem<DT>::kVec]) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (g < nrows) {
-      const S* base = static_cast<const S*>(p.target) + target_row(p, row0 + g) * p.target_stride;
-      load_chunk<DT, EPT, FAST>(base, v0, vend, p.target_aligned, -INFINITY, x[g]);
+  for (int i = 0; i < EPT / Elem<DT>::kVec; ++i) out[i] = load_target16(base + vec_col<DT>(s0, i));
+}
+
+// DT row sub-chunk, bounds-checked: elements at or beyond vend read as `fill`.
+template <int DT, int EPT>
+__device__ inline void load_raw_checked(const typename Elem<DT>::storage* __restrict__ base,
+                                        int64_t s0, int64_t vend, bool aligned,
+                                        typename Elem<DT>::storage fill,
+                                        u32x4 (&out)[EPT / Elem<DT>::kVec]) {
+  using S = typename Elem<DT>::storage;
+  constexpr int VEC = Elem<DT>::kVec;
+#pragma unroll
+  for (int i = 0; i < EPT / VEC; ++i) {
+    const int64_t col = vec_col<DT>(s0, i);
+    if (aligned && col + VEC <= vend) {
+      out[i] = load_target16(base + col);
     } else {
+      S tmp[VEC];
 #pragma unroll
-      for (int k = 0; k < EPT; ++k) x[g][k] = -INFINITY;
+      for (int j = 0; j < VEC; ++j) tmp[j] = col + j < vend ? base[col + j] : fill;
+      out[i] = *reinterpret_cast<const u32x4*>(tmp);
     }
   }
 }
+
+// fp32 row sub-chunk in DT layout; FAST: full and aligned, else bounds-checked with `fill`.
+template <int DT, int EPT, bool FAST>
+__device__ inline void load_raw_f32(const float* __restrict__ base, int64_t s0, int64_t vend,
+                                    bool aligned, float fill, u32x4 (&out)[EPT / 4]) {
+  constexpr int VEC = Elem<DT>::kVec;
+#pragma unroll
+  for (int m = 0; m < EPT / 4; ++m) {
+    const int64_t col = vec_col<DT>(s0, m / (VEC / 4)) + (m % (VEC / 4)) * 4;
+    if (FAST || (aligned && col + 4 <= vend)) {
+      out[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + col));
+    } else {
+      float tmp[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tmp[j] = col + j < vend ? base[col + j] : fill;
+      out[m] = *reinterpret_cast<const u32x4*>(tmp);
+    }
+  }
+}
+
+// Walk [v0, vend) in SUB-column sub-chunks: load(buf, s0, Fast<bool>) issues a sub-chunk's
+// loads, body(buf, s0, Fast<bool>) consumes them.  hook() runs once, after the first loads
+// are issued.  Unaligned inputs and the partial last sub-chunk take the checked path.
+template <int SUB, typename Buf, typename Load, typename Body, typename Hook>
+__device__ inline void pipeline(int64_t v0, int64_t vend, bool aligned, Load&& load, Body&& body,
+                                Hook&& hook) {
+  const int nfull = aligned ? (int)((vend - v0) / SUB) : 0;
+  Buf a, b;
+  if (nfull > 0) {
+    load(a, v0, Fast<true>());
+    hook();
+    for (int j = 0;;) {
+      if (j + 1 < nfull) load(b, v0 + (int64_t)(j + 1) * SUB, Fast<true>());
+      body(a, v0 + (int64_t)j * SUB, Fast<true>());
+      if (++j == nfull) break;
+      if (j + 1 < nfull) load(a, v0 + (int64_t)(j + 1) * SUB, Fast<true>());
+      body(b, v0 + (int64_t)j * SUB, Fast<true>());
+      if (++j == nfull) break;
+    }
+  } else {
+    hook();
+  }
+  for (int64_t s0 = v0 + (int64_t)nfull * SUB; s0 < vend; s0 += SUB) {
+    load(a, s0, Fast<false>());
+    body(a, s0, Fast<false>());
+  }
+}
+
+// Base pointers of the group's target rows (rows past nrows repeat the last one).
+template <int DT, int G>
+__device__ inline void target_bases(const VerifyParams& p, int row0, int nrows,
+                                    const typename Elem<DT>::storage* (&tb)[G]) {
+  using S = typename Elem<DT>::storage;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    tb[g] = static_cast<const S*>(p.target) + target_row(p, row0 + min(g, nrows - 1)) * p.target_stride;
+}
+
+template <int DT, int EPT, int G>
+struct TargetBuf {
+  u32x4 x[G][EPT / Elem<DT>::kVec];
+};
+
+template <int DT, int EPT, int G>
+struct ScoreBuf {
+  u32x4 x[G][EPT / Elem<DT>::kVec];
+  u32x4 q[G][EPT / 4];
+  u32x4 e[EPT / 4];
+};
 
 // Value of a per-row register array for row = this thread's index (threads < G).
 template <int G, typename T>
@@ -410,134 +485,222 @@ __device__ inline T row_of_thread(const T (&a)[G]) {
   return v;
 }
 
+template <int DT, int EPT, int G>
+__device__ inline auto target_loader(const VerifyParams& p, const typename Elem<DT>::storage* (&tb)[G],
+                                     int nrows, int64_t vend) {
+  return [&p, &tb, nrows, vend](TargetBuf<DT, EPT, G>& buf, int64_t s0, auto fast) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (g < nrows) {
+        if constexpr (decltype(fast)::value) load_raw<DT, EPT>(tb[g], s0, buf.x[g]);
+        else load_raw_checked<DT, EPT>(tb[g], s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x[g]);
+      }
+    }
+  };
+}
+
 // Greedy task: chunk-local argmax of the raw logits (NaN first, lowest index wins).
-template <int DT, int EPT, int G, bool FAST>
+template <int DT, int EPT, int G, typename Hook>
 __device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int nrows, int64_t v0,
-                                   int64_t vend, uint64_t* s_key) {
-  float x[G][EPT];
-  load_rows<DT, EPT, G, FAST>(p, row0, nrows, v0, vend, x);
-  uint64_t key[G];
+                                   int64_t vend, uint64_t* s_key, Hook&& after_loads) {
+  using S = typename Elem<DT>::storage;
+  const S* tb[G];
+  target_bases<DT, G>(p, row0, nrows, tb);
+  float bv[G];
+  int bi[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float bv = -INFINITY;
-    int bi = (int)v0;
-#pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-      const int idx = elem_index<DT, EPT>(v0, k);
-      const float v = x[g][k];
-      // indices rise along k: a strict compare keeps the first maximum; a NaN beats numbers
-      const bool take = ((v > bv) | ((v != v) & (bv == bv))) & (FAST || idx < vend);
-      bv = take ? v : bv;
-      bi = take ? idx : bi;
-    }
-    key[g] = argmax_key(bv, bi);
+    bv[g] = -INFINITY;
+    bi[g] = (int)v0;
   }
+  auto body = [&](const TargetBuf<DT, EPT, G>& buf, int64_t s0, auto fast) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (g < nrows) {
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+          const int idx = elem_index<DT, EPT>(s0, k);
+          const float v = raw_elem<DT>(buf.x[g], k);
+          // columns rise with s0 and k: a strict compare keeps the first maximum; NaN wins
+          const bool take = ((v > bv[g]) | ((v != v) & (bv[g] == bv[g]))) &
+                            (decltype(fast)::value || idx < vend);
+          bv[g] = take ? v : bv[g];
+          bi[g] = take ? idx : bi[g];
+        }
+      }
+    }
+  };
+  pipeline<kVThreads * EPT, TargetBuf<DT, EPT, G>>(v0, vend, p.target_aligned,
+                                                   target_loader<DT, EPT, G>(p, tb, nrows, vend),
+                                                   body, after_loads);
+  uint64_t key[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) key[g] = argmax_key(bv[g], bi[g]);
   const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
   if ((int)threadIdx.x < nrows) slot_store(p.arg_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c, best);
 }
 
-// A-task: per row of the group, the chunk's raw max and sum of exp2((x - mx) * c1).
-template <int DT, int EPT, int G, bool FAST>
-__device__ inline void task_stats(const VerifyParams& p, int c, int r, int row0, int nrows,
-                                  int64_t v0, int64_t vend, float* s_red) {
-  float x[G][EPT];
-  load_rows<DT, EPT, G, FAST>(p, row0, nrows, v0, vend, x);
-  const float c1 = exp2_scale(req_temperature(p, r));
-  float m[G];
+// A-task: per row of the group, the chunk's raw max mx and sum of exp2((x - mx) * c1), kept
+// online per thread (the running sum is rescaled when the thread's max grows).
+template <int DT, int EPT, int G, typename Hook>
+__device__ inline void task_stats(const VerifyParams& p, int c, float c1, int row0, int nrows,
+                                  int64_t v0, int64_t vend, float* s_red, Hook&& after_loads) {
+  using S = typename Elem<DT>::storage;
+  const S* tb[G];
+  target_bases<DT, G>(p, row0, nrows, tb);
+  float m[G], s[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float mm = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < EPT; ++k) mm = fmaxf(mm, x[g][k]);
-    m[g] = mm;
+    m[g] = -INFINITY;
+    s[g] = 0.f;
   }
-  block_max<G, kVWaves>(m, s_red);
-  float s[G];
+  auto body = [&](const TargetBuf<DT, EPT, G>& buf, int64_t, auto) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float mg = m[g] == -INFINITY ? 0.f : m[g];
-    float ss = 0.f;
+    for (int g = 0; g < G; ++g) {
+      if (g < nrows) {
+        float x[EPT];
+        float lm = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) ss += __builtin_amdgcn_exp2f((x[g][k] - mg) * c1);
-    s[g] = ss;
-  }
+        for (int k = 0; k < EPT; ++k) {
+          x[k] = raw_elem<DT>(buf.x[g], k);
+          lm = fmaxf(lm, x[k]);
+        }
+        if (lm > m[g]) {  // m = -inf: the old sum is 0 and exp2(-inf) = 0
+          s[g] *= __builtin_amdgcn_exp2f((m[g] - lm) * c1);
+          m[g] = lm;
+        }
+        const float ref = m[g] == -INFINITY ? 0.f : m[g];
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) acc += __builtin_amdgcn_exp2f((x[k] - ref) * c1);
+        s[g] += acc;
+      }
+    }
+  };
+  pipeline<kVThreads * EPT, TargetBuf<DT, EPT, G>>(v0, vend, p.target_aligned,
+                                                   target_loader<DT, EPT, G>(p, tb, nrows, vend),
+                                                   body, after_loads);
+  float M[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) M[g] = m[g];
+  block_max<G, kVWaves>(M, s_red);
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    s[g] = m[g] == -INFINITY ? 0.f : s[g] * __builtin_amdgcn_exp2f((m[g] - M[g]) * c1);
   const float srow = block_sum_to_row_thread<G, kVWaves>(s, s_red);
   if ((int)threadIdx.x < nrows) {
-    const float mrow = row_of_thread<G>(m);
+    const float mrow = row_of_thread<G>(M);
     slot_store(p.stat_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c,
                pack_stats(mrow, mrow == -INFINITY ? 0.f : srow));
   }
 }
 
-// B-task: per row of the group, the chunk-local argmax of max(p - q, 0) * (1 / E).  All of
-// the task's loads (the target slice again, noise chunk, draft chunks) are issued up front;
-// the group's stats were published by A-tasks holding lower tickets.
-template <int DT, int EPT, int G, bool FAST>
-__device__ inline void task_scores(const VerifyParams& p, int c, int r, int row0, int nrows,
-                                   int64_t v0, int64_t vend, uint64_t* s_key, float* s_M,
-                                   float* s_L) {
-  float x[G][EPT];
-  load_rows<DT, EPT, G, FAST>(p, row0, nrows, v0, vend, x);
-  float inv[EPT];
-  load_chunk_f32<DT, EPT, FAST>(p.noise + (int64_t)r * p.noise_stride, v0, vend, p.noise_aligned,
-                                1.f, inv);
-  float q[G][EPT];
+// B-task: per row of the group, the chunk-local argmax of max(p - q, 0) * (1 / E).  The
+// group's stats were published by A-tasks holding lower tickets; the wait for them overlaps
+// with the first sub-chunk's loads.
+template <int DT, int EPT, int G, typename Hook>
+__device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1, int row0,
+                                   int nrows, int64_t v0, int64_t vend, uint64_t* s_key,
+                                   float* s_M, float* s_L, Hook&& after_loads) {
+  using S = typename Elem<DT>::storage;
+  using Buf = ScoreBuf<DT, EPT, G>;
+  const S* tb[G];
+  target_bases<DT, G>(p, row0, nrows, tb);
+  const float* qb[G];
+  int d[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    if (p.draft && g < nrows) {
-      load_chunk_f32<DT, EPT, FAST>(p.draft + (int64_t)(row0 + g) * p.draft_stride, v0, vend,
-                                    p.draft_aligned, 0.f, q[g]);
-    } else {
-#pragma unroll
-      for (int k = 0; k < EPT; ++k) q[g][k] = 0.f;
-    }
+    const int row = row0 + min(g, nrows - 1);
+    qb[g] = p.draft ? p.draft + (int64_t)row * p.draft_stride : nullptr;
+    d[g] = p.draft ? -1 : p.draft_ids[row];
   }
-  const float c1 = exp2_scale(req_temperature(p, r));
-  if (wave_id() < nrows) {
-    float MX, S;
-    if (!wave_row_stats(p.stat_slots + (int64_t)(row0 + wave_id()) * p.nc, p.nc, c1, MX, S) &&
-        lane_id() == 0)
-      atomic_store_relaxed(&p.ctrl[1], 1);
-    if (lane_id() == 0) {
-      s_M[wave_id()] = MX;
-      s_L[wave_id()] = (float)(-log2((double)S));
-    }
-  }
-  __syncthreads();
+  const float* eb = p.noise + (int64_t)r * p.noise_stride;
+  const bool aligned = p.target_aligned && p.noise_aligned && (p.draft_aligned || !p.draft);
+
+  auto load = [&](Buf& buf, int64_t s0, auto fast) {
+    constexpr bool F = decltype(fast)::value;
 #pragma unroll
-  for (int k = 0; k < EPT; ++k) inv[k] = 1.0f / inv[k];
-  uint64_t key[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float bv = -INFINITY;
-    int bi = (int)v0;
-    if (g < nrows) {
-      const float MX = s_M[g];
-      const float nl = s_L[g];
-      const int d = p.draft ? -1 : p.draft_ids[row0 + g];
-#pragma unroll
-      for (int k = 0; k < EPT; ++k) {
-        const int idx = elem_index<DT, EPT>(v0, k);
-        const float prob = __builtin_amdgcn_exp2f(fmaf(x[g][k] - MX, c1, nl));  // softmax
-        const float w = p.draft ? fmaxf(prob - q[g][k], 0.f) : (idx == d ? 0.f : prob);
-        const float score = w * inv[k];
-        // indices rise along k, so a strict compare keeps the first maximum
-        const bool take = (score > bv) & (FAST || idx < vend);
-        bv = take ? score : bv;
-        bi = take ? idx : bi;
+    for (int g = 0; g < G; ++g) {
+      if (g < nrows) {
+        if constexpr (F) load_raw<DT, EPT>(tb[g], s0, buf.x[g]);
+        else load_raw_checked<DT, EPT>(tb[g], s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x[g]);
+        if (p.draft) load_raw_f32<DT, EPT, F>(qb[g], s0, vend, p.draft_aligned, 0.f, buf.q[g]);
       }
     }
-    key[g] = argmax_key(bv, bi);
+    load_raw_f32<DT, EPT, F>(eb, s0, vend, p.noise_aligned, 1.f, buf.e);
+  };
+
+  float MX[G], NL[G];
+  auto wait_stats = [&]() {
+    after_loads();
+    if (wave_id() < nrows) {
+      float mx, sum;
+      if (!wave_row_stats(p.stat_slots + (int64_t)(row0 + wave_id()) * p.nc, p.nc, c1, &p.ctrl[1], mx, sum) &&
+          lane_id() == 0)
+        atomic_store_relaxed(&p.ctrl[1], 1);
+      if (lane_id() == 0) {
+        s_M[wave_id()] = mx;
+        s_L[wave_id()] = (float)(-log2((double)sum));
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      MX[g] = s_M[g];
+      NL[g] = s_L[g];
+    }
+  };
+
+  float bv[G];
+  int bi[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    bv[g] = -INFINITY;
+    bi[g] = (int)v0;
   }
+  auto body = [&](const Buf& buf, int64_t s0, auto fast) {
+    float inv[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) inv[k] = 1.0f / raw_f32(buf.e, k);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (g < nrows) {
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+          const int idx = elem_index<DT, EPT>(s0, k);
+          const float x = raw_elem<DT>(buf.x[g], k);
+          const float prob = __builtin_amdgcn_exp2f(fmaf(x - MX[g], c1, NL[g]));  // softmax
+          const float w = p.draft ? fmaxf(prob - raw_f32(buf.q[g], k), 0.f)
+                                  : (idx == d[g] ? 0.f : prob);
+          const float score = w * inv[k];
+          // columns rise with s0 and k, so a strict compare keeps the first maximum
+          const bool take = (score > bv[g]) & (decltype(fast)::value || idx < vend);
+          bv[g] = take ? score : bv[g];
+          bi[g] = take ? idx : bi[g];
+        }
+      }
+    }
+  };
+  pipeline<kVThreads * EPT, Buf>(v0, vend, aligned, load, body, wait_stats);
+  uint64_t key[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) key[g] = argmax_key(bv[g], bi[g]);
   const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
   if ((int)threadIdx.x < nrows) slot_store(p.arg_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c, best);
 }
 
 // ------------------------------------------------------------------ main kernel ------
-// Tunables (compile-time): elements per thread per row, and an optional cap on waves per SIMD
-// that bounds the register budget (0 = let the compiler choose).
-#ifndef MVSD_VERIFY_EPT
-#define MVSD_VERIFY_EPT 8
+// Tunables (compile-time): elements per thread per row (fp32 targets; 16-bit targets), rows
+// per group, and an optional cap on waves per SIMD that bounds the register budget (0 = let
+// the compiler choose).
+#ifndef MVSD_VERIFY_EPT_F32
+#define MVSD_VERIFY_EPT_F32 4
+#endif
+#ifndef MVSD_VERIFY_EPT_16
+#define MVSD_VERIFY_EPT_16 8
+#endif
+#ifndef MVSD_VERIFY_GROUP
+#define MVSD_VERIFY_GROUP 4
 #endif
 #ifndef MVSD_VERIFY_WAVES_PER_EU
 #define MVSD_VERIFY_WAVES_PER_EU 0
@@ -547,10 +710,49 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, int row0
 #else
 #define MVSD_VERIFY_ATTRS
 #endif
+#ifndef MVSD_FUSED_WAVES_PER_EU
+#define MVSD_FUSED_WAVES_PER_EU 0
+#endif
+#if MVSD_FUSED_WAVES_PER_EU > 0
+#define MVSD_FUSED_ATTRS __attribute__((amdgpu_waves_per_eu(MVSD_FUSED_WAVES_PER_EU, 8)))
+#else
+#define MVSD_FUSED_ATTRS
+#endif
 
-// Ticket t -> step s = t / steps_size: the first nc tickets of step s are the A-chunks (stats,
+// Ticket t -> step s = t / step_size: the first nc tickets of step s are the A-chunks (stats,
 // or the argmax for greedy groups) of group s; when the batch has random requests the next nc
 // are the B-chunks (scores) of group s - lag.  Slots of absent groups are claimed and skipped.
+struct TaskDecode {
+  int total, step_size, nc, lag, groups, two_phase;
+};
+
+// Thread 0: decode ticket t and fetch its group descriptor into dst[0..6]
+// = {t, chunk, valid | phase_b << 1, request, first row, rows | groups << 8 | flags << 16,
+// bits of c1}.
+__device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, int t, int* dst) {
+  int c = 0, flags = 0;
+  int4 d = make_int4(0, 0, 0, 0);
+  if (t < td.total) {
+    const int step = t / td.step_size;
+    const int w = t - step * td.step_size;
+    const bool phase_b = w >= td.nc;
+    c = phase_b ? w - td.nc : w;
+    const int gi = phase_b ? step - td.lag : step;
+    if (gi >= 0 && gi < td.groups) {
+      d = p.grp_desc[gi];
+      const bool full = (d.z >> 16) & kFull;
+      flags = (!phase_b || full ? 1 : 0) | (phase_b ? 2 : 0);
+    }
+  }
+  dst[0] = t;
+  dst[1] = c;
+  dst[2] = flags;
+  dst[3] = d.x;
+  dst[4] = d.y;
+  dst[5] = d.z;
+  dst[6] = d.w;
+}
+
 template <int DT, int EPT, int G>
 __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(VerifyParams p) {
   static_assert(EPT % Elem<DT>::kVec == 0, "EPT must be a multiple of the vector width");
@@ -558,58 +760,61 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   __shared__ uint64_t s_key[G * kVWaves];
   __shared__ float s_M[G];
   __shared__ float s_L[G];
-  __shared__ int s_task;
+  __shared__ int s_info[2][8];  // double-buffered decoded ticket (current, next)
   __shared__ int s_last;
   __shared__ FinalizeSmem fsm;
 
   const int tid = threadIdx.x;
-  const int nc = p.nc;
-  const int lag = p.lag;
-  const int groups = p.grp_off[p.B];
-  const int step_size = p.two_phase ? 2 * nc : nc;
-  const int total = (groups + (p.two_phase ? lag : 0)) * step_size;
+  TaskDecode td;
+  td.nc = p.nc;
+  td.lag = p.lag;
+  td.groups = p.grp_off[p.B];
+  td.two_phase = p.two_phase;
+  td.step_size = p.two_phase ? 2 * td.nc : td.nc;
+  td.total = (td.groups + (p.two_phase ? td.lag : 0)) * td.step_size;
 
-  for (;;) {
-    if (tid == 0) s_task = atomic_add_relaxed(&p.ctrl[0], 1);
-    __syncthreads();
-    const int t = s_task;
-    __syncthreads();
-    if (t >= total) break;
-
-    const int step = t / step_size;
-    const int w = t - step * step_size;
-    const bool phase_b = w >= nc;
-    const int c = phase_b ? w - nc : w;
-    const int gi = phase_b ? step - lag : step;
-    if (gi < 0 || gi >= groups) continue;
-    const int r = p.grp_req[gi];
-    int begin, K;
-    req_range(p, r, begin, K);
-    const int g0 = gi - p.grp_off[r];
-    const int row0 = begin + g0 * G;
-    const int nrows = min(G, K - g0 * G);
-    const int ngr = (K + G - 1) / G;
-    const bool greedy = req_is_greedy(p, r);
-    const bool full = !greedy && p.recovered == nullptr;
-    if (phase_b && !full) continue;
+  // The next ticket is claimed when a task starts and decoded once the task's loads are in
+  // flight, so the atomic and the descriptor fetch overlap with HBM traffic.
+  if (tid == 0) fetch_task(p, td, atomic_add_relaxed(&p.ctrl[0], 1), s_info[0]);
+  __syncthreads();
+  for (int par = 0;; par ^= 1) {
+    const int* info = s_info[par];
+    const int t = info[0];
+    if (t >= td.total) break;
+    int tnext = 0;
+    if (tid == 0) tnext = atomic_add_relaxed(&p.ctrl[0], 1);
+    auto prefetch = [&]() {
+      if (tid == 0) fetch_task(p, td, tnext, s_info[par ^ 1]);
+    };
+    const int tflags = info[2];
+    if (!(tflags & 1)) {
+      prefetch();
+      __syncthreads();
+      continue;
+    }
+    const bool phase_b = tflags & 2;
+    const int c = info[1];
+    const int r = info[3];
+    const int row0 = info[4];
+    const int nrows = info[5] & 0xff;
+    const int ngr = (info[5] >> 8) & 0xff;
+    const int gflags = info[5] >> 16;
+    const float c1 = __int_as_float(info[6]);
+    const bool greedy = gflags & kGreedy;
+    const bool full = gflags & kFull;
     const int64_t v0 = (int64_t)c * p.chunk;
     const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
-    const bool fast = p.target_aligned && vend - v0 == p.chunk &&
-                      (!phase_b || (p.noise_aligned && (p.draft_aligned || !p.draft)));
     if (greedy) {
-      if (fast) task_argmax<DT, EPT, G, true>(p, c, row0, nrows, v0, vend, s_key);
-      else task_argmax<DT, EPT, G, false>(p, c, row0, nrows, v0, vend, s_key);
+      task_argmax<DT, EPT, G>(p, c, row0, nrows, v0, vend, s_key, prefetch);
     } else if (!phase_b) {
-      if (fast) task_stats<DT, EPT, G, true>(p, c, r, row0, nrows, v0, vend, s_red);
-      else task_stats<DT, EPT, G, false>(p, c, r, row0, nrows, v0, vend, s_red);
+      task_stats<DT, EPT, G>(p, c, c1, row0, nrows, v0, vend, s_red, prefetch);
     } else {
-      if (fast) task_scores<DT, EPT, G, true>(p, c, r, row0, nrows, v0, vend, s_key, s_M, s_L);
-      else task_scores<DT, EPT, G, false>(p, c, r, row0, nrows, v0, vend, s_key, s_M, s_L);
+      task_scores<DT, EPT, G>(p, c, r, c1, row0, nrows, v0, vend, s_key, s_M, s_L, prefetch);
     }
     // ---- request completion: the last counted task runs the accept/reject chain ----
     // (counted: B-tasks of full random requests, A-tasks otherwise)
     if (full == phase_b) {
-      if (tid == 0) s_last = atomic_add_relaxed(&p.req_cnt[r], 1) == ngr * nc - 1;
+      if (tid == 0) s_last = atomic_add_relaxed(&p.req_cnt[r], 1) == ngr * td.nc - 1;
       __syncthreads();
       if (s_last) finalize_request(p, r, greedy, full, fsm);
     }
@@ -617,17 +822,406 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   }
 
   // The last workgroup out (every other one has made its final claim and finished reading
-  // grp_off / grp_req) returns the group tables, ticket and exit counter to zero, so the whole
-  // workspace is zero again whatever layout the next call uses.
+  // grp_off / grp_desc) returns the group tables, ticket and exit counter to zero, so the
+  // whole workspace is zero again whatever layout the next call uses.
   if (tid == 0) s_last = atomic_add_relaxed(&p.ctrl[2], 1) == (int)gridDim.x - 1;
   __syncthreads();
   if (s_last) {
     for (int i = tid; i <= p.B; i += kVThreads) p.grp_off[i] = 0;
-    for (int i = tid; i < groups; i += kVThreads) p.grp_req[i] = 0;
+    for (int i = tid; i < td.groups; i += kVThreads) p.grp_desc[i] = make_int4(0, 0, 0, 0);
     if (tid == 0) {
       atomic_store_relaxed(&p.ctrl[0], 0);
       atomic_store_relaxed(&p.ctrl[2], 0);
     }
+  }
+}
+
+// ------------------------------------------------------------------ fused kernel -----
+// Single-read kernel for batches that need recovered scores.  One task per (group, chunk)
+// with a chunk of exactly kVThreads * EPT columns; workgroup w takes tasks w, w + grid,
+// w + 2 grid, ... (static assignment, no ticket atomics).  Iteration i of a workgroup:
+//   1. issues the stats-slot loads of task i-L's rows (L = kLag), then task i's target chunk
+//      and task i-L's draft / noise chunks;
+//   2. reduces task i's target chunk into per-row stats (or the argmax for greedy groups),
+//      publishes them and parks the chunk in LDS;
+//   3. scores task i-L (target from LDS) against its group's combined stats and publishes
+//      the chunk-local recovered candidate.
+// Every input byte is read once.  Latency is hidden by running several small workgroups per
+// CU; within a workgroup the loads of one iteration are issued together, with the polls
+// first so that waiting for them never waits for the data loads.  Loads are unconditional
+// 16-byte loads (rows past a group's end and absent tasks load duplicates of valid
+// addresses), so every path issues the same loads and the in-order load counters stay exact.
+//
+// Progress: scoring task i-L waits for the stats of its group, whose tasks t' satisfy
+// t' <= t_{i-L} + nc - 1 < t_{i-L} + grid when grid >= nc, so they belong to iterations
+// <= i-L+1 <= i of their workgroups and are published in step 2 before any wait there.
+// Ordering events by (iteration, step), every wait is on an earlier event, hence no cycle,
+// provided all workgroups are resident: the host launches at most the resident capacity and
+// only when it is >= nc.
+
+constexpr int kRing = 64;  // task descriptors cached per workgroup (LDS ring)
+#ifndef MVSD_FUSED_LAG
+#define MVSD_FUSED_LAG 2
+#endif
+// Iterations between a task's stats step and its score step: its group's other chunks are
+// reduced by other workgroups in the same iteration, and the lag gives the slowest of them
+// time to publish before the scores need the combined stats.
+constexpr int kLag = MVSD_FUSED_LAG;
+static_assert(kLag >= 1 && kLag < kRing / 2, "lag must fit the descriptor ring");
+
+template <int DT, int EPT, int G>
+struct FusedBuf {
+  u32x4 x[G][EPT / Elem<DT>::kVec];  // target chunk of task i
+  u32x4 q[G][EPT / 4];               // draft chunk of task i-L
+  u32x4 e[EPT / 4];                  // noise chunk of task i-L
+};
+
+struct FusedTask {
+  int c;      // chunk, or -1 when absent
+  int r;      // request
+  int row0;   // first verify row
+  int nrows;  // rows in the group
+  int ngr;    // groups of the request
+  int flags;  // kGreedy | kFull
+  float c1;   // log2(e) / T
+};
+
+// Per-workgroup LDS ring of task descriptors and target-row indices, so that issuing an
+// iteration's loads never waits on a descriptor load.
+template <int G>
+struct TaskRing {
+  int4 d[kRing];
+  float c1[kRing];
+  int trow[kRing][G];
+};
+
+template <int G>
+__device__ inline FusedTask ring_task(const TaskRing<G>& ring, int i) {
+  const int4 a = ring.d[i % kRing];
+  FusedTask t;
+  t.c = a.x;
+  t.r = a.y;
+  t.row0 = a.z;
+  t.nrows = a.w & 0xff;
+  t.ngr = (a.w >> 8) & 0xff;
+  t.flags = a.w >> 16;
+  t.c1 = ring.c1[i % kRing];
+  return t;
+}
+
+// Wave 0 fills the entries of iterations [i0, i0 + n) (n <= 64) of this workgroup.
+template <int G>
+__device__ inline void ring_fill(const VerifyParams& p, TaskRing<G>& ring, int i0, int n, int total) {
+  const int lane = lane_id();
+  if (wave_id() == 0 && lane < n) {
+    const int i = i0 + lane;
+    const int64_t t = (int64_t)blockIdx.x + (int64_t)i * gridDim.x;
+    int4 a = make_int4(-1, 0, 0, 1 | 1 << 8);
+    float c1 = 1.f;
+    if (t < total) {
+      const int gi = (int)(t / p.nc);
+      const int4 d = p.grp_desc[gi];
+      a = make_int4((int)(t - (int64_t)gi * p.nc), d.x, d.y, d.z);
+      c1 = __int_as_float(d.w);
+    }
+    const int slot = i % kRing;
+    ring.d[slot] = a;
+    ring.c1[slot] = c1;
+    const int nrows = a.w & 0xff;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      ring.trow[slot][g] = a.x < 0 ? 0 : (int)target_row(p, a.z + min(g, nrows - 1));
+  }
+}
+
+template <int DT, int EPT, int G, bool HAS_DRAFT>
+__global__ __launch_bounds__(kVThreads) MVSD_FUSED_ATTRS void verify_fused_kernel(VerifyParams p) {
+  static_assert(EPT % Elem<DT>::kVec == 0, "EPT must be a multiple of the vector width");
+  using S = typename Elem<DT>::storage;
+  constexpr int NV = EPT / Elem<DT>::kVec;
+  constexpr int N32 = EPT / 4;
+  constexpr int R = 4;  // stats slots per lane held from one poll (nc <= 256 on the fast path)
+  __shared__ u32x4 s_x[kLag + 1][G][NV][kVThreads];  // parked target chunks
+  __shared__ TaskRing<G> s_ring;
+  __shared__ float s_red[G * kVWaves];
+  __shared__ uint64_t s_key[G * kVWaves];
+  __shared__ float s_M[G];
+  __shared__ float s_L[G];
+  __shared__ int s_last;
+  __shared__ FinalizeSmem fsm;
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wid = wave_id();
+  const int nc = p.nc;
+  const int total = p.grp_off[p.B] * nc;
+  const S* target = static_cast<const S*>(p.target);
+
+  ring_fill<G>(p, s_ring, 0, kRing, total);
+  __syncthreads();
+  // tasks of this workgroup: blockIdx.x + k * grid < total
+  const int n_iter = (int)((total - (int64_t)blockIdx.x + gridDim.x - 1) / gridDim.x);
+
+  // Loads of an iteration's data: target chunk of task tx, draft / noise of task tq.
+  // Every load is an unconditional 16-byte load at a clamped in-bounds address (the host
+  // uses this kernel only for aligned rows with V a multiple of the vector width); absent
+  // tasks and rows past a group's end load duplicates.  Columns past vend are masked where
+  // the data is consumed.
+  auto issue = [&](FusedBuf<DT, EPT, G>& b, const FusedTask& tx, int ix, const FusedTask& tq) {
+    {
+      const int64_t v0 = tx.c < 0 ? 0 : (int64_t)tx.c * p.chunk;
+      const int64_t vlast = min((int64_t)p.V, v0 + p.chunk) - Elem<DT>::kVec;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const S* base = target + (int64_t)s_ring.trow[ix % kRing][g] * p.target_stride;
+#pragma unroll
+        for (int n = 0; n < NV; ++n)
+          b.x[g][n] = load_target16(base + min(vec_col<DT>(v0, n), vlast));
+      }
+    }
+    {
+      const bool absent = tq.c < 0 || !(tq.flags & kFull);
+      const int64_t v0 = absent ? 0 : (int64_t)tq.c * p.chunk;
+      const int64_t vlast = min((int64_t)p.V, v0 + p.chunk) - 4;
+      constexpr int VEC = Elem<DT>::kVec;
+      if constexpr (HAS_DRAFT) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float* base = p.draft + (int64_t)(absent ? 0 : tq.row0 + min(g, tq.nrows - 1)) * p.draft_stride;
+#pragma unroll
+          for (int m = 0; m < N32; ++m)
+            b.q[g][m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                base + min(vec_col<DT>(v0, m / (VEC / 4)) + (m % (VEC / 4)) * 4, vlast)));
+        }
+      }
+      const float* eb = p.noise + (int64_t)(absent ? 0 : tq.r) * p.noise_stride;
+#pragma unroll
+      for (int m = 0; m < N32; ++m)
+        b.e[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            eb + min(vec_col<DT>(v0, m / (VEC / 4)) + (m % (VEC / 4)) * 4, vlast)));
+    }
+  };
+
+  // Deferred request-completion counts (one from the stats / argmax step, one from the score
+  // step): each atomic's result is examined one iteration later.
+  struct Pending {
+    int cnt, r, target, greedy, full;
+  };
+  Pending pa{0, -1, 0, 0, 0}, pb{0, -1, 0, 0, 0};
+  auto settle_one = [&](Pending& pd) {
+    if (pd.r >= 0) {
+      if (tid == 0) s_last = pd.cnt == pd.target - 1;
+      __syncthreads();
+      if (s_last) finalize_request(p, pd.r, pd.greedy, pd.full, fsm);
+      __syncthreads();
+      pd.r = -1;
+    }
+  };
+  auto count = [&](Pending& pd, const FusedTask& t, bool greedy, bool full) {
+    if (tid == 0) pd.cnt = atomic_add_relaxed(&p.req_cnt[t.r], 1);
+    pd.r = t.r;
+    pd.target = t.ngr * nc;
+    pd.greedy = greedy;
+    pd.full = full;
+  };
+
+  // One iteration (task i's stats, task i-L's scores).  Returns false when this workgroup is
+  // done.
+  auto iteration = [&](int i) -> bool {
+    if (i >= n_iter + kLag) return false;
+    FusedTask tp = ring_task<G>(s_ring, i + kRing - kLag);  // task i - kLag
+    const FusedTask tc = ring_task<G>(s_ring, i);
+    const bool b_live = i >= kLag && tp.c >= 0 && (tp.flags & kFull);
+    if (!b_live) tp.c = -1;
+    FusedBuf<DT, EPT, G> cur;
+
+    // ---- 1. stats-slot polls and draft ids for task i - kLag, then this iteration's data ----
+    uint64_t pv[R];
+    int dp[G];
+    {
+      if (b_live && wid < tp.nrows) {
+        const uint64_t* slots = p.stat_slots + (int64_t)(tp.row0 + wid) * nc;
+#pragma unroll
+        for (int j = 0; j < R; ++j) pv[j] = slot_load(slots + min(lane + j * kWave, nc - 1));
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        dp[g] = HAS_DRAFT ? -1 : p.draft_ids[b_live ? tp.row0 + min(g, tp.nrows - 1) : 0];
+    }
+    issue(cur, tc, i, tp);
+    settle_one(pa);
+    settle_one(pb);
+    // Ring refill at i = 32 k + kLag (k >= 1): entries [32 k + 32, 32 k + 64) replace
+    // entries [32 k - 32, 32 k), all older than the oldest one still needed (i - kLag).
+    if (i >= kRing / 2 + kLag && (i - kLag) % (kRing / 2) == 0) {
+      __syncthreads();
+      ring_fill<G>(p, s_ring, i - kLag + kRing / 2, kRing / 2, total);
+    }
+
+    // ---- 2. task i: stats (or greedy argmax), park the chunk in LDS ----
+    if (tc.c >= 0) {
+      const int64_t v0 = (int64_t)tc.c * p.chunk;
+      const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
+      const bool greedy = tc.flags & kGreedy;
+      const bool full = tc.flags & kFull;
+      // target value k of row g, -inf past vend (FAST: the chunk is full)
+      auto xval = [&](int g, int k, auto fast) {
+        const float v = raw_elem<DT>(cur.x[g], k);
+        if constexpr (decltype(fast)::value) return v;
+        else return elem_index<DT, EPT>(v0, k) < vend ? v : -INFINITY;
+      };
+      auto reduce = [&](auto fast) {
+        if (greedy) {
+          uint64_t key[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float bv = -INFINITY;
+            int bi = (int)v0;
+            if (g < tc.nrows) {
+#pragma unroll
+              for (int k = 0; k < EPT; ++k) {
+                const float v = xval(g, k, fast);
+                const bool take = (v > bv) | ((v != v) & (bv == bv));
+                bv = take ? v : bv;
+                bi = take ? elem_index<DT, EPT>(v0, k) : bi;
+              }
+            }
+            key[g] = argmax_key(bv, bi);
+          }
+          const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
+          if (tid < tc.nrows) slot_store(p.arg_slots + (int64_t)(tc.row0 + tid) * nc + tc.c, best);
+        } else {
+          float M[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float mm = -INFINITY;
+            if (g < tc.nrows) {
+#pragma unroll
+              for (int k = 0; k < EPT; ++k) mm = fmaxf(mm, xval(g, k, fast));
+            }
+            M[g] = mm;
+          }
+          block_max<G, kVWaves>(M, s_red);
+          float sm[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float ref = M[g] == -INFINITY ? 0.f : M[g];
+            float acc = 0.f;
+            if (g < tc.nrows) {
+#pragma unroll
+              for (int k = 0; k < EPT; ++k)
+                acc += __builtin_amdgcn_exp2f((xval(g, k, fast) - ref) * tc.c1);
+            }
+            sm[g] = acc;
+          }
+          const float srow = block_sum_to_row_thread<G, kVWaves>(sm, s_red);
+          if (tid < tc.nrows) {
+            const float mrow = row_of_thread<G>(M);
+            slot_store(p.stat_slots + (int64_t)(tc.row0 + tid) * nc + tc.c,
+                       pack_stats(mrow, mrow == -INFINITY ? 0.f : srow));
+          }
+        }
+      };
+      if (vend - v0 == p.chunk) reduce(Fast<true>());
+      else reduce(Fast<false>());
+      if (full) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int n = 0; n < NV; ++n) s_x[i % (kLag + 1)][g][n][tid] = cur.x[g][n];
+      }
+      if (!full) count(pa, tc, greedy, false);
+    }
+
+    // ---- 3. task i - kLag: recovered-token scores ----
+    if (b_live) {
+      if (wid < tp.nrows) {
+        bool ready = true;
+#pragma unroll
+        for (int j = 0; j < R; ++j) ready &= pv[j] != 0;
+        float mx, sum;
+        if (__all(ready) && nc <= R * kWave) {
+          float m = -INFINITY;
+#pragma unroll
+          for (int j = 0; j < R; ++j)
+            if (lane + j * kWave < nc) m = fmaxf(m, unpack_stats(pv[j]).x);
+          mx = wave_max(m);
+          float acc = 0.f;
+#pragma unroll
+          for (int j = 0; j < R; ++j) {
+            const float2 st = unpack_stats(pv[j]);
+            if (lane + j * kWave < nc && st.x != -INFINITY)
+              acc += st.y * exp2f((st.x - mx) * tp.c1);
+          }
+          sum = wave_sum(acc);
+        } else if (!wave_row_stats(p.stat_slots + (int64_t)(tp.row0 + wid) * nc, nc, tp.c1, &p.ctrl[1], mx, sum) &&
+                   lane == 0) {
+          atomic_store_relaxed(&p.ctrl[1], 1);
+        }
+        if (lane == 0) {
+          s_M[wid] = mx;
+          s_L[wid] = (float)(-log2((double)sum));
+        }
+      }
+      __syncthreads();
+      const int64_t v0 = (int64_t)tp.c * p.chunk;
+      const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
+      float inv[EPT];
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) inv[k] = 1.0f / raw_f32(cur.e, k);
+      uint64_t key[G];
+      auto score_rows = [&](auto fast) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float bv = -INFINITY;
+          int bi = (int)v0;
+          if (g < tp.nrows) {
+            const float MX = s_M[g];
+            const float NL = s_L[g];
+            const int d = dp[g];
+            u32x4 xr[NV];
+#pragma unroll
+            for (int n = 0; n < NV; ++n) xr[n] = s_x[(i - kLag) % (kLag + 1)][g][n][tid];
+#pragma unroll
+            for (int k = 0; k < EPT; ++k) {
+              const int idx = elem_index<DT, EPT>(v0, k);
+              const float prob = __builtin_amdgcn_exp2f(fmaf(raw_elem<DT>(xr, k) - MX, tp.c1, NL));
+              float w;
+              if constexpr (HAS_DRAFT) w = fmaxf(prob - raw_f32(cur.q[g], k), 0.f);
+              else w = idx == d ? 0.f : prob;
+              const float score = w * inv[k];
+              // columns rise with k, so a strict compare keeps the first maximum
+              bool take = score > bv;
+              if constexpr (!decltype(fast)::value) take &= idx < vend;
+              bv = take ? score : bv;
+              bi = take ? idx : bi;
+            }
+          }
+          key[g] = argmax_key(bv, bi);
+        }
+      };
+      if (vend - v0 == p.chunk) score_rows(Fast<true>());
+      else score_rows(Fast<false>());
+      const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
+      if (tid < tp.nrows) slot_store(p.arg_slots + (int64_t)(tp.row0 + tid) * nc + tp.c, best);
+      count(pb, tp, false, true);
+    }
+    __syncthreads();
+    return true;
+  };
+
+  for (int i = 0; iteration(i); ++i) {
+  }
+  settle_one(pa);
+  settle_one(pb);
+
+  // The last workgroup out returns the group tables and exit counter to zero.
+  if (tid == 0) s_last = atomic_add_relaxed(&p.ctrl[2], 1) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (s_last) {
+    for (int i = tid; i <= p.B; i += kVThreads) p.grp_off[i] = 0;
+    for (int i = tid; i < total / nc; i += kVThreads) p.grp_desc[i] = make_int4(0, 0, 0, 0);
+    if (tid == 0) atomic_store_relaxed(&p.ctrl[2], 0);
   }
 }
 
@@ -647,49 +1241,62 @@ hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream) {
 }
 
 // ------------------------------------------------------------------ dispatch ---------
-constexpr int kEpt = MVSD_VERIFY_EPT;
-constexpr int kGroup = 4;
+constexpr int kGroup = MVSD_VERIFY_GROUP;
+template <int DT>
+constexpr int ept_of() {
+  return DT == MVSD_F32 ? MVSD_VERIFY_EPT_F32 : MVSD_VERIFY_EPT_16;
+}
+#ifndef MVSD_VERIFY_TASKS_PER_WG
+#define MVSD_VERIFY_TASKS_PER_WG 16
+#endif
 
-VerifyPlan verify_plan(int target_dtype, int64_t vocab_size) {
+VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int phases, int cap) {
   VerifyPlan plan;
-  plan.ept = kEpt;
+  plan.ept = target_dtype == MVSD_F32 ? ept_of<MVSD_F32>() : ept_of<MVSD_BF16>();
   plan.g = kGroup;
-  plan.chunk = kVThreads * plan.ept;
+  plan.sub = kVThreads * plan.ept;
+  plan.nsub = (int)((vocab_size + plan.sub - 1) / plan.sub);
+  // Chunks per row: enough tasks for about MVSD_VERIFY_TASKS_PER_WG per resident workgroup,
+  // each task as long as possible (fewer ticket claims, longer load pipelines).
+  int64_t nc = plan.nsub;
+  if (groups > 0 && cap > 0) {
+    nc = ((int64_t)MVSD_VERIFY_TASKS_PER_WG * cap + phases * groups - 1) / (phases * groups);
+    if (const char* env = getenv("MVSD_VERIFY_NC")) nc = atoi(env);
+    nc = nc < 1 ? 1 : (nc > plan.nsub ? plan.nsub : nc);
+  }
+  const int64_t subs_per_chunk = (plan.nsub + nc - 1) / nc;
+  plan.chunk = (int)(subs_per_chunk * plan.sub);
   plan.nc = (int)((vocab_size + plan.chunk - 1) / plan.chunk);
-  (void)target_dtype;
   return plan;
 }
 
-const void* verify_kernel_ptr(int target_dtype) {
+template <int DT>
+const void* kernel_for(bool fused, bool has_draft) {
+  constexpr int E = ept_of<DT>();
+  if (!fused) return reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup>);
+  return has_draft ? reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, true>)
+                   : reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, false>);
+}
+
+const void* verify_kernel_ptr(int target_dtype, bool fused, bool has_draft) {
   switch (target_dtype) {
-    case MVSD_F32: return reinterpret_cast<const void*>(&verify_kernel<MVSD_F32, kEpt, kGroup>);
-    case MVSD_BF16: return reinterpret_cast<const void*>(&verify_kernel<MVSD_BF16, kEpt, kGroup>);
-    case MVSD_F16: return reinterpret_cast<const void*>(&verify_kernel<MVSD_F16, kEpt, kGroup>);
+    case MVSD_F32: return kernel_for<MVSD_F32>(fused, has_draft);
+    case MVSD_BF16: return kernel_for<MVSD_BF16>(fused, has_draft);
+    case MVSD_F16: return kernel_for<MVSD_F16>(fused, has_draft);
     default: return nullptr;
   }
 }
 
-hipError_t launch_verify(const VerifyParams& params, int target_dtype, int grid,
+hipError_t launch_verify(const VerifyParams& params, int target_dtype, bool fused, int grid,
                          hipStream_t stream) {
   hipLaunchKernelGGL(verify_init_kernel, dim3(1), dim3(1024), 0, stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.P == 0) return err;
-  switch (target_dtype) {
-    case MVSD_F32:
-      hipLaunchKernelGGL((verify_kernel<MVSD_F32, kEpt, kGroup>), dim3(grid), dim3(kVThreads), 0,
-                         stream, params);
-      break;
-    case MVSD_BF16:
-      hipLaunchKernelGGL((verify_kernel<MVSD_BF16, kEpt, kGroup>), dim3(grid), dim3(kVThreads), 0,
-                         stream, params);
-      break;
-    case MVSD_F16:
-      hipLaunchKernelGGL((verify_kernel<MVSD_F16, kEpt, kGroup>), dim3(grid), dim3(kVThreads), 0,
-                         stream, params);
-      break;
-    default:
-      return hipErrorInvalidValue;
-  }
+  const void* fn = verify_kernel_ptr(target_dtype, fused, params.draft != nullptr);
+  if (!fn) return hipErrorInvalidValue;
+  void* args[] = {const_cast<VerifyParams*>(&params)};
+  err = hipLaunchKernel(fn, dim3(grid), dim3(kVThreads), args, 0, stream);
+  if (err != hipSuccess) return err;
   return hipGetLastError();
 }
 

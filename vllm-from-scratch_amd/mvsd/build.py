@@ -5,6 +5,9 @@ file.  Flags:
   * ``-fhip-fp32-correctly-rounded-divide-sqrt``: IEEE fp32 division, so the temperature
     divide and ``p / q`` round like the reference's fp32 arithmetic;
   * ``-Xclang -target-feature -Xclang -packed-fp32-ops``: no packed-FP32 VALU instructions;
+  * ``-mllvm -amdgpu-atomic-optimizer-strategy=None``: single-lane counter atomics stay plain
+    atomics whose results are waited for where they are used, instead of being rewritten
+    into a wave reduction that waits for the result (and every older load) at once;
   * no fast-math.
 
 Run ``python -m mvsd.build`` (from ``vllm-from-scratch_amd/``) or call :func:`build`.
@@ -34,6 +37,7 @@ HIPCC_FLAGS = [
     "-shared",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall",
     "-Wno-unused-function",
 ]
