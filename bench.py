@@ -2,11 +2,17 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config h|c1|c2|c3|c4|c5]
 
-A step is one ``rejection_sample`` call (one fused HIP launch plus its small init launch) over
-the whole batch, inputs already resident in HBM; the default workload is the headline
-configuration (B=256, k=4, V=151936, fp32 target logits and draft probs, random T=0.8).
-Prints ONE JSON line: value = achieved GB/s (algorithmic bytes per step / step time), with
-verified tokens/s, the roofline object and a host-CPU baseline of the oracle.
+A step is one ``rejection_sample`` call (the persistent verify kernel plus its small init
+kernel) over the whole batch, inputs already resident in HBM; the default workload is the
+headline configuration (B=256, k=4, V=151936, fp32 target logits and draft probs, random
+T=0.8).  Prints ONE JSON line: value = achieved GB/s (algorithmic bytes per step / step time
+over the timed region), with verified tokens/s, the roofline object (kernel time from HIP
+events recorded around every launch on the launch stream) and a host-CPU baseline of the
+oracle on a bounded sample.
+
+``--pmc-driver`` runs a 1 GiB device copy (the calibration kernel for rocprofv3 counters)
+followed by a few headline steps, and prints nothing else; profiles/ records the rocprofv3
+commands that use it.
 """
 
 from __future__ import annotations
@@ -27,7 +33,7 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "verify_kernel_headline_traffic.md"
 
 
 def parse_args():
@@ -36,9 +42,11 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="h", choices=["h", "c1", "c2", "c3", "c4", "c5"])
-    ap.add_argument("--cpu-sample", type=int, default=None,
-                    help="requests in the CPU-baseline sample (default: sized to ~10-20 s)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="minimum CPU time of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-driver", action="store_true",
+                    help="run the counter-calibration copy and a few steps, print nothing")
     return ap.parse_args()
 
 
@@ -66,20 +74,25 @@ def run_step(w):
 
 
 def time_steps(step, steps, warmup):
+    """Time `steps` calls after `warmup` untimed ones.  Returns (ms per step over the whole
+    timed region, mean ms between the events recorded right before and after each call, wall
+    ms per step, last output).  All events are recorded on the current stream, the stream the
+    kernels are launched on."""
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(2 * steps)]
     t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(steps):
+    for i in range(steps):
+        marks[2 * i].record(stream)
         out = step()
-    end.record(stream)
+        marks[2 * i + 1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return start.elapsed_time(end) / steps, wall / steps * 1e3, out
+    total = marks[0].elapsed_time(marks[-1]) / steps
+    per_launch = float(np.mean([marks[2 * i].elapsed_time(marks[2 * i + 1]) for i in range(steps)]))
+    return total, per_launch, wall / steps * 1e3, out
 
 
 def accept_histogram(outputs, num_draft_tokens, max_k):
@@ -90,54 +103,56 @@ def accept_histogram(outputs, num_draft_tokens, max_k):
     return hist
 
 
-def cpu_baseline(w, sample_requests):
-    """Time the CPU oracle (torch CPU, all host threads) on the first `sample_requests`
-    requests of the same workload; returns GB/s over that sample's algorithmic bytes."""
+def cpu_baseline(w, min_seconds):
+    """Time the CPU oracle (oracle/rejection.py on torch-CPU, all host threads) over the whole
+    workload, repeated until at least `min_seconds` of CPU work; returns GB/s over the
+    algorithmic bytes processed."""
     from mvsd.testing import configs
     from oracle import rejection as orc
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    ks = w.num_draft_tokens[:sample_requests]
-    P = int(sum(ks))
-    rows = (w.target_rows[:P].long() if w.target_rows is not None else torch.arange(P,
-                                                                                   device=w.target_logits.device))
-    tl = w.target_logits[rows].cpu()
-    dp = None if w.draft_probs is None else w.draft_probs[:P].cpu()
-    noise = None if w.exp_noise is None else w.exp_noise[:len(ks)].cpu()
-    u = None if w.uniforms is None else w.uniforms[:P].cpu()
-    temp = None if w.temperature is None else w.temperature[:len(ks)].cpu()
-    ids = w.draft_token_ids[:P].cpu()
-    bonus = w.bonus_token_ids[:len(ks)].cpu()
+    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    ks = w.num_draft_tokens
+    rows = w.target_rows.long() if w.target_rows is not None else None
+    tl = (w.target_logits if rows is None else w.target_logits[rows]).cpu()
+    dp = None if w.draft_probs is None else w.draft_probs.cpu()
+    noise = None if w.exp_noise is None else w.exp_noise.cpu()
+    u = None if w.uniforms is None else w.uniforms.cpu()
+    temp = None if w.temperature is None else w.temperature.cpu()
+    ids = w.draft_token_ids.cpu()
+    bonus = w.bonus_token_ids.cpu()
 
     def run():
         return orc.rejection_sample(ids, ks, w.max_spec_len, dp, tl, bonus, temperature=temp,
                                     all_greedy=w.all_greedy, uniforms=u, exp_noise=noise,
                                     apply_temperature=w.apply_temperature)
 
-    run()
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
+    run()  # warm-up
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
         run()
-        times.append(time.perf_counter() - t0)
-    sec = float(np.median(times))
-    sub = configs.Workload(w.name, ks, w.max_spec_len, ids, w.cu_num_draft_tokens[:len(ks)],
-                           tl, None, dp, bonus, temp, w.all_greedy, w.all_random, u, noise)
-    nbytes = configs.algorithmic_bytes(sub)
-    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"first {len(ks)} of {w.batch_size} requests ({P} verify rows, V={w.vocab_size}) "
-                      f"of the same workload through oracle/rejection.py on torch-CPU; median of 3 "
-                      f"runs, {sec:.2f} s each; {nbytes} algorithmic bytes",
-            "seconds": round(sec, 3)}
+        reps += 1
+        sec = time.perf_counter() - t0
+        if sec >= min_seconds:
+            break
+    nbytes = configs.algorithmic_bytes(w) * reps
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"the whole workload ({w.batch_size} requests, {w.num_tokens} verify rows, "
+                      f"V={w.vocab_size}) through oracle/rejection.py on torch-CPU, {reps} "
+                      f"back-to-back runs in {sec:.1f} s after one warm-up; inputs in host "
+                      f"memory, same uniforms and noise as the GPU run",
+            "seconds": round(sec, 2)}
 
 
 def load_traffic(config):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (a line ``traffic_bytes_per_launch[<config>] = N``), or None."""
     if TRAFFIC_FILE.exists():
-        data = json.loads(TRAFFIC_FILE.read_text())
-        entry = data.get(config)
-        if entry:
-            return entry.get("bytes_per_launch")
+        key = f"traffic_bytes_per_launch[{config}] = "
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith(key):
+                return int(line[len(key):].strip())
     return None
 
 
@@ -153,7 +168,7 @@ def bench_ngram(args, device):
     def step():
         return ngram_propose_device(tokens, lens, min_n=2, max_n=5, k=5)
 
-    ms, wall_ms, (d, v) = time_steps(step, args.steps, args.warmup)
+    ms, _, wall_ms, (d, v) = time_steps(step, args.steps, args.warmup)
     nbytes = B * L * 4 + B * 4 + B * 5 * 4 + B * 4
     tn, ln = tokens.cpu().numpy(), lens.cpu().numpy()
     t0 = time.perf_counter()
@@ -189,11 +204,22 @@ def main():
 
     w = make_workload(args.config, device)
     step = run_step(w)
-    ms, wall_ms, out = time_steps(step, args.steps, args.warmup)
+    if args.pmc_driver:
+        a = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=device)  # 1 GiB
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        return
+    ms, launch_ms, wall_ms, out = time_steps(step, args.steps, args.warmup)
     nbytes = configs.algorithmic_bytes(w)
     outputs, _ = RejectionSampler.parse_output(out, w.vocab_size)
     tokens = sum(len(o) for o in outputs)
     gbs = nbytes / (ms / 1e3) / 1e9
+    kernel_gbs = nbytes / (launch_ms / 1e3) / 1e9
     hist = accept_histogram(outputs, w.num_draft_tokens, w.max_spec_len)
     line = {
         "metric": "rejection-sampler HBM GB/s (% of peak) + verified tok/s, B=256 k=4 V=152k",
@@ -219,14 +245,15 @@ def main():
         "verified_tokens_per_step": tokens,
         "accept_length_hist": hist,
         "wall_ms_per_step": round(wall_ms, 5),
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic(args.config)},
+        "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic(args.config),
+                     "kernel": "mvsd::verify_kernel (+ verify_init_kernel) per rejection_sample",
+                     "kernel_ms": round(launch_ms, 5)},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        sample = args.cpu_sample or max(1, min(w.batch_size, 48 * 4 // max(w.max_spec_len, 1)))
-        line["cpu_baseline"] = cpu_baseline(w, sample)
+        line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
 
