@@ -9,11 +9,13 @@ Same public names, signatures, dtypes and error behaviour as the reference modul
     apply_sampling_constraints / expand_batch_to_tokens / generate_uniform_probs /
     sample_recovered_tokens, PLACEHOLDER_TOKEN_ID, GREEDY_TEMPERATURE, MAX_SPEC_LEN
 
-The arithmetic is one fused HIP launch (``mvsd_rejection_sample`` in include/mvsd.h): target
-softmax statistics, greedy argmax, exponential-race recovered tokens, acceptance chain and
-bonus emission, reading each target / draft / noise element once.  ``RejectionSampler.forward``
-also folds the gather of verify rows and the temperature divide into that launch when no
-logits processor or top-k/top-p needs the processed logits.
+The arithmetic is one persistent HIP launch (``mvsd_rejection_sample`` in include/mvsd.h,
+after a one-block init launch): target softmax statistics, greedy argmax, exponential-race
+recovered tokens, acceptance chain and bonus emission, reading each draft / noise element once
+and each target element once per phase (statistics, then scores; the single-read variant is
+selected with MVSD_VERIFY_MODE=fused).  ``RejectionSampler.forward`` also folds the gather of
+verify rows and the temperature divide into that launch when no logits processor or
+top-k/top-p needs the processed logits.
 
 Randomness is drawn by the same seams as the reference, and both stay monkeypatchable:
 ``generate_uniform_probs`` (fp64 [P]) and the exponential noise of
