@@ -164,6 +164,20 @@ int mvsd_sample_recovered_tokens(int32_t* recovered_token_ids, const int32_t* cu
                                  int64_t vocab_size, int64_t max_spec_len, mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
+/* apply_top_k_top_p — mask non-candidate logits to -inf, in place.                        */
+/* Replaces: apply_top_k_top_p, minivllm/sample/ops/topk_topp_sampler.py:48-79, as called  */
+/*           by apply_sampling_constraints (minivllm/sample/rejection_sampler.py:563-571). */
+/* logits: fp32 rows at logits + r * logits_stride.  top_k [num_rows] int64 (NULL = none):  */
+/* keep values >= the k-th largest (ties kept); k <= 0 or k >= V keeps the whole row.       */
+/* top_p [num_rows] fp32 (NULL = none): over the top-k-masked row, mask the ascending       */
+/* (value, then index) prefix whose cumulative softmax mass is <= 1 - p, never the largest  */
+/* entry; p > 1 masks nothing.  Requires 1 <= V < 2^31.                                    */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_apply_top_k_top_p(float* logits, int64_t logits_stride, const int64_t* top_k,
+                           const float* top_p, int64_t num_rows, int64_t vocab_size,
+                           mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
 /* ngram_propose — prompt-lookup drafts for a batch of int32 token histories.            */
 /* Replaces: NgramGPUKernel._find_first_and_extract_all_n_parallel + forward             */
 /*           (minivllm/spec_decode/ngram_proposer_gpu.py:56-148) with the in-place       */

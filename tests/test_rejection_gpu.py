@@ -142,6 +142,18 @@ def test_greedy_argmax_at_every_position(device, dtype, V):
     assert got == logits.float().argmax(-1).cpu().tolist()
 
 
+def test_greedy_argmax_treats_signed_zeros_as_equal(device):
+    """-0.0 == +0.0 for torch.argmax: the first of them is the argmax."""
+    logits = torch.tensor([[-1.0, -0.0, 0.0, -2.0], [-3.0, 0.0, -0.0, -0.0]], device=device)
+    drafts = [[3], [3]]
+    meta = make_metadata(drafts, device=device)
+    out = rs.rejection_sample(meta.draft_token_ids, meta.num_draft_tokens, 1,
+                              meta.cu_num_draft_tokens, None, logits,
+                              torch.full((2, 1), 7, dtype=torch.int32, device=device),
+                              sm_for([0.0, 0.0], drafts, device))
+    assert out[:, 0].cpu().tolist() == [1, 1] == logits.argmax(-1).cpu().tolist()
+
+
 def test_expand_kats(device):
     for case in KATS["expand"]:
         x = torch.tensor(case["x"], device=device)

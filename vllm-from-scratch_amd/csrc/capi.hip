@@ -10,6 +10,7 @@
 
 #include "mvsd_device.h"
 #include "rows.h"
+#include "topk.h"
 #include "verify.h"
 
 namespace {
@@ -274,6 +275,17 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
     grid = (int)(tasks < cap ? tasks : cap);
   }
   return hip_status(mvsd::launch_verify(p, a->target_dtype, fused, grid, (hipStream_t)stream));
+}
+
+int mvsd_apply_top_k_top_p(float* logits, int64_t logits_stride, const int64_t* top_k,
+                           const float* top_p, int64_t num_rows, int64_t vocab_size,
+                           mvsd_stream_t stream) {
+  if (num_rows < 0 || vocab_size <= 0) return MVSD_E_INVALID;
+  if (num_rows == 0 || (!top_k && !top_p)) return MVSD_OK;
+  if (!logits || logits_stride < vocab_size) return MVSD_E_INVALID;
+  if (vocab_size > 0x7fffffff || num_rows > 0x7fffffff) return MVSD_E_RANGE;
+  return hip_status(mvsd::launch_topk_topp(logits, logits_stride, top_k, top_p, num_rows,
+                                           vocab_size, (hipStream_t)stream));
 }
 
 int mvsd_softmax_rows(float* probs, int64_t probs_stride, const void* logits, int dtype,

@@ -228,10 +228,12 @@ __device__ inline void block_argmax(float (&v)[N], int (&i)[N], float* sv, int* 
 // 0xffffffff - index so that equal values prefer the lower index.  Key 0 is below every
 // real pair (the smallest float, -inf, maps to 0x007fffff).
 
+// Order-preserving key of a float: -0.0 and +0.0 share a key (they compare equal), NaN is
+// above every number.
 __device__ inline uint32_t ordered_bits(float x) {
   const uint32_t b = __float_as_uint(x);
   const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return (x != x) ? 0xffffffffu : o;
+  return (x != x) ? 0xffffffffu : (x == 0.f ? 0x80000000u : o);
 }
 
 __device__ inline uint64_t argmax_key(float v, int idx) {

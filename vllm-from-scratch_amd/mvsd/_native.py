@@ -78,6 +78,8 @@ SIGNATURES = {
     "mvsd_rejection_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int, c_int64]),
     "mvsd_rejection_workspace_init": (c_int, [c_void_p, c_int64, c_void_p]),
     "mvsd_rejection_sample": (c_int, [ctypes.POINTER(RejectionArgs), c_void_p]),
+    "mvsd_apply_top_k_top_p": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
+                                       c_void_p]),
     "mvsd_softmax_rows": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int64, c_void_p, c_int64,
                                   c_int64, c_void_p]),
     "mvsd_sample_recovered_tokens": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
