@@ -58,11 +58,23 @@ def make_workload(name, device):
 
 
 def run_step(w):
+    """One verification step.  Workloads with top-k / top-p (c4) go through the processed
+    path of RejectionSampler.forward: fp32 upcast of the verify rows, temperature divide and
+    top-k / top-p masking (apply_sampling_constraints), then rejection_sample."""
     from mvsd.sample.metadata import SamplingMetadata
-    from mvsd.sample.rejection_sampler import rejection_sample
+    from mvsd.sample.rejection_sampler import apply_sampling_constraints, rejection_sample
 
     sm = SamplingMetadata(temperature=w.temperature, all_greedy=w.all_greedy,
-                          all_random=w.all_random, top_k=None, top_p=None)
+                          all_random=w.all_random, top_k=w.top_k, top_p=w.top_p)
+    if w.top_k is not None or w.top_p is not None:
+        def step():
+            rows = w.target_logits if w.target_rows is None else w.target_logits[w.target_rows.long()]
+            processed = apply_sampling_constraints(rows.float(), w.cu_num_draft_tokens, sm)
+            return rejection_sample(
+                w.draft_token_ids, w.num_draft_tokens, w.max_spec_len, w.cu_num_draft_tokens,
+                w.draft_probs, processed, w.bonus_token_ids, sm, uniform_probs=w.uniforms,
+                exp_noise=w.exp_noise)
+        return step
 
     def step():
         return rejection_sample(
@@ -121,7 +133,22 @@ def cpu_baseline(w, min_seconds):
     ids = w.draft_token_ids.cpu()
     bonus = w.bonus_token_ids.cpu()
 
+    constrained = w.top_k is not None or w.top_p is not None
+    if constrained:
+        from oracle import topk_topp as otp
+
+        req = torch.from_numpy(orc.request_of_row(ks))
+        row_t = temp[req]
+        row_t = torch.where(row_t == 0, torch.ones_like(row_t), row_t)
+        row_k = None if w.top_k is None else w.top_k.cpu()[req]
+        row_p = None if w.top_p is None else w.top_p.cpu()[req]
+
     def run():
+        if constrained:  # processed path: temperature, top-k / top-p, then verification
+            x = otp.apply_top_k_top_p(tl.float() / row_t.unsqueeze(-1), row_k, row_p)
+            return orc.rejection_sample(ids, ks, w.max_spec_len, dp, x, bonus, temperature=temp,
+                                        all_greedy=w.all_greedy, uniforms=u, exp_noise=noise,
+                                        apply_temperature=False)
         return orc.rejection_sample(ids, ks, w.max_spec_len, dp, tl, bonus, temperature=temp,
                                     all_greedy=w.all_greedy, uniforms=u, exp_noise=noise,
                                     apply_temperature=w.apply_temperature)
@@ -236,7 +263,7 @@ def main():
         "data": "synthetic (seeded on-device Philox; random logits, no checkpoint)",
         "config": {"workload": {"h": "headline B=256 k=4 V=151936 fp32 random T=0.8",
                                 "c1": "c1 greedy B=4 k=3 fp32", "c2": "c2 random B=64 k=4 fp32",
-                                "c4": "c4 ragged B=512 bf16 (no top-k/top-p)",
+                                "c4": "c4 ragged B=512 bf16, top-k=50 / top-p=0.9 quartiles",
                                 "c5": "c5 eagle B=1024 k=7 bf16 target"}[args.config],
                    "batch_size": w.batch_size, "num_draft_rows": w.num_tokens,
                    "vocab_size": w.vocab_size, "algorithmic_bytes": nbytes},
