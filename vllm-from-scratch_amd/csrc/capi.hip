@@ -46,10 +46,10 @@ constexpr int kMaxDevices = 64;
 // (CUs x occupancy).
 int verify_capacity(int device, int dtype, bool fused, bool has_draft) {
   static std::mutex mu;
-  static int cache[kMaxDevices][3][3];
+  static int cache[kMaxDevices][3][4];
   if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2) return 0;
   std::lock_guard<std::mutex> lock(mu);
-  int& slot = cache[device][dtype][fused ? (has_draft ? 2 : 1) : 0];
+  int& slot = cache[device][dtype][(fused ? 2 : 0) + (has_draft ? 1 : 0)];
   if (slot > 0) return slot;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
@@ -204,7 +204,7 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
         cap = fcap;
       }
     }
-    if (!fused) cap = verify_capacity(device, a->target_dtype, false, false);
+    if (!fused) cap = verify_capacity(device, a->target_dtype, false, a->draft_probs != nullptr);
     if (cap <= 0) return hip_status(hipErrorInvalidDevice);
   }
   // Upper bound on groups: min(P, B * ceil(max_spec_len / G)).

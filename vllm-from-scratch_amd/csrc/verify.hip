@@ -429,6 +429,9 @@ __device__ inline void load_raw_f32(const float* __restrict__ base, int64_t s0, 
 // Walk [v0, vend) in SUB-column sub-chunks: load(buf, s0, Fast<bool>) issues a sub-chunk's
 // loads, body(buf, s0, Fast<bool>) consumes them.  hook() runs once, after the first loads
 // are issued.  Unaligned inputs and the partial last sub-chunk take the checked path.
+// The next sub-chunk's loads are issued unconditionally (the last one of the run reloads the
+// final sub-chunk, an L2 hit): every path then issues the same loads, so the compiler's
+// in-order load counter lets body(j) wait for sub-chunk j alone while j + 1 is in flight.
 template <int SUB, typename Buf, typename Load, typename Body, typename Hook>
 __device__ inline void pipeline(int64_t v0, int64_t vend, bool aligned, Load&& load, Body&& body,
                                 Hook&& hook) {
@@ -438,10 +441,10 @@ __device__ inline void pipeline(int64_t v0, int64_t vend, bool aligned, Load&& l
     load(a, v0, Fast<true>());
     hook();
     for (int j = 0;;) {
-      if (j + 1 < nfull) load(b, v0 + (int64_t)(j + 1) * SUB, Fast<true>());
+      load(b, v0 + (int64_t)min(j + 1, nfull - 1) * SUB, Fast<true>());
       body(a, v0 + (int64_t)j * SUB, Fast<true>());
       if (++j == nfull) break;
-      if (j + 1 < nfull) load(a, v0 + (int64_t)(j + 1) * SUB, Fast<true>());
+      load(a, v0 + (int64_t)min(j + 1, nfull - 1) * SUB, Fast<true>());
       body(b, v0 + (int64_t)j * SUB, Fast<true>());
       if (++j == nfull) break;
     }
@@ -488,13 +491,13 @@ __device__ inline T row_of_thread(const T (&a)[G]) {
 template <int DT, int EPT, int G>
 __device__ inline auto target_loader(const VerifyParams& p, const typename Elem<DT>::storage* (&tb)[G],
                                      int nrows, int64_t vend) {
-  return [&p, &tb, nrows, vend](TargetBuf<DT, EPT, G>& buf, int64_t s0, auto fast) {
+  // every row slot loads (rows past nrows repeat the last row), so every path issues the
+  // same loads
+  return [&p, &tb, vend](TargetBuf<DT, EPT, G>& buf, int64_t s0, auto fast) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      if (g < nrows) {
-        if constexpr (decltype(fast)::value) load_raw<DT, EPT>(tb[g], s0, buf.x[g]);
-        else load_raw_checked<DT, EPT>(tb[g], s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x[g]);
-      }
+      if constexpr (decltype(fast)::value) load_raw<DT, EPT>(tb[g], s0, buf.x[g]);
+      else load_raw_checked<DT, EPT>(tb[g], s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x[g]);
     }
   };
 }
@@ -598,7 +601,7 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
 // B-task: per row of the group, the chunk-local argmax of max(p - q, 0) * (1 / E).  The
 // group's stats were published by A-tasks holding lower tickets; the wait for them overlaps
 // with the first sub-chunk's loads.
-template <int DT, int EPT, int G, typename Hook>
+template <int DT, int EPT, int G, bool HAS_DRAFT, typename Hook>
 __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1, int row0,
                                    int nrows, int64_t v0, int64_t vend, uint64_t* s_key,
                                    float* s_M, float* s_L, Hook&& after_loads) {
@@ -611,21 +614,21 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int row = row0 + min(g, nrows - 1);
-    qb[g] = p.draft ? p.draft + (int64_t)row * p.draft_stride : nullptr;
-    d[g] = p.draft ? -1 : p.draft_ids[row];
+    qb[g] = HAS_DRAFT ? p.draft + (int64_t)row * p.draft_stride : nullptr;
+    d[g] = HAS_DRAFT ? -1 : p.draft_ids[row];
   }
   const float* eb = p.noise + (int64_t)r * p.noise_stride;
-  const bool aligned = p.target_aligned && p.noise_aligned && (p.draft_aligned || !p.draft);
+  const bool aligned = p.target_aligned && p.noise_aligned && (p.draft_aligned || !HAS_DRAFT);
 
+  // every row slot loads (rows past nrows repeat the last row): one load sequence on every path
   auto load = [&](Buf& buf, int64_t s0, auto fast) {
     constexpr bool F = decltype(fast)::value;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      if (g < nrows) {
-        if constexpr (F) load_raw<DT, EPT>(tb[g], s0, buf.x[g]);
-        else load_raw_checked<DT, EPT>(tb[g], s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x[g]);
-        if (p.draft) load_raw_f32<DT, EPT, F>(qb[g], s0, vend, p.draft_aligned, 0.f, buf.q[g]);
-      }
+      if constexpr (F) load_raw<DT, EPT>(tb[g], s0, buf.x[g]);
+      else load_raw_checked<DT, EPT>(tb[g], s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x[g]);
+      if constexpr (HAS_DRAFT)
+        load_raw_f32<DT, EPT, F>(qb[g], s0, vend, p.draft_aligned, 0.f, buf.q[g]);
     }
     load_raw_f32<DT, EPT, F>(eb, s0, vend, p.noise_aligned, 1.f, buf.e);
   };
@@ -670,8 +673,9 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
           const int idx = elem_index<DT, EPT>(s0, k);
           const float x = raw_elem<DT>(buf.x[g], k);
           const float prob = __builtin_amdgcn_exp2f(fmaf(x - MX[g], c1, NL[g]));  // softmax
-          const float w = p.draft ? fmaxf(prob - raw_f32(buf.q[g], k), 0.f)
-                                  : (idx == d[g] ? 0.f : prob);
+          float w;
+          if constexpr (HAS_DRAFT) w = fmaxf(prob - raw_f32(buf.q[g], k), 0.f);
+          else w = idx == d[g] ? 0.f : prob;
           const float score = w * inv[k];
           // columns rise with s0 and k, so a strict compare keeps the first maximum
           const bool take = (score > bv[g]) & (decltype(fast)::value || idx < vend);
@@ -753,7 +757,7 @@ __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, i
   dst[6] = d.w;
 }
 
-template <int DT, int EPT, int G>
+template <int DT, int EPT, int G, bool HAS_DRAFT>
 __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(VerifyParams p) {
   static_assert(EPT % Elem<DT>::kVec == 0, "EPT must be a multiple of the vector width");
   __shared__ float s_red[G * kVWaves];
@@ -809,7 +813,8 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
     } else if (!phase_b) {
       task_stats<DT, EPT, G>(p, c, c1, row0, nrows, v0, vend, s_red, prefetch);
     } else {
-      task_scores<DT, EPT, G>(p, c, r, c1, row0, nrows, v0, vend, s_key, s_M, s_L, prefetch);
+      task_scores<DT, EPT, G, HAS_DRAFT>(p, c, r, c1, row0, nrows, v0, vend, s_key, s_M, s_L,
+                                         prefetch);
     }
     // ---- request completion: the last counted task runs the accept/reject chain ----
     // (counted: B-tasks of full random requests, A-tasks otherwise)
@@ -1273,7 +1278,9 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int
 template <int DT>
 const void* kernel_for(bool fused, bool has_draft) {
   constexpr int E = ept_of<DT>();
-  if (!fused) return reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup>);
+  if (!fused)
+    return has_draft ? reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, true>)
+                     : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false>);
   return has_draft ? reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, true>)
                    : reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, false>);
 }
