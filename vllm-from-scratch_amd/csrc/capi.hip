@@ -80,7 +80,7 @@ int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 // Workspace layout.  ctrl = {ticket, sticky spin-limit flag (byte offset 4), exit counter}.
 struct WorkspaceLayout {
-  int64_t ctrl, grp_off, grp_desc, req_cnt, stat_slots, arg_slots, total;
+  int64_t ctrl, grp_off, grp_desc, req_cnt, queues, qgi, stat_slots, arg_slots, total;
 };
 
 WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
@@ -94,6 +94,10 @@ WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
   off = align_up(off + (P > 0 ? P : 1) * 16, 256);
   l.req_cnt = off;
   off = align_up(off + (B > 0 ? B : 1) * 4, 256);
+  l.queues = off;  // qticket, qcount, qoff: kMaxQueues ints each
+  off = align_up(off + 3 * mvsd::kMaxQueues * 4, 256);
+  l.qgi = off;
+  off = align_up(off + (P > 0 ? P : 1) * 4, 256);
   l.stat_slots = off;
   off = align_up(off + P * nc * 8, 256);
   l.arg_slots = off;
@@ -252,6 +256,15 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   p.grp_off = reinterpret_cast<int*>(ws + lay.grp_off);
   p.grp_desc = reinterpret_cast<int4*>(ws + lay.grp_desc);
   p.req_cnt = reinterpret_cast<int*>(ws + lay.req_cnt);
+  p.qticket = reinterpret_cast<int*>(ws + lay.queues);
+  p.qcount = p.qticket + mvsd::kMaxQueues;
+  p.qoff = p.qcount + mvsd::kMaxQueues;
+  p.qgi = reinterpret_cast<int*>(ws + lay.qgi);
+  // Work queues (MVSD_VERIFY_QUEUES, 1..16; one per XCD gives each queue one L2).  One queue
+  // measured fastest at the headline: the re-read is served by the Infinity Cache anyway.
+  int nq = 1;
+  if (const char* env = getenv("MVSD_VERIFY_QUEUES")) nq = atoi(env);
+  p.nq = nq < 1 ? 1 : (nq > mvsd::kMaxQueues ? mvsd::kMaxQueues : nq);
   p.stat_slots = reinterpret_cast<uint64_t*>(ws + lay.stat_slots);
   p.arg_slots = reinterpret_cast<uint64_t*>(ws + lay.arg_slots);
 
@@ -260,19 +273,23 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
     int64_t tasks;
     if (fused) {
       tasks = groups * plan.nc;
+      grid = (int)(tasks < cap ? tasks : cap);
     } else {
-      // B-chunks of a group are claimed `lag` groups after its A-chunks: far enough that the
-      // resident workgroups (each holding a current and a prefetched ticket) have finished the
-      // A-chunks, so score tasks rarely wait.
+      // Each queue is served by grid / nq workgroups.  A group's score chunks are claimed
+      // `lag` groups after its stats chunks: enough for that queue's workgroups (each holding
+      // a current and a prefetched ticket) to have finished the stats, and as few as possible
+      // so that the score tasks re-read the target chunk while it is still in the XCD's L2.
       p.two_phase = two_phase;
-      int lag = (2 * cap + 2 * plan.nc - 1) / (2 * plan.nc) + 2;
+      grid = cap / p.nq * p.nq;
+      if (grid < p.nq) grid = p.nq;
+      const int per_queue = grid / p.nq;
+      int lag = (2 * per_queue + 2 * plan.nc - 1) / (2 * plan.nc) + 1;
       if (const char* env = getenv("MVSD_VERIFY_LAG")) lag = atoi(env);
       p.lag = lag < 1 ? 1 : (lag > 4096 ? 4096 : lag);
       const int64_t step = p.two_phase ? 2 * plan.nc : plan.nc;
-      tasks = (groups + (p.two_phase ? p.lag : 0)) * step;
+      tasks = (groups + (p.two_phase ? p.lag * p.nq : 0)) * step;
     }
     if (tasks > 0x7fffffff - 2 * (int64_t)cap) return MVSD_E_RANGE;
-    grid = (int)(tasks < cap ? tasks : cap);
   }
   return hip_status(mvsd::launch_verify(p, a->target_dtype, fused, grid, (hipStream_t)stream));
 }

@@ -7,6 +7,7 @@
 namespace mvsd {
 
 constexpr int kMaxSpecLen = 128;  // reference MAX_SPEC_LEN, rejection_sampler.py:83
+constexpr int kMaxQueues = 16;    // work queues of the split verify kernel
 #ifndef MVSD_VERIFY_THREADS
 #define MVSD_VERIFY_THREADS 512
 #endif
@@ -54,6 +55,14 @@ struct VerifyParams {
   int4* grp_desc;        // [P] per group: request, first row, rows | groups << 8 | flags << 16,
                          //     bits of log2(e) / T   (flags: 1 greedy, 2 needs recovered scores)
   int* req_cnt;          // [B] finished tasks per request (zero between calls)
+  // Work queues of the split kernel: request r belongs to queue r % nq, and workgroup w
+  // serves queue w % nq (workgroups are dispatched round-robin over the XCDs, so a queue's
+  // tasks share one L2).  qgi lists each queue's groups in request order.
+  int nq;
+  int* qticket;          // [nq] ticket counters
+  int* qcount;           // [nq] groups per queue
+  int* qoff;             // [nq] offset of each queue's list in qgi
+  int* qgi;              // [groups] group indices, queue-major
   uint64_t* stat_slots;  // [P * nc] packed (chunk max, chunk sumexp); 0 = empty
   uint64_t* arg_slots;   // [P * nc] packed (chunk argmax value, index + 1); 0 = empty
 };

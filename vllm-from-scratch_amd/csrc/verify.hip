@@ -170,6 +170,41 @@ __global__ __launch_bounds__(1024) void verify_init_kernel(VerifyParams p) {
     __syncthreads();
   }
   if (tid == 0) p.grp_off[p.B] = s_carry;
+  __syncthreads();
+
+  // Queue lists: queue q holds the groups of requests q, q + nq, ... in request order.
+  __shared__ int s_qoff;
+  if (tid == 0) s_qoff = 0;
+  __syncthreads();
+  for (int q = 0; q < p.nq; ++q) {
+    if (tid == 0) {
+      s_carry = 0;
+      p.qoff[q] = s_qoff;
+    }
+    __syncthreads();
+    for (int base = q; base < p.B; base += 1024 * p.nq) {
+      const int r = base + tid * p.nq;
+      const int ng = r < p.B ? p.grp_off[r + 1] - p.grp_off[r] : 0;
+      s_scan[tid] = ng;
+      __syncthreads();
+      for (int off = 1; off < 1024; off <<= 1) {
+        const int add = tid >= off ? s_scan[tid - off] : 0;
+        __syncthreads();
+        s_scan[tid] += add;
+        __syncthreads();
+      }
+      const int lo = s_qoff + s_carry + s_scan[tid] - ng;
+      for (int j = 0; j < ng; ++j) p.qgi[lo + j] = p.grp_off[r] + j;
+      __syncthreads();
+      if (tid == 1023) s_carry += s_scan[1023];
+      __syncthreads();
+    }
+    if (tid == 0) {
+      p.qcount[q] = s_carry;
+      s_qoff += s_carry;
+    }
+    __syncthreads();
+  }
 }
 
 // ------------------------------------------------------------------ row statistics ---
@@ -367,26 +402,34 @@ __device__ inline int64_t vec_col(int64_t s0, int i) {
   return s0 + ((int64_t)i * kVThreads + threadIdx.x) * VEC;
 }
 
-// Target loads: non-temporal unless MVSD_VERIFY_NT_TARGET is 0 (tuning switch).
-#ifndef MVSD_VERIFY_NT_TARGET
-#define MVSD_VERIFY_NT_TARGET 1
+// Target loads.  The stats tasks' loads are temporal so that the lines stay cached for the
+// score tasks' re-read of the same chunk (MVSD_VERIFY_NT_STATS=1 makes them non-temporal);
+// the score tasks' loads (MVSD_VERIFY_NT_SCORES) and the single-read kernel's are the last
+// use and stream non-temporally.
+#ifndef MVSD_VERIFY_NT_STATS
+#define MVSD_VERIFY_NT_STATS 0
 #endif
+#ifndef MVSD_VERIFY_NT_SCORES
+#define MVSD_VERIFY_NT_SCORES 1
+#endif
+template <bool NT>
 __device__ inline u32x4 load_target16(const void* p) {
   const u32x4* q = static_cast<const u32x4*>(p);
-  if constexpr (MVSD_VERIFY_NT_TARGET) return __builtin_nontemporal_load(q);
+  if constexpr (NT) return __builtin_nontemporal_load(q);
   else return *q;
 }
 
 // DT row sub-chunk, full and aligned.
-template <int DT, int EPT>
+template <int DT, int EPT, bool NT>
 __device__ inline void load_raw(const typename Elem<DT>::storage* __restrict__ base, int64_t s0,
                                 u32x4 (&out)[EPT / Elem<DT>::kVec]) {
 #pragma unroll
-  for (int i = 0; i < EPT / Elem<DT>::kVec; ++i) out[i] = load_target16(base + vec_col<DT>(s0, i));
+  for (int i = 0; i < EPT / Elem<DT>::kVec; ++i)
+    out[i] = load_target16<NT>(base + vec_col<DT>(s0, i));
 }
 
 // DT row sub-chunk, bounds-checked: elements at or beyond vend read as `fill`.
-template <int DT, int EPT>
+template <int DT, int EPT, bool NT>
 __device__ inline void load_raw_checked(const typename Elem<DT>::storage* __restrict__ base,
                                         int64_t s0, int64_t vend, bool aligned,
                                         typename Elem<DT>::storage fill,
@@ -397,7 +440,7 @@ __device__ inline void load_raw_checked(const typename Elem<DT>::storage* __rest
   for (int i = 0; i < EPT / VEC; ++i) {
     const int64_t col = vec_col<DT>(s0, i);
     if (aligned && col + VEC <= vend) {
-      out[i] = load_target16(base + col);
+      out[i] = load_target16<NT>(base + col);
     } else {
       S tmp[VEC];
 #pragma unroll
@@ -429,31 +472,55 @@ __device__ inline void load_raw_f32(const float* __restrict__ base, int64_t s0, 
 // Walk [v0, vend) in SUB-column sub-chunks: load(buf, s0, Fast<bool>) issues a sub-chunk's
 // loads, body(buf, s0, Fast<bool>) consumes them.  hook() runs once, after the first loads
 // are issued.  Unaligned inputs and the partial last sub-chunk take the checked path.
-// The next sub-chunk's loads are issued unconditionally (the last one of the run reloads the
-// final sub-chunk, an L2 hit): every path then issues the same loads, so the compiler's
-// in-order load counter lets body(j) wait for sub-chunk j alone while j + 1 is in flight.
+// The loads of the next MVSD_VERIFY_DEPTH - 1 sub-chunks are issued unconditionally (past the
+// end of the run they reload the final sub-chunk, an L2 hit): every path then issues the same
+// loads, so the compiler's in-order load counter lets body(j) wait for sub-chunk j alone while
+// the following ones are in flight.
+#ifndef MVSD_VERIFY_DEPTH
+#define MVSD_VERIFY_DEPTH 2
+#endif
 template <int SUB, typename Buf, typename Load, typename Body, typename Hook>
 __device__ inline void pipeline(int64_t v0, int64_t vend, bool aligned, Load&& load, Body&& body,
                                 Hook&& hook) {
   const int nfull = aligned ? (int)((vend - v0) / SUB) : 0;
-  Buf a, b;
+  auto at = [&](int j) { return v0 + (int64_t)min(j, nfull - 1) * SUB; };
   if (nfull > 0) {
-    load(a, v0, Fast<true>());
-    hook();
-    for (int j = 0;;) {
-      load(b, v0 + (int64_t)min(j + 1, nfull - 1) * SUB, Fast<true>());
-      body(a, v0 + (int64_t)j * SUB, Fast<true>());
-      if (++j == nfull) break;
-      load(a, v0 + (int64_t)min(j + 1, nfull - 1) * SUB, Fast<true>());
-      body(b, v0 + (int64_t)j * SUB, Fast<true>());
-      if (++j == nfull) break;
+    if constexpr (MVSD_VERIFY_DEPTH >= 3) {  // sub-chunks j+1 and j+2 in flight during body(j)
+      Buf a, b, c;
+      load(a, at(0), Fast<true>());
+      load(b, at(1), Fast<true>());
+      hook();
+      for (int j = 0;;) {
+        load(c, at(j + 2), Fast<true>());
+        body(a, v0 + (int64_t)j * SUB, Fast<true>());
+        if (++j == nfull) break;
+        load(a, at(j + 2), Fast<true>());
+        body(b, v0 + (int64_t)j * SUB, Fast<true>());
+        if (++j == nfull) break;
+        load(b, at(j + 2), Fast<true>());
+        body(c, v0 + (int64_t)j * SUB, Fast<true>());
+        if (++j == nfull) break;
+      }
+    } else {
+      Buf a, b;
+      load(a, at(0), Fast<true>());
+      hook();
+      for (int j = 0;;) {
+        load(b, at(j + 1), Fast<true>());
+        body(a, v0 + (int64_t)j * SUB, Fast<true>());
+        if (++j == nfull) break;
+        load(a, at(j + 1), Fast<true>());
+        body(b, v0 + (int64_t)j * SUB, Fast<true>());
+        if (++j == nfull) break;
+      }
     }
   } else {
     hook();
   }
   for (int64_t s0 = v0 + (int64_t)nfull * SUB; s0 < vend; s0 += SUB) {
-    load(a, s0, Fast<false>());
-    body(a, s0, Fast<false>());
+    Buf t;
+    load(t, s0, Fast<false>());
+    body(t, s0, Fast<false>());
   }
 }
 
@@ -496,8 +563,11 @@ __device__ inline auto target_loader(const VerifyParams& p, const typename Elem<
   return [&p, &tb, vend](TargetBuf<DT, EPT, G>& buf, int64_t s0, auto fast) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      if constexpr (decltype(fast)::value) load_raw<DT, EPT>(tb[g], s0, buf.x[g]);
-      else load_raw_checked<DT, EPT>(tb[g], s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x[g]);
+      if constexpr (decltype(fast)::value)
+        load_raw<DT, EPT, MVSD_VERIFY_NT_STATS>(tb[g], s0, buf.x[g]);
+      else
+        load_raw_checked<DT, EPT, MVSD_VERIFY_NT_STATS>(tb[g], s0, vend, p.target_aligned,
+                                                        Elem<DT>::ninf(), buf.x[g]);
     }
   };
 }
@@ -625,8 +695,11 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
     constexpr bool F = decltype(fast)::value;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      if constexpr (F) load_raw<DT, EPT>(tb[g], s0, buf.x[g]);
-      else load_raw_checked<DT, EPT>(tb[g], s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x[g]);
+      if constexpr (F)
+        load_raw<DT, EPT, MVSD_VERIFY_NT_SCORES>(tb[g], s0, buf.x[g]);
+      else
+        load_raw_checked<DT, EPT, MVSD_VERIFY_NT_SCORES>(tb[g], s0, vend, p.target_aligned,
+                                                         Elem<DT>::ninf(), buf.x[g]);
       if constexpr (HAS_DRAFT)
         load_raw_f32<DT, EPT, F>(qb[g], s0, vend, p.draft_aligned, 0.f, buf.q[g]);
     }
@@ -728,6 +801,7 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
 // are the B-chunks (scores) of group s - lag.  Slots of absent groups are claimed and skipped.
 struct TaskDecode {
   int total, step_size, nc, lag, groups, two_phase;
+  const int* qgi;  // queue position -> group index (nullptr: identity)
 };
 
 // Thread 0: decode ticket t and fetch its group descriptor into dst[0..6]
@@ -741,9 +815,9 @@ __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, i
     const int w = t - step * td.step_size;
     const bool phase_b = w >= td.nc;
     c = phase_b ? w - td.nc : w;
-    const int gi = phase_b ? step - td.lag : step;
-    if (gi >= 0 && gi < td.groups) {
-      d = p.grp_desc[gi];
+    const int li = phase_b ? step - td.lag : step;
+    if (li >= 0 && li < td.groups) {
+      d = p.grp_desc[td.qgi ? td.qgi[li] : li];
       const bool full = (d.z >> 16) & kFull;
       flags = (!phase_b || full ? 1 : 0) | (phase_b ? 2 : 0);
     }
@@ -769,24 +843,28 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   __shared__ FinalizeSmem fsm;
 
   const int tid = threadIdx.x;
+  const int queue = blockIdx.x % p.nq;
+  int* ticket = &p.qticket[queue];
+  const int groups = p.grp_off[p.B];
   TaskDecode td;
   td.nc = p.nc;
   td.lag = p.lag;
-  td.groups = p.grp_off[p.B];
+  td.groups = p.qcount[queue];
+  td.qgi = p.qgi + p.qoff[queue];
   td.two_phase = p.two_phase;
   td.step_size = p.two_phase ? 2 * td.nc : td.nc;
   td.total = (td.groups + (p.two_phase ? td.lag : 0)) * td.step_size;
 
   // The next ticket is claimed when a task starts and decoded once the task's loads are in
   // flight, so the atomic and the descriptor fetch overlap with HBM traffic.
-  if (tid == 0) fetch_task(p, td, atomic_add_relaxed(&p.ctrl[0], 1), s_info[0]);
+  if (tid == 0) fetch_task(p, td, atomic_add_relaxed(ticket, 1), s_info[0]);
   __syncthreads();
   for (int par = 0;; par ^= 1) {
     const int* info = s_info[par];
     const int t = info[0];
     if (t >= td.total) break;
     int tnext = 0;
-    if (tid == 0) tnext = atomic_add_relaxed(&p.ctrl[0], 1);
+    if (tid == 0) tnext = atomic_add_relaxed(ticket, 1);
     auto prefetch = [&]() {
       if (tid == 0) fetch_task(p, td, tnext, s_info[par ^ 1]);
     };
@@ -833,11 +911,16 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   __syncthreads();
   if (s_last) {
     for (int i = tid; i <= p.B; i += kVThreads) p.grp_off[i] = 0;
-    for (int i = tid; i < td.groups; i += kVThreads) p.grp_desc[i] = make_int4(0, 0, 0, 0);
-    if (tid == 0) {
-      atomic_store_relaxed(&p.ctrl[0], 0);
-      atomic_store_relaxed(&p.ctrl[2], 0);
+    for (int i = tid; i < groups; i += kVThreads) {
+      p.grp_desc[i] = make_int4(0, 0, 0, 0);
+      p.qgi[i] = 0;
     }
+    for (int q = tid; q < p.nq; q += kVThreads) {
+      atomic_store_relaxed(&p.qticket[q], 0);
+      p.qcount[q] = 0;
+      p.qoff[q] = 0;
+    }
+    if (tid == 0) atomic_store_relaxed(&p.ctrl[2], 0);
   }
 }
 
@@ -981,7 +1064,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_FUSED_ATTRS void verify_fused_kerne
         const S* base = target + (int64_t)s_ring.trow[ix % kRing][g] * p.target_stride;
 #pragma unroll
         for (int n = 0; n < NV; ++n)
-          b.x[g][n] = load_target16(base + min(vec_col<DT>(v0, n), vlast));
+          b.x[g][n] = load_target16<true>(base + min(vec_col<DT>(v0, n), vlast));
       }
     }
     {
@@ -1225,7 +1308,14 @@ __global__ __launch_bounds__(kVThreads) MVSD_FUSED_ATTRS void verify_fused_kerne
   __syncthreads();
   if (s_last) {
     for (int i = tid; i <= p.B; i += kVThreads) p.grp_off[i] = 0;
-    for (int i = tid; i < total / nc; i += kVThreads) p.grp_desc[i] = make_int4(0, 0, 0, 0);
+    for (int i = tid; i < total / nc; i += kVThreads) {
+      p.grp_desc[i] = make_int4(0, 0, 0, 0);
+      p.qgi[i] = 0;
+    }
+    for (int q = tid; q < p.nq; q += kVThreads) {
+      p.qcount[q] = 0;
+      p.qoff[q] = 0;
+    }
     if (tid == 0) atomic_store_relaxed(&p.ctrl[2], 0);
   }
 }
