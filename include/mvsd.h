@@ -206,6 +206,14 @@ int mvsd_ngram_propose(int32_t* drafts, int32_t* num_valid, int32_t* token_ids,
                        int32_t min_n, int32_t max_n, int32_t k, int cap_by_model_len,
                        int64_t max_model_len, mvsd_stream_t stream);
 
+/* ------------------------------------------------------------------------------------ */
+/* selftest — on-device check of an arithmetic assumption of the kernels.  No counterpart   */
+/* in the reference.  test 0: the FMA-corrected hardware reciprocal used for 1/E equals     */
+/* IEEE fp32 division for every b in [2^-126, 2^126); adds the number of mismatches to      */
+/* *failures (a device uint64 the caller zeroes).                                          */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -404,3 +404,13 @@ def test_forward_fast_path_matches_processed_path(device):
                             meta.cu_num_draft_tokens, w.draft_probs, processed, w.bonus_token_ids,
                             sm, uniform_probs=u, exp_noise=e)
     assert torch.equal(a, b)
+
+
+def test_corrected_reciprocal_equals_ieee_division(device):
+    """The score kernels compute 1/E with the hardware reciprocal plus one FMA correction;
+    it must equal IEEE fp32 division for every normal E with a normal reciprocal."""
+    from mvsd import _native as nat
+    failures = torch.zeros(1, dtype=torch.int64, device=device)
+    nat.check(nat.lib().mvsd_selftest(0, failures.data_ptr(), nat.stream_of(device)),
+              "mvsd_selftest")
+    assert int(failures.item()) == 0

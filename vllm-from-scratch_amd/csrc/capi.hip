@@ -10,6 +10,7 @@
 
 #include "mvsd_device.h"
 #include "rows.h"
+#include "selftest.h"
 #include "topk.h"
 #include "verify.h"
 
@@ -292,6 +293,13 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
     if (tasks > 0x7fffffff - 2 * (int64_t)cap) return MVSD_E_RANGE;
   }
   return hip_status(mvsd::launch_verify(p, a->target_dtype, fused, grid, (hipStream_t)stream));
+}
+
+int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream) {
+  if (!failures) return MVSD_E_INVALID;
+  if (test != 0) return MVSD_E_INVALID;
+  return hip_status(mvsd::launch_selftest_reciprocal(
+      reinterpret_cast<unsigned long long*>(failures), (hipStream_t)stream));
 }
 
 int mvsd_apply_top_k_top_p(float* logits, int64_t logits_stride, const int64_t* top_k,

@@ -92,6 +92,22 @@ __device__ inline void argmax_update(float& bv, int& bi, float v, int i, bool va
   bi = take ? i : bi;
 }
 
+// ------------------------------------------------------------------ reciprocal -------
+// 1.0f / b, correctly rounded, from the hardware reciprocal: v_rcp_f32 is faithful (one of
+// the two floats bracketing 1/b) for normal b with a normal reciprocal, and one FMA correction
+// step then rounds to nearest except when the mantissa of b is all ones and the rcp result is
+// the lower neighbour (r2 then sits on a power of two; the correct result is one ulp above,
+// and both candidates already differ from that power only in the last bit).  Checked against
+// IEEE division for every mantissa of every exponent in [2^-126, 2^126) (mvsd_selftest).
+// Outside that range (and for NaN / inf / negative b) the IEEE division is used.
+__device__ inline float recip_rn(float b) {
+  float r = __builtin_amdgcn_rcpf(b);
+  r = fmaf(fmaf(-b, r, 1.0f), r, r);
+  r = (__float_as_uint(b) & 0x7fffffu) == 0x7fffffu ? __uint_as_float(__float_as_uint(r) | 1u) : r;
+  if (!(b >= 0x1p-126f && b < 0x1p126f)) r = 1.0f / b;
+  return r;
+}
+
 // ------------------------------------------------------------------ wave reductions --
 // Cross-lane steps use DPP row permutations (VALU, no LDS round trip): quad swaps for lane
 // xor 1 and 2, then the half-row and row mirrors, after which every lane of a 16-lane row

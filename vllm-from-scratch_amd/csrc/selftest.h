@@ -1,0 +1,11 @@
+// Host launchers of the on-device arithmetic self-checks (selftest.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace mvsd {
+
+// Adds to *failures the number of fp32 b in [2^-126, 2^126) with recip_rn(b) != 1.0f / b.
+hipError_t launch_selftest_reciprocal(unsigned long long* failures, hipStream_t stream);
+
+}  // namespace mvsd

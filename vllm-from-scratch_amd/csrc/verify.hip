@@ -172,7 +172,15 @@ __global__ __launch_bounds__(1024) void verify_init_kernel(VerifyParams p) {
   if (tid == 0) p.grp_off[p.B] = s_carry;
   __syncthreads();
 
-  // Queue lists: queue q holds the groups of requests q, q + nq, ... in request order.
+  // Queue lists: queue q holds the groups of requests q, q + nq, ... in request order.  One
+  // queue is the identity list and is not materialised.
+  if (p.nq == 1) {
+    if (tid == 0) {
+      p.qcount[0] = s_carry;
+      p.qoff[0] = 0;
+    }
+    return;
+  }
   __shared__ int s_qoff;
   if (tid == 0) s_qoff = 0;
   __syncthreads();
@@ -727,17 +735,19 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
     }
   };
 
+  // Scores are max(p - q, 0) / E >= 0 and ties keep the lowest index, so starting from
+  // (0, v0) and taking only strictly larger scores gives the same argmax without the clamp.
   float bv[G];
   int bi[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    bv[g] = -INFINITY;
+    bv[g] = 0.f;
     bi[g] = (int)v0;
   }
   auto body = [&](const Buf& buf, int64_t s0, auto fast) {
     float inv[EPT];
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) inv[k] = 1.0f / raw_f32(buf.e, k);
+    for (int k = 0; k < EPT; ++k) inv[k] = recip_rn(raw_f32(buf.e, k));
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       if (g < nrows) {
@@ -747,7 +757,7 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
           const float x = raw_elem<DT>(buf.x[g], k);
           const float prob = __builtin_amdgcn_exp2f(fmaf(x - MX[g], c1, NL[g]));  // softmax
           float w;
-          if constexpr (HAS_DRAFT) w = fmaxf(prob - raw_f32(buf.q[g], k), 0.f);
+          if constexpr (HAS_DRAFT) w = prob - raw_f32(buf.q[g], k);  // clamp folded into bv >= 0
           else w = idx == d[g] ? 0.f : prob;
           const float score = w * inv[k];
           // columns rise with s0 and k, so a strict compare keeps the first maximum
@@ -850,7 +860,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   td.nc = p.nc;
   td.lag = p.lag;
   td.groups = p.qcount[queue];
-  td.qgi = p.qgi + p.qoff[queue];
+  td.qgi = p.nq > 1 ? p.qgi + p.qoff[queue] : nullptr;
   td.two_phase = p.two_phase;
   td.step_size = p.two_phase ? 2 * td.nc : td.nc;
   td.total = (td.groups + (p.two_phase ? td.lag : 0)) * td.step_size;
@@ -1256,12 +1266,12 @@ __global__ __launch_bounds__(kVThreads) MVSD_FUSED_ATTRS void verify_fused_kerne
       const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
       float inv[EPT];
 #pragma unroll
-      for (int k = 0; k < EPT; ++k) inv[k] = 1.0f / raw_f32(cur.e, k);
+      for (int k = 0; k < EPT; ++k) inv[k] = recip_rn(raw_f32(cur.e, k));
       uint64_t key[G];
       auto score_rows = [&](auto fast) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          float bv = -INFINITY;
+          float bv = 0.f;  // scores are >= 0: the clamp is folded into the strict compare
           int bi = (int)v0;
           if (g < tp.nrows) {
             const float MX = s_M[g];
@@ -1275,7 +1285,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_FUSED_ATTRS void verify_fused_kerne
               const int idx = elem_index<DT, EPT>(v0, k);
               const float prob = __builtin_amdgcn_exp2f(fmaf(raw_elem<DT>(xr, k) - MX, tp.c1, NL));
               float w;
-              if constexpr (HAS_DRAFT) w = fmaxf(prob - raw_f32(cur.q[g], k), 0.f);
+              if constexpr (HAS_DRAFT) w = prob - raw_f32(cur.q[g], k);
               else w = idx == d ? 0.f : prob;
               const float score = w * inv[k];
               // columns rise with k, so a strict compare keeps the first maximum

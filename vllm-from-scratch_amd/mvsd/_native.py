@@ -80,6 +80,7 @@ SIGNATURES = {
     "mvsd_rejection_sample": (c_int, [ctypes.POINTER(RejectionArgs), c_void_p]),
     "mvsd_apply_top_k_top_p": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                                        c_void_p]),
+    "mvsd_selftest": (c_int, [c_int, c_void_p, c_void_p]),
     "mvsd_softmax_rows": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int64, c_void_p, c_int64,
                                   c_int64, c_void_p]),
     "mvsd_sample_recovered_tokens": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
