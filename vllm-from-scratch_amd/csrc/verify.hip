@@ -865,6 +865,19 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   td.step_size = p.two_phase ? 2 * td.nc : td.nc;
   td.total = (td.groups + (p.two_phase ? td.lag : 0)) * td.step_size;
 
+  // Deferred request-completion count (see below).
+  int pend_cnt = 0, pend_r = -1, pend_target = 0;
+  bool pend_greedy = false, pend_full = false;
+  auto settle = [&]() {
+    if (pend_r >= 0) {
+      if (tid == 0) s_last = pend_cnt == pend_target - 1;
+      __syncthreads();
+      if (s_last) finalize_request(p, pend_r, pend_greedy, pend_full, fsm);
+      __syncthreads();
+      pend_r = -1;
+    }
+  };
+
   // The next ticket is claimed when a task starts and decoded once the task's loads are in
   // flight, so the atomic and the descriptor fetch overlap with HBM traffic.
   if (tid == 0) fetch_task(p, td, atomic_add_relaxed(ticket, 1), s_info[0]);
@@ -905,14 +918,19 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
                                          prefetch);
     }
     // ---- request completion: the last counted task runs the accept/reject chain ----
-    // (counted: B-tasks of full random requests, A-tasks otherwise)
+    // (counted: B-tasks of full random requests, A-tasks otherwise).  The counter's result
+    // is examined after the next task, so the atomic's round trip is never waited for.
+    settle();
     if (full == phase_b) {
-      if (tid == 0) s_last = atomic_add_relaxed(&p.req_cnt[r], 1) == ngr * td.nc - 1;
-      __syncthreads();
-      if (s_last) finalize_request(p, r, greedy, full, fsm);
+      if (tid == 0) pend_cnt = atomic_add_relaxed(&p.req_cnt[r], 1);
+      pend_r = r;
+      pend_target = ngr * td.nc;
+      pend_greedy = greedy;
+      pend_full = full;
     }
     __syncthreads();
   }
+  settle();
 
   // The last workgroup out (every other one has made its final claim and finished reading
   // grp_off / grp_desc) returns the group tables, ticket and exit counter to zero, so the
