@@ -95,7 +95,8 @@ typedef struct mvsd_rejection_args {
   const int32_t* target_rows;
   int64_t target_num_rows;              /* rows addressable from target_logits (indices are clamped) */
 
-  /* draft probabilities [P, V] (dtype F32, BF16 or F16), or NULL for point-mass drafts
+  /* draft probabilities [P, V], dtype F32 (other dtype codes return MVSD_E_INVALID), or NULL
+   * for point-mass drafts
    * (ngram: q[d] = 1, recovered distribution = p with the draft id removed, :793-795,:891-897) */
   const void* draft_probs;
   int draft_dtype;

@@ -279,7 +279,8 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
       // Each queue is served by grid / nq workgroups.  A group's score chunks are claimed
       // `lag` groups after its stats chunks: enough for that queue's workgroups (each holding
       // a current and a prefetched ticket) to have finished the stats, and as few as possible
-      // so that the score tasks re-read the target chunk while it is still in the XCD's L2.
+      // so that the score tasks re-read the target chunk while it is still cached (L2 or the
+      // Infinity Cache).
       p.two_phase = two_phase;
       grid = cap / p.nq * p.nq;
       if (grid < p.nq) grid = p.nq;
