@@ -58,30 +58,23 @@ def make_workload(name, device):
 
 
 def run_step(w):
-    """One verification step.  Workloads with top-k / top-p (c4) go through the processed
-    path of RejectionSampler.forward: fp32 upcast of the verify rows, temperature divide and
-    top-k / top-p masking (apply_sampling_constraints), then rejection_sample."""
+    """One verification step: rejection_sample on the raw target rows with the temperature
+    divide and, for workloads with top-k / top-p (c4), the sampling constraints applied in the
+    kernels (RejectionSampler.forward's path when no penalty needs the processed rows)."""
     from mvsd.sample.metadata import SamplingMetadata
-    from mvsd.sample.rejection_sampler import apply_sampling_constraints, rejection_sample
+    from mvsd.sample.rejection_sampler import rejection_sample
 
     sm = SamplingMetadata(temperature=w.temperature, all_greedy=w.all_greedy,
                           all_random=w.all_random, top_k=w.top_k, top_p=w.top_p)
-    if w.top_k is not None or w.top_p is not None:
-        def step():
-            rows = w.target_logits if w.target_rows is None else w.target_logits[w.target_rows.long()]
-            processed = apply_sampling_constraints(rows.float(), w.cu_num_draft_tokens, sm)
-            return rejection_sample(
-                w.draft_token_ids, w.num_draft_tokens, w.max_spec_len, w.cu_num_draft_tokens,
-                w.draft_probs, processed, w.bonus_token_ids, sm, uniform_probs=w.uniforms,
-                exp_noise=w.exp_noise)
-        return step
+    constrained = w.top_k is not None or w.top_p is not None
 
     def step():
         return rejection_sample(
             w.draft_token_ids, w.num_draft_tokens, w.max_spec_len, w.cu_num_draft_tokens,
             w.draft_probs, w.target_logits, w.bonus_token_ids, sm, uniform_probs=w.uniforms,
             exp_noise=w.exp_noise, target_rows=w.target_rows,
-            apply_temperature=w.apply_temperature)
+            apply_temperature=w.apply_temperature or constrained,
+            apply_top_k_top_p=constrained)
     return step
 
 
@@ -275,7 +268,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(args.config),
-                     "kernel": "mvsd::verify_kernel (+ verify_init_kernel) per rejection_sample",
+                     "kernel": ("mvsd::verify_kernel (+ verify_init_kernel"
+                                + (", constraints_kernel" if w.top_k is not None or w.top_p is not None
+                                   else "") + ") per rejection_sample"),
                      "kernel_ms": round(launch_ms, 5)},
         "cpu_baseline": None,
     }

@@ -76,7 +76,9 @@ int mvsd_expand_batch_to_tokens(void* out, const void* x, int dtype,
 /* rejection_greedy_sample_kernel (:678-740), sample_recovered_tokens + its kernel       */
 /* (:627-670, :850-928) and rejection_random_sample_kernel (:744-822); and, when          */
 /* apply_temperature != 0, the temperature divide of apply_sampling_constraints (:553-561)*/
-/* that RejectionSampler.forward (:195-196) runs before it.                               */
+/* that RejectionSampler.forward (:195-196) runs before it; and, when top_k or top_p is   */
+/* given (and not all_greedy), the top-k / top-p masking of that function (:563-571,      */
+/* minivllm/sample/ops/topk_topp_sampler.py:48-79) applied to the divided rows.           */
 /*                                                                                        */
 /* Request i is greedy iff all_greedy != 0 or temperature[i] == 0 (:469-473).            */
 /* Random requests need exp_noise (one Exp(1) row per request, :648-655) unless           */
@@ -126,6 +128,13 @@ typedef struct mvsd_rejection_args {
 
   void* workspace;                      /* >= mvsd_rejection_workspace_bytes(...) bytes */
   int64_t workspace_bytes;
+
+  /* Optional per-request sampling constraints on the verify rows (NULL = none): keep the
+   * top_k[i] largest values (k <= 0 or k >= V keeps all) and the smallest set of largest
+   * values whose probability reaches top_p[i] (p >= 1 keeps all).  Masked entries get
+   * probability 0 and are never a greedy argmax, as the reference's -inf does. */
+  const int64_t* top_k;                 /* [batch_size] */
+  const float* top_p;                   /* [batch_size] */
 } mvsd_rejection_args;
 
 /* Workspace contract: zero-filled before its first use (mvsd_rejection_workspace_init, or
@@ -140,6 +149,18 @@ int64_t mvsd_rejection_workspace_bytes(int64_t batch_size, int64_t num_tokens,
 /* Zero-fill a workspace on `stream` with a kernel (no hipMemsetAsync). */
 int mvsd_rejection_workspace_init(void* workspace, int64_t workspace_bytes, mvsd_stream_t stream);
 int mvsd_rejection_sample(const mvsd_rejection_args* args, mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* sampling_masks — the per-row masks mvsd_rejection_sample applies for top_k / top_p.     */
+/* Replaces: nothing directly; it exposes, as thresholds, what apply_sampling_constraints  */
+/* (minivllm/sample/rejection_sampler.py:537-571) does to the verify rows.  Reads the      */
+/* target, cu_num_draft_tokens, temperature / all_greedy / apply_temperature, top_k and    */
+/* top_p fields of *args.  masks: [num_tokens, 4] fp32, 16-byte aligned; row j gets        */
+/* (A, B, J as int bits, 0): entry i of verify row j, raw value x (before the temperature  */
+/* divide), is masked iff x < A || (x < B && i <= J).  Rows without constraints get        */
+/* (-inf, -inf, -1).                                                                        */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_sampling_masks(const mvsd_rejection_args* args, float* masks, mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
 /* softmax_rows — probs[j, :] = softmax(logits[row_j, :] / t_j) in fp32.                 */
@@ -172,7 +193,8 @@ int mvsd_sample_recovered_tokens(int32_t* recovered_token_ids, const int32_t* cu
 /* keep values >= the k-th largest (ties kept); k <= 0 or k >= V keeps the whole row.       */
 /* top_p [num_rows] fp32 (NULL = none): over the top-k-masked row, mask the ascending       */
 /* (value, then index) prefix whose cumulative softmax mass is <= 1 - p, never the largest  */
-/* entry; p > 1 masks nothing.  Requires 1 <= V < 2^31.                                    */
+/* entry; p >= 1 masks nothing (the reference's p = 1 masks only entries whose fp32       */
+/* probability underflows to 0).  Requires 1 <= V < 2^31.                                 */
 /* ------------------------------------------------------------------------------------ */
 int mvsd_apply_top_k_top_p(float* logits, int64_t logits_stride, const int64_t* top_k,
                            const float* top_p, int64_t num_rows, int64_t vocab_size,
@@ -210,8 +232,10 @@ int mvsd_ngram_propose(int32_t* drafts, int32_t* num_valid, int32_t* token_ids,
 /* ------------------------------------------------------------------------------------ */
 /* selftest — on-device check of an arithmetic assumption of the kernels.  No counterpart   */
 /* in the reference.  test 0: the FMA-corrected hardware reciprocal used for 1/E equals     */
-/* IEEE fp32 division for every b in [2^-126, 2^126); adds the number of mismatches to      */
-/* *failures (a device uint64 the caller zeroes).                                          */
+/* IEEE fp32 division for every b in [2^-126, 2^126).  test 1: the corrected division x/T  */
+/* used by the sampling-constraint kernel equals IEEE fp32 division for every float x at   */
+/* sixteen divisors.  Adds the number of mismatches to *failures (a device uint64 the      */
+/* caller zeroes).                                                                         */
 /* ------------------------------------------------------------------------------------ */
 int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream);
 

@@ -1,0 +1,214 @@
+"""GPU parity of the in-kernel sampling constraints: top-k / top-p applied to the raw verify
+rows as per-row thresholds (mvsd_sampling_masks, rejection_sample(apply_top_k_top_p=True)).
+
+Bar:
+  * the masks the kernels apply, expanded over the raw rows, equal the masks of the
+    processed path (temperature divide, then apply_top_k_top_p on the divided fp32 rows)
+    entry for entry, and match oracle/topk_topp.py on the divided rows except top-p
+    decisions within 1e-5 of the 1 - p crossing (counted);
+  * the verify outputs equal the oracle's rejection sampler run on the rows masked the same
+    way, up to the counted flips oracle.compare allows;
+  * the corrected division x / T the thresholds rely on equals IEEE division for every
+    float x (mvsd_selftest(1))."""
+
+import numpy as np
+import pytest
+import torch
+
+from mvsd import _native as nat
+from mvsd.sample.metadata import SamplingMetadata
+from mvsd.sample.ops.topk_topp_sampler import apply_top_k_top_p
+from mvsd.sample.rejection_sampler import (apply_sampling_constraints, rejection_sample,
+                                           sampling_masks)
+from mvsd.testing import configs
+from oracle import rejection as orc
+from oracle import topk_topp as otp
+
+pytestmark = pytest.mark.gpu
+
+
+def _expand(masks: torch.Tensor, x: np.ndarray) -> np.ndarray:
+    """Boolean [P, V] masked entries of raw rows x from the [P, 4] row masks."""
+    m = masks.cpu().numpy()
+    a, b = m[:, 0:1], m[:, 1:2]
+    j = np.ascontiguousarray(m[:, 2]).view(np.int32)[:, None]
+    idx = np.arange(x.shape[1])[None, :]
+    return (x < a) | ((x < b) & (idx <= j))
+
+
+def _divided(x: np.ndarray, temperature: np.ndarray, req: np.ndarray) -> np.ndarray:
+    t = temperature[req]
+    t = np.where(t == 0, 1.0, t).astype(np.float32)
+    return (torch.from_numpy(x) / torch.from_numpy(t).unsqueeze(-1)).numpy()
+
+
+def _check_against_oracle(xt, masked, ks, ps, label):
+    """masked (bool [P, V]) against the oracle's masks of the divided rows xt."""
+    ref = otp.apply_top_k_top_p(torch.from_numpy(xt), torch.from_numpy(ks),
+                                torch.from_numpy(ps)).numpy()
+    want = ~np.isfinite(ref) & np.isfinite(xt)
+    flips = 0
+    for r in range(xt.shape[0]):
+        if np.array_equal(masked[r], want[r]):
+            continue
+        k = int(ks[r])
+        k = k if 0 < k < xt.shape[1] else None
+        amb = otp.near_boundary(xt[r], k, float(ps[r]))
+        bad = (masked[r] != want[r]) & ~amb
+        assert not bad.any(), (label, r, np.nonzero(bad)[0][:10], ks[r], ps[r])
+        flips += int((masked[r] != want[r]).sum())
+    print(f"[{label}] rows={xt.shape[0]} boundary flips={flips}", flush=True)
+
+
+def _metadata(w):
+    return SamplingMetadata(temperature=w.temperature, all_greedy=False, all_random=False,
+                            top_k=w.top_k, top_p=w.top_p)
+
+
+@pytest.mark.parametrize("B", [96])
+def test_c4_masks_match_processed_path_and_oracle(device, B):
+    w = configs.ragged_c4(device, B=B)
+    sm = _metadata(w)
+    masks = sampling_masks(w.target_logits, w.cu_num_draft_tokens, sm)
+    x = w.target_logits.float()
+    x_cpu = x.cpu().numpy()
+    got = _expand(masks, x_cpu)
+    processed = apply_sampling_constraints(x.clone(), w.cu_num_draft_tokens, sm)
+    want = ~torch.isfinite(processed).cpu().numpy()
+    assert np.array_equal(got, want), np.argwhere(got != want)[:10]
+    req = orc.request_of_row(w.num_draft_tokens)
+    xt = _divided(x_cpu, w.temperature.cpu().numpy(), req)
+    _check_against_oracle(xt, got, w.top_k.cpu().numpy()[req], w.top_p.cpu().numpy()[req],
+                          "c4 in-kernel masks")
+
+
+def test_c4_in_kernel_constraints_then_verify(device):
+    """rejection_sample on the raw bf16 rows with the divide and the constraints in the
+    kernels, against the oracle sampler on the same rows masked by the processed path."""
+    w = configs.ragged_c4(device, B=128, seed=2024)
+    sm = _metadata(w)
+    out = rejection_sample(w.draft_token_ids, w.num_draft_tokens, w.max_spec_len,
+                           w.cu_num_draft_tokens, w.draft_probs, w.target_logits,
+                           w.bonus_token_ids, sm, uniform_probs=w.uniforms,
+                           exp_noise=w.exp_noise, apply_temperature=True,
+                           apply_top_k_top_p=True)
+    processed = apply_sampling_constraints(w.target_logits.float(), w.cu_num_draft_tokens, sm)
+    ref = orc.rejection_sample(w.draft_token_ids.cpu(), w.num_draft_tokens, w.max_spec_len,
+                               w.draft_probs.cpu(), processed.cpu(), w.bonus_token_ids.cpu(),
+                               temperature=w.temperature.cpu(), all_greedy=False,
+                               uniforms=w.uniforms.cpu(), exp_noise=w.exp_noise.cpu(),
+                               apply_temperature=False)
+    rep = orc.compare(out.cpu().numpy(), ref, w.draft_token_ids.cpu(), w.num_draft_tokens)
+    print(f"[c4 in-kernel constraints] requests={rep.requests} mismatched={rep.mismatched} "
+          f"accept_flips={rep.accept_flips} recovered_flips={rep.recovered_flips}", flush=True)
+    assert not rep.unexplained, rep.unexplained[:5]
+
+
+def _single_request_rows(device, x: np.ndarray, temps, ks, ps, dtype=torch.float32):
+    """One verify row per request: (target, cu, metadata) for rows x [n, V]."""
+    n = x.shape[0]
+    target = torch.from_numpy(x).to(device=device, dtype=dtype)
+    cu = torch.arange(1, n + 1, dtype=torch.int32, device=device)
+    sm = SamplingMetadata(temperature=torch.tensor(temps, dtype=torch.float32, device=device),
+                          all_greedy=False, all_random=False,
+                          top_k=torch.tensor(ks, dtype=torch.int64, device=device),
+                          top_p=torch.tensor(ps, dtype=torch.float32, device=device))
+    return target, cu, sm
+
+
+def test_temperature_merging_neighbours(device):
+    """Raw values one ulp apart that the divide by T maps to one value: the masks on the raw
+    rows treat them as the equal values the processed rows hold (ties by index)."""
+    V = 2048
+    g = np.random.default_rng(5)
+    base = g.normal(0, 2, size=(24, V)).astype(np.float32)
+    pairs = g.integers(0, V, size=(24, 400))
+    for r in range(24):
+        src, dst = pairs[r, :200], pairs[r, 200:]
+        base[r, dst] = np.nextafter(base[r, src], np.float32(np.inf))
+    temps = [3.0, 0.7, 1.3, 2.9] * 6
+    ks = [V, 7, 50, 300, V, 1] * 4
+    ps = [0.5, 1.0, 0.9, 1.0, 0.95, 1.0] * 4
+    target, cu, sm = _single_request_rows(device, base, temps, ks, ps)
+    masks = sampling_masks(target, cu, sm)
+    got = _expand(masks, base)
+    processed = apply_sampling_constraints(target.clone(), cu, sm)
+    want = ~torch.isfinite(processed).cpu().numpy()
+    assert np.array_equal(got, want), np.argwhere(got != want)[:10]
+    xt = _divided(base, np.array(temps, dtype=np.float32), np.arange(24))
+    _check_against_oracle(xt, got, np.array(ks), np.array(ps, dtype=np.float32), "merged")
+
+
+@pytest.mark.parametrize("case", ["k_above_512", "all_equal_k", "all_equal_p", "p_all"])
+def test_fallback_paths(device, case):
+    """The bisection fallbacks (k > 512, more tied candidates or bin entries than LDS holds)
+    and the every-entry-but-one case, through the in-place op and the row masks."""
+    V = 8192
+    g = np.random.default_rng(11)
+    if case == "k_above_512":
+        x = g.normal(0, 2, size=(8, V)).astype(np.float32)
+        ks, ps = [600, 1000, 4000, 8000, 513, 2048, 777, 5000], [1.0] * 4 + [0.9, 0.5, 0.99, 0.3]
+    elif case == "all_equal_k":
+        x = np.zeros((4, V), dtype=np.float32)
+        x[1, ::3] = 1.0
+        x[2] = np.round(g.normal(0, 1, size=V)).astype(np.float32)
+        ks, ps = [50, 5000, 100, 4097], [1.0, 1.0, 0.6, 1.0]
+    elif case == "all_equal_p":
+        x = np.zeros((4, V), dtype=np.float32)
+        x[1, : V // 2] = -0.5
+        x[2] = np.round(g.normal(0, 0.2, size=V) * 4) / 4
+        x[3, 100:] = -1e-3
+        ks, ps = [V, V, V, V], [0.5, 0.3, 0.7, 0.1]
+    else:
+        x = g.normal(0, 2, size=(4, V)).astype(np.float32)
+        x[3, [10, 20, 30]] = x[3].max() + 1.0
+        ks, ps = [V, 100, V, V], [1e-9, 1e-9, -0.5, 1e-9]
+    temps = [1.0] * x.shape[0]
+    ks_np, ps_np = np.array(ks, dtype=np.int64), np.array(ps, dtype=np.float32)
+    xg = torch.from_numpy(x).to(device)
+    apply_top_k_top_p(xg, torch.from_numpy(ks_np).to(device), torch.from_numpy(ps_np).to(device))
+    inplace = ~torch.isfinite(xg).cpu().numpy()
+    target, cu, sm = _single_request_rows(device, x, temps, ks, ps)
+    got = _expand(sampling_masks(target, cu, sm), x)
+    assert np.array_equal(got, inplace)
+    _check_against_oracle(x, got, ks_np, ps_np, case)
+
+
+def test_greedy_row_argmax_respects_top_p_tie_order(device):
+    """A greedy request in a mixed batch is masked too (the reference divides by 1 and masks
+    every row): with a tiny top_p only the last of the tied maxima survives, so the greedy
+    token is that entry, not the first maximum."""
+    V = 4096
+    g = np.random.default_rng(3)
+    x = g.normal(0, 1, size=(3, V)).astype(np.float32)
+    x[0, [5, 10, 700]] = 9.0
+    draft_ids = torch.tensor([5, 700, 1], dtype=torch.int32, device=device)
+    cu = torch.tensor([1, 3], dtype=torch.int32, device=device)
+    target = torch.from_numpy(x).to(device)
+    temperature = torch.tensor([0.0, 0.9], dtype=torch.float32, device=device)
+    sm = SamplingMetadata(temperature=temperature, all_greedy=False, all_random=False,
+                          top_k=torch.tensor([V, 20], dtype=torch.int64, device=device),
+                          top_p=torch.tensor([1e-7, 1.0], dtype=torch.float32, device=device))
+    draft_probs = torch.softmax(torch.from_numpy(x).to(device) / 0.9, dim=-1)
+    uniforms = torch.tensor([0.5, 0.5, 0.5], dtype=torch.float64, device=device)
+    noise = torch.empty((2, V), device=device).exponential_()
+    bonus = torch.tensor([[1], [2]], dtype=torch.int32, device=device)
+    out = rejection_sample(draft_ids, [1, 2], 2, cu, draft_probs, target, bonus, sm,
+                           uniform_probs=uniforms, exp_noise=noise, apply_temperature=True,
+                           apply_top_k_top_p=True)
+    processed = apply_sampling_constraints(target.clone(), cu, sm)
+    ref = orc.rejection_sample(draft_ids.cpu(), [1, 2], 2, draft_probs.cpu(), processed.cpu(),
+                               bonus.cpu(), temperature=temperature.cpu(), all_greedy=False,
+                               uniforms=uniforms.cpu(), exp_noise=noise.cpu(),
+                               apply_temperature=False)
+    o = out.cpu().numpy()
+    assert o[0, 0] == 700, o[0]
+    rep = orc.compare(o, ref, draft_ids.cpu(), [1, 2])
+    assert not rep.unexplained, rep.unexplained
+
+
+def test_division_selftest(device):
+    failures = torch.zeros(1, dtype=torch.int64, device=device)
+    nat.check(nat.lib().mvsd_selftest(1, failures.data_ptr(), nat.stream_of(device)),
+              "mvsd_selftest")
+    assert int(failures.item()) == 0

@@ -11,7 +11,6 @@
 #include "mvsd_device.h"
 #include "rows.h"
 #include "selftest.h"
-#include "topk.h"
 #include "verify.h"
 
 namespace {
@@ -45,17 +44,18 @@ constexpr int kMaxDevices = 64;
 
 // Resident-workgroup capacity of a verify kernel per device, dtype and kernel kind
 // (CUs x occupancy).
-int verify_capacity(int device, int dtype, bool fused, bool has_draft) {
+int verify_capacity(int device, int dtype, bool fused, bool has_draft, bool masked) {
   static std::mutex mu;
-  static int cache[kMaxDevices][3][4];
+  static int cache[kMaxDevices][3][8];
   if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2) return 0;
+  if (fused && masked) return 0;
   std::lock_guard<std::mutex> lock(mu);
-  int& slot = cache[device][dtype][(fused ? 2 : 0) + (has_draft ? 1 : 0)];
+  int& slot = cache[device][dtype][(masked ? 4 : 0) + (fused ? 2 : 0) + (has_draft ? 1 : 0)];
   if (slot > 0) return slot;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     return 0;
-  const void* fn = mvsd::verify_kernel_ptr(dtype, fused, has_draft);
+  const void* fn = mvsd::verify_kernel_ptr(dtype, fused, has_draft, masked);
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, mvsd::kVThreads, 0) != hipSuccess)
     return 0;
@@ -81,7 +81,7 @@ int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 // Workspace layout.  ctrl = {ticket, sticky spin-limit flag (byte offset 4), exit counter}.
 struct WorkspaceLayout {
-  int64_t ctrl, grp_off, grp_desc, req_cnt, queues, qgi, stat_slots, arg_slots, total;
+  int64_t ctrl, grp_off, grp_desc, req_cnt, queues, qgi, masks, stat_slots, arg_slots, total;
 };
 
 WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
@@ -99,6 +99,8 @@ WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
   off = align_up(off + 3 * mvsd::kMaxQueues * 4, 256);
   l.qgi = off;
   off = align_up(off + (P > 0 ? P : 1) * 4, 256);
+  l.masks = off;  // row masks of the sampling constraints (written before use, not cleared)
+  off = align_up(off + (P > 0 ? P : 1) * 16, 256);
   l.stat_slots = off;
   off = align_up(off + P * nc * 8, 256);
   l.arg_slots = off;
@@ -188,6 +190,8 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   // that need recovered scores, when its progress condition (resident workgroups >= chunks
   // per row) and its load-width requirements hold.
   const int two_phase = (!a->all_greedy && !a->recovered_token_ids) ? 1 : 0;
+  // Sampling constraints apply only when some request samples (rejection_sampler.py:549-550).
+  const bool masked = !a->all_greedy && (a->top_k || a->top_p);
   int cap = 0;
   bool fused = false;
   if (P > 0) {
@@ -202,14 +206,16 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
                         (!a->draft_probs || aligned16(a->draft_probs, a->draft_stride * 4)) &&
                         V % (16 / esz) == 0;
     const char* mode = getenv("MVSD_VERIFY_MODE");
-    if (two_phase && vec_ok && mode && strcmp(mode, "fused") == 0) {
-      const int fcap = verify_capacity(device, a->target_dtype, true, a->draft_probs != nullptr);
+    if (two_phase && vec_ok && !masked && mode && strcmp(mode, "fused") == 0) {
+      const int fcap = verify_capacity(device, a->target_dtype, true, a->draft_probs != nullptr,
+                                       false);
       if (fcap >= size_plan.nsub && fcap > 0) {
         fused = true;
         cap = fcap;
       }
     }
-    if (!fused) cap = verify_capacity(device, a->target_dtype, false, a->draft_probs != nullptr);
+    if (!fused)
+      cap = verify_capacity(device, a->target_dtype, false, a->draft_probs != nullptr, masked);
     if (cap <= 0) return hip_status(hipErrorInvalidDevice);
   }
   // Upper bound on groups: min(P, B * ceil(max_spec_len / G)).
@@ -266,6 +272,9 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   int nq = 1;
   if (const char* env = getenv("MVSD_VERIFY_QUEUES")) nq = atoi(env);
   p.nq = nq < 1 ? 1 : (nq > mvsd::kMaxQueues ? mvsd::kMaxQueues : nq);
+  p.top_k = masked ? a->top_k : nullptr;
+  p.top_p = masked ? a->top_p : nullptr;
+  p.masks = masked ? reinterpret_cast<float4*>(ws + lay.masks) : nullptr;
   p.stat_slots = reinterpret_cast<uint64_t*>(ws + lay.stat_slots);
   p.arg_slots = reinterpret_cast<uint64_t*>(ws + lay.arg_slots);
 
@@ -298,9 +307,51 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
 
 int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream) {
   if (!failures) return MVSD_E_INVALID;
-  if (test != 0) return MVSD_E_INVALID;
-  return hip_status(mvsd::launch_selftest_reciprocal(
-      reinterpret_cast<unsigned long long*>(failures), (hipStream_t)stream));
+  unsigned long long* f = reinterpret_cast<unsigned long long*>(failures);
+  if (test == 0) return hip_status(mvsd::launch_selftest_reciprocal(f, (hipStream_t)stream));
+  if (test == 1) {
+    // temperatures of the kind requests carry, both ends of the fast range, and divisors
+    // outside it (IEEE path), plus 1 (greedy rows)
+    static const float divisors[] = {1.0f, 0.3f, 0.8f, 1.5f, 0.7f, 1.0f / 3.0f, 0.9999999f,
+                                     1.0000001f, 2.5f, 0.01f, 123.456f, 0x1p-20f, 0x1p20f,
+                                     0x1.fffffep-21f, 3e-7f, 5e6f};
+    return hip_status(mvsd::launch_selftest_division(
+        divisors, (int)(sizeof(divisors) / sizeof(divisors[0])), f, (hipStream_t)stream));
+  }
+  return MVSD_E_INVALID;
+}
+
+int mvsd_sampling_masks(const mvsd_rejection_args* a, float* masks, mvsd_stream_t stream) {
+  if (!a || !masks) return MVSD_E_INVALID;
+  const int64_t B = a->batch_size, P = a->num_tokens, V = a->vocab_size;
+  if (B < 0 || P < 0 || V <= 0) return MVSD_E_INVALID;
+  if (B > 0x7fffffff || P > 0x7fffffff || V > 0x7fffffff) return MVSD_E_RANGE;
+  if (P == 0) return MVSD_OK;
+  if (!a->target_logits || !a->cu_num_draft_tokens) return MVSD_E_INVALID;
+  if (a->target_dtype != MVSD_F32 && a->target_dtype != MVSD_BF16 && a->target_dtype != MVSD_F16)
+    return MVSD_E_INVALID;
+  if (!a->all_greedy && !a->temperature) return MVSD_E_INVALID;
+  if (a->target_stride < V) return MVSD_E_INVALID;
+  if (a->target_rows && a->target_num_rows < 1) return MVSD_E_INVALID;
+  if ((uintptr_t)masks % 16 != 0) return MVSD_E_ALIGN;
+  mvsd::VerifyParams p;
+  memset(&p, 0, sizeof(p));
+  p.target = a->target_logits;
+  p.target_stride = a->target_stride;
+  p.target_rows = a->target_rows;
+  p.target_num_rows = a->target_num_rows;
+  p.cu = a->cu_num_draft_tokens;
+  p.temperature = a->temperature;
+  p.target_dtype = a->target_dtype;
+  p.all_greedy = a->all_greedy ? 1 : 0;
+  p.apply_temperature = a->apply_temperature ? 1 : 0;
+  p.B = (int)B;
+  p.P = (int)P;
+  p.V = (int)V;
+  p.top_k = a->top_k;
+  p.top_p = a->top_p;
+  p.masks = reinterpret_cast<float4*>(masks);
+  return hip_status(mvsd::launch_constraints(p, a->target_dtype, (hipStream_t)stream));
 }
 
 int mvsd_apply_top_k_top_p(float* logits, int64_t logits_stride, const int64_t* top_k,

@@ -65,7 +65,37 @@ struct VerifyParams {
   int* qgi;              // [groups] group indices, queue-major
   uint64_t* stat_slots;  // [P * nc] packed (chunk max, chunk sumexp); 0 = empty
   uint64_t* arg_slots;   // [P * nc] packed (chunk argmax value, index + 1); 0 = empty
+  // Sampling constraints (top-k / top-p per request, either may be null).  When set, the
+  // constraints kernel writes one row mask per verify row, (A, B, J as bits, 0): entry i of
+  // the row, raw value x, is masked iff x < A || (x < B && i <= J).
+  const int64_t* top_k;  // [B]
+  const float* top_p;    // [B]
+  float4* masks;         // [P], null when no constraint applies
 };
+
+// Verify row j's row in the target tensor: target_rows[j] clamped to the tensor, or j.
+__device__ inline int64_t target_row(const VerifyParams& p, int row) {
+  if (!p.target_rows) return row;
+  const int64_t t = p.target_rows[row];
+  return t < 0 ? 0 : (t >= p.target_num_rows ? p.target_num_rows - 1 : t);
+}
+
+__device__ inline bool req_is_greedy(const VerifyParams& p, int r) {
+  return p.all_greedy || p.temperature[r] == 0.f;
+}
+
+// Temperature applied to request r's rows: 1 unless apply_temperature; 0 (greedy) -> 1
+// as expand_batch_to_tokens(replace_from=0, replace_to=1) does (rejection_sampler.py:553-559).
+__device__ inline float req_temperature(const VerifyParams& p, int r) {
+  if (!p.apply_temperature || p.all_greedy) return 1.f;
+  const float t = p.temperature[r];
+  return t == 0.f ? 1.f : t;
+}
+
+// Whether entry i (raw value x) of a row is masked by that row's constraints.
+__device__ inline bool row_masked(const float4& m, float x, int i) {
+  return (x < m.x) | ((x < m.y) & (i <= __float_as_int(m.z)));
+}
 
 struct VerifyPlan {
   int ept;    // elements per thread per row in one sub-chunk
@@ -81,10 +111,19 @@ struct VerifyPlan {
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int phases, int cap);
 // fused: the single-read kernel (one sub-chunk per task, scores computed by the workgroup that
 // loaded the target chunk); otherwise the split kernel (stats tasks, then score tasks that
-// re-read the target).
-const void* verify_kernel_ptr(int target_dtype, bool fused, bool has_draft);
+// re-read the target).  masked: the variant that applies the row masks (split kernel only;
+// null for the fused kernel).
+const void* verify_kernel_ptr(int target_dtype, bool fused, bool has_draft, bool masked);
 hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream);
 hipError_t launch_verify(const VerifyParams& params, int target_dtype, bool fused, int grid,
                          hipStream_t stream);
+// One workgroup per verify row: writes params.masks from top_k / top_p (constraints.hip).
+hipError_t launch_constraints(const VerifyParams& params, int target_dtype, hipStream_t stream);
+// Top-k / top-p masking in place on fp32 rows logits + r * stride, r < num_rows (one request
+// per row, no temperature): masked entries become -inf.  top_k [num_rows] int64 or null;
+// top_p [num_rows] fp32 or null.
+hipError_t launch_topk_topp(float* logits, int64_t stride, const int64_t* top_k,
+                            const float* top_p, int64_t num_rows, int64_t vocab_size,
+                            hipStream_t stream);
 
 }  // namespace mvsd

@@ -58,45 +58,6 @@ __device__ inline void req_range(const VerifyParams& p, int r, int& begin, int& 
   K = min(e - b, p.max_spec_len);
 }
 
-__device__ inline int64_t target_row(const VerifyParams& p, int row) {
-  if (!p.target_rows) return row;
-  const int64_t t = p.target_rows[row];
-  return t < 0 ? 0 : (t >= p.target_num_rows ? p.target_num_rows - 1 : t);
-}
-
-__device__ inline bool req_is_greedy(const VerifyParams& p, int r) {
-  return p.all_greedy || p.temperature[r] == 0.f;
-}
-
-// Temperature applied to request r's rows: 1 unless apply_temperature; 0 (greedy) -> 1
-// as expand_batch_to_tokens(replace_from=0, replace_to=1) does (rejection_sampler.py:553-559).
-__device__ inline float req_temperature(const VerifyParams& p, int r) {
-  if (!p.apply_temperature || p.all_greedy) return 1.f;
-  const float t = p.temperature[r];
-  return t == 0.f ? 1.f : t;
-}
-
-// x / t, correctly rounded, given rt = 1 / t correctly rounded (Markstein's correction:
-// q0 = x * rt is within an ulp, the FMA residual x - q0 * t is exact, and q0 + residual * rt
-// rounds to the IEEE quotient).  Three VALU ops instead of the ten of the IEEE sequence.
-__device__ inline float div_by(float x, float t, float rt) {
-  const float q0 = x * rt;
-  return fmaf(fmaf(-q0, t, x), rt, q0);
-}
-
-// exp(d) for d <= 0 (or -inf): 2^(d log2 e) with the product split into a rounded head and
-// an FMA-recovered tail so large |d| keeps full accuracy; ~1.5 ulp.
-__device__ inline float exp_le0(float d) {
-  constexpr float kLog2e = 1.44269502925872802734375f;      // RN(log2 e)
-  constexpr float kLog2eLo = 1.925963033500011079e-08f;     // log2 e - kLog2e
-  constexpr float kLn2 = 0.693147180559945309f;
-  d = fmaxf(d, -200.f);  // exp(-200) underflows to 0; keeps the tail finite for -inf
-  const float t = d * kLog2e;
-  const float lo = fmaf(d, kLog2eLo, fmaf(d, kLog2e, -t));
-  const float e = __builtin_amdgcn_exp2f(t);
-  return fmaf(e, lo * kLn2, e);
-}
-
 // log2(e) / T rounded once from double.
 __device__ inline float exp2_scale(float temp) {
   return (float)(1.4426950408889634074 / (double)temp);
@@ -351,7 +312,8 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
           x = Elem<MVSD_F16>::cvt(static_cast<const _Float16*>(p.target)[trow * p.target_stride + d]);
         }
         const float temp = req_temperature(p, r);
-        const float pd = expf(x / temp - sm.M[pos] / temp) / sm.S[pos];
+        float pd = expf(x / temp - sm.M[pos] / temp) / sm.S[pos];
+        if (p.masks && row_masked(p.masks[row], x, d)) pd = 0.f;  // -inf after the constraints
         accepted = q > 0.f && (double)(pd / q) >= u;
       }
       token = accepted ? d : sm.tok[pos];
@@ -580,13 +542,24 @@ __device__ inline auto target_loader(const VerifyParams& p, const typename Elem<
   };
 }
 
-// Greedy task: chunk-local argmax of the raw logits (NaN first, lowest index wins).
-template <int DT, int EPT, int G, typename Hook>
+// Row masks of the group's rows (rows past nrows repeat the last row).
+template <bool MASKED, int G>
+__device__ inline void row_masks(const VerifyParams& p, int row0, int nrows, float4 (&mk)[G]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    mk[g] = MASKED ? p.masks[row0 + min(g, nrows - 1)] : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// Greedy task: chunk-local argmax of the raw logits (NaN first, lowest index wins); with
+// MASKED, entries masked by the row's sampling constraints count as -inf.
+template <int DT, int EPT, int G, bool MASKED, typename Hook>
 __device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int nrows, int64_t v0,
                                    int64_t vend, uint64_t* s_key, Hook&& after_loads) {
   using S = typename Elem<DT>::storage;
   const S* tb[G];
   target_bases<DT, G>(p, row0, nrows, tb);
+  float4 mk[G];
+  row_masks<MASKED, G>(p, row0, nrows, mk);
   float bv[G];
   int bi[G];
 #pragma unroll
@@ -601,7 +574,8 @@ __device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int n
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
           const int idx = elem_index<DT, EPT>(s0, k);
-          const float v = raw_elem<DT>(buf.x[g], k);
+          float v = raw_elem<DT>(buf.x[g], k);
+          if constexpr (MASKED) v = row_masked(mk[g], v, idx) ? -INFINITY : v;
           // columns rise with s0 and k: a strict compare keeps the first maximum; NaN wins
           const bool take = ((v > bv[g]) | ((v != v) & (bv[g] == bv[g]))) &
                             (decltype(fast)::value || idx < vend);
@@ -622,20 +596,25 @@ __device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int n
 }
 
 // A-task: per row of the group, the chunk's raw max mx and sum of exp2((x - mx) * c1), kept
-// online per thread (the running sum is rescaled when the thread's max grows).
-template <int DT, int EPT, int G, typename Hook>
+// online per thread (the running sum is rescaled when the thread's max grows).  With MASKED,
+// entries masked by the row's sampling constraints add nothing to the sum; the maximum still
+// runs over every entry, which only moves the reference point of the exponentials (the
+// largest value of a row is never masked).
+template <int DT, int EPT, int G, bool MASKED, typename Hook>
 __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int row0, int nrows,
                                   int64_t v0, int64_t vend, float* s_red, Hook&& after_loads) {
   using S = typename Elem<DT>::storage;
   const S* tb[G];
   target_bases<DT, G>(p, row0, nrows, tb);
+  float4 mk[G];
+  row_masks<MASKED, G>(p, row0, nrows, mk);
   float m[G], s[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
     s[g] = 0.f;
   }
-  auto body = [&](const TargetBuf<DT, EPT, G>& buf, int64_t, auto) {
+  auto body = [&](const TargetBuf<DT, EPT, G>& buf, int64_t s0, auto) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       if (g < nrows) {
@@ -653,7 +632,11 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
         const float ref = m[g] == -INFINITY ? 0.f : m[g];
         float acc = 0.f;
 #pragma unroll
-        for (int k = 0; k < EPT; ++k) acc += __builtin_amdgcn_exp2f((x[k] - ref) * c1);
+        for (int k = 0; k < EPT; ++k) {
+          const float e = __builtin_amdgcn_exp2f((x[k] - ref) * c1);
+          if constexpr (MASKED) acc += row_masked(mk[g], x[k], elem_index<DT, EPT>(s0, k)) ? 0.f : e;
+          else acc += e;
+        }
         s[g] += acc;
       }
     }
@@ -679,7 +662,7 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
 // B-task: per row of the group, the chunk-local argmax of max(p - q, 0) * (1 / E).  The
 // group's stats were published by A-tasks holding lower tickets; the wait for them overlaps
 // with the first sub-chunk's loads.
-template <int DT, int EPT, int G, bool HAS_DRAFT, typename Hook>
+template <int DT, int EPT, int G, bool HAS_DRAFT, bool MASKED, typename Hook>
 __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1, int row0,
                                    int nrows, int64_t v0, int64_t vend, uint64_t* s_key,
                                    float* s_M, float* s_L, Hook&& after_loads) {
@@ -687,6 +670,8 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
   using Buf = ScoreBuf<DT, EPT, G>;
   const S* tb[G];
   target_bases<DT, G>(p, row0, nrows, tb);
+  float4 mk[G];
+  row_masks<MASKED, G>(p, row0, nrows, mk);
   const float* qb[G];
   int d[G];
 #pragma unroll
@@ -755,7 +740,8 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
         for (int k = 0; k < EPT; ++k) {
           const int idx = elem_index<DT, EPT>(s0, k);
           const float x = raw_elem<DT>(buf.x[g], k);
-          const float prob = __builtin_amdgcn_exp2f(fmaf(x - MX[g], c1, NL[g]));  // softmax
+          float prob = __builtin_amdgcn_exp2f(fmaf(x - MX[g], c1, NL[g]));  // softmax
+          if constexpr (MASKED) prob = row_masked(mk[g], x, idx) ? 0.f : prob;
           float w;
           if constexpr (HAS_DRAFT) w = prob - raw_f32(buf.q[g], k);  // clamp folded into bv >= 0
           else w = idx == d[g] ? 0.f : prob;
@@ -841,7 +827,7 @@ __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, i
   dst[6] = d.w;
 }
 
-template <int DT, int EPT, int G, bool HAS_DRAFT>
+template <int DT, int EPT, int G, bool HAS_DRAFT, bool MASKED>
 __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(VerifyParams p) {
   static_assert(EPT % Elem<DT>::kVec == 0, "EPT must be a multiple of the vector width");
   __shared__ float s_red[G * kVWaves];
@@ -910,12 +896,12 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
     const int64_t v0 = (int64_t)c * p.chunk;
     const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
     if (greedy) {
-      task_argmax<DT, EPT, G>(p, c, row0, nrows, v0, vend, s_key, prefetch);
+      task_argmax<DT, EPT, G, MASKED>(p, c, row0, nrows, v0, vend, s_key, prefetch);
     } else if (!phase_b) {
-      task_stats<DT, EPT, G>(p, c, c1, row0, nrows, v0, vend, s_red, prefetch);
+      task_stats<DT, EPT, G, MASKED>(p, c, c1, row0, nrows, v0, vend, s_red, prefetch);
     } else {
-      task_scores<DT, EPT, G, HAS_DRAFT>(p, c, r, c1, row0, nrows, v0, vend, s_key, s_M, s_L,
-                                         prefetch);
+      task_scores<DT, EPT, G, HAS_DRAFT, MASKED>(p, c, r, c1, row0, nrows, v0, vend, s_key, s_M,
+                                                 s_L, prefetch);
     }
     // ---- request completion: the last counted task runs the accept/reject chain ----
     // (counted: B-tasks of full random requests, A-tasks otherwise).  The counter's result
@@ -1394,20 +1380,25 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int
 }
 
 template <int DT>
-const void* kernel_for(bool fused, bool has_draft) {
+const void* kernel_for(bool fused, bool has_draft, bool masked) {
   constexpr int E = ept_of<DT>();
-  if (!fused)
-    return has_draft ? reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, true>)
-                     : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false>);
+  if (!fused) {
+    if (masked)
+      return has_draft ? reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, true, true>)
+                       : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false, true>);
+    return has_draft ? reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, true, false>)
+                     : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false, false>);
+  }
+  if (masked) return nullptr;  // the single-read kernel does not apply sampling constraints
   return has_draft ? reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, true>)
                    : reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, false>);
 }
 
-const void* verify_kernel_ptr(int target_dtype, bool fused, bool has_draft) {
+const void* verify_kernel_ptr(int target_dtype, bool fused, bool has_draft, bool masked) {
   switch (target_dtype) {
-    case MVSD_F32: return kernel_for<MVSD_F32>(fused, has_draft);
-    case MVSD_BF16: return kernel_for<MVSD_BF16>(fused, has_draft);
-    case MVSD_F16: return kernel_for<MVSD_F16>(fused, has_draft);
+    case MVSD_F32: return kernel_for<MVSD_F32>(fused, has_draft, masked);
+    case MVSD_BF16: return kernel_for<MVSD_BF16>(fused, has_draft, masked);
+    case MVSD_F16: return kernel_for<MVSD_F16>(fused, has_draft, masked);
     default: return nullptr;
   }
 }
@@ -1417,7 +1408,12 @@ hipError_t launch_verify(const VerifyParams& params, int target_dtype, bool fuse
   hipLaunchKernelGGL(verify_init_kernel, dim3(1), dim3(1024), 0, stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.P == 0) return err;
-  const void* fn = verify_kernel_ptr(target_dtype, fused, params.draft != nullptr);
+  if (params.masks) {
+    err = launch_constraints(params, target_dtype, stream);
+    if (err != hipSuccess) return err;
+  }
+  const void* fn = verify_kernel_ptr(target_dtype, fused, params.draft != nullptr,
+                                     params.masks != nullptr);
   if (!fn) return hipErrorInvalidValue;
   void* args[] = {const_cast<VerifyParams*>(&params)};
   err = hipLaunchKernel(fn, dim3(grid), dim3(kVThreads), args, 0, stream);

@@ -65,6 +65,8 @@ class RejectionArgs(ctypes.Structure):
         ("max_spec_len", c_int64),
         ("workspace", c_void_p),
         ("workspace_bytes", c_int64),
+        ("top_k", c_void_p),
+        ("top_p", c_void_p),
     ]
 
 
@@ -81,6 +83,7 @@ SIGNATURES = {
     "mvsd_apply_top_k_top_p": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                                        c_void_p]),
     "mvsd_selftest": (c_int, [c_int, c_void_p, c_void_p]),
+    "mvsd_sampling_masks": (c_int, [ctypes.POINTER(RejectionArgs), c_void_p, c_void_p]),
     "mvsd_softmax_rows": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int64, c_void_p, c_int64,
                                   c_int64, c_void_p]),
     "mvsd_sample_recovered_tokens": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64,

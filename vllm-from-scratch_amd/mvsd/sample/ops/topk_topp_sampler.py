@@ -1,7 +1,9 @@
 """top-k / top-p masking (drop-in for minivllm/sample/ops/topk_topp_sampler.py:48-79).
 
-One HIP workgroup per row (``mvsd_apply_top_k_top_p``): radix selection of the k-th largest
-value and of the top-p crossing point, then one masking pass — no sort of the vocabulary.
+One HIP workgroup per row (``mvsd_apply_top_k_top_p``): the k-th largest value from the
+entries at or above the k-th largest per-thread maximum, gathered and sorted in LDS; the
+top-p crossing from a logarithmic mass histogram and the entries of the crossing bin; then one
+masking pass -- no sort of the vocabulary.
 """
 
 from __future__ import annotations
@@ -22,7 +24,8 @@ def apply_top_k_top_p(logits: torch.Tensor, k: torch.Tensor | None,
     the top-k-masked row drop the ascending prefix whose cumulative probability is <= 1 - p,
     always keeping the largest entry.  Equal values are ordered by index (a stable sort).
     ``logits`` must be a 2-D fp32 device tensor whose rows are contiguous; the reference's
-    callers guarantee 0 < k < V, and here k >= V (rows without top-k) keeps the row.
+    callers guarantee 0 < k < V, and here k >= V (rows without top-k) keeps the row.  p >= 1
+    keeps the row (the reference's p = 1 masks only entries whose fp32 probability is 0).
     """
     if k is None and p is None:
         return logits

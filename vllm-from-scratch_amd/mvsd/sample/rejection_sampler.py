@@ -106,18 +106,24 @@ class RejectionSampler:
                                     else "raw_logits"))
         bonus_token_ids = bonus_out.sampled_token_ids
 
+        constrained = (sampling_metadata.top_k is not None
+                       or sampling_metadata.top_p is not None)
         needs_processing = (not sampling_metadata.no_penalties
                             or _has_active_min_tokens(sampling_metadata)
-                            or sampling_metadata.top_k is not None
-                            or sampling_metadata.top_p is not None)
+                            # a replaced recovered-token seam receives materialised
+                            # probabilities, which must carry the constraints
+                            or (constrained
+                                and sample_recovered_tokens is not _SAMPLE_RECOVERED_TOKENS))
         if not needs_processing:
-            # 2+3 fused: gather, fp32 upcast and temperature divide happen in the kernel
+            # 2+3 fused: gather, fp32 upcast, temperature divide and top-k / top-p happen in
+            # the kernels (the constraints become per-row thresholds on the raw rows)
             output_token_ids = rejection_sample(
                 metadata.draft_token_ids, metadata.num_draft_tokens, metadata.max_spec_len,
                 metadata.cu_num_draft_tokens, draft_probs, logits, bonus_token_ids,
                 sampling_metadata, synthetic_mode=self.synthetic_mode,
                 synthetic_conditional_rates=self.synthetic_conditional_rates,
-                target_rows=metadata.target_logits_indices, apply_temperature=True)
+                target_rows=metadata.target_logits_indices, apply_temperature=True,
+                apply_top_k_top_p=constrained)
         else:
             target_logits = logits[metadata.target_logits_indices].to(torch.float32)
             target_logits = self.apply_logits_processors(target_logits, sampling_metadata,
@@ -181,6 +187,7 @@ def rejection_sample(
     exp_noise: torch.Tensor | None = None,
     target_rows: torch.Tensor | None = None,
     apply_temperature: bool = False,
+    apply_top_k_top_p: bool = False,
 ) -> torch.Tensor:
     """Verify a batch of drafts; returns ``[B, max_spec_len + 1]`` int32, -1 padded.
 
@@ -190,7 +197,9 @@ def rejection_sample(
       * ``target_rows`` [P] int32 selects verify row j as ``target_logits[target_rows[j]]``
         (no gather copy), and ``apply_temperature`` divides by the request temperature in the
         kernel (greedy T = 0 -> 1), which together replace the gather + ``div_`` that
-        RejectionSampler.forward runs before this function.
+        RejectionSampler.forward runs before this function;
+      * ``apply_top_k_top_p`` applies ``sampling_metadata.top_k`` / ``top_p`` to the (divided)
+        verify rows in the kernels, as ``apply_sampling_constraints`` (:563-571) would.
     """
     assert draft_token_ids.ndim == 1
     assert draft_probs is None or draft_probs.ndim == 2
@@ -225,9 +234,21 @@ def rejection_sample(
     if uniform_probs is None and (synthetic_mode or not all_greedy):
         uniform_probs = generate_uniform_probs(num_tokens, num_draft_tokens,
                                                sampling_metadata.generators, device)
+    top_k = top_p = None
+    if apply_top_k_top_p and not all_greedy:
+        if sampling_metadata.top_k is not None:
+            top_k = _as(sampling_metadata.top_k, torch.int64, device)
+            assert top_k.shape == (batch_size,)
+        if sampling_metadata.top_p is not None:
+            top_p = _as(sampling_metadata.top_p, torch.float32, device)
+            assert top_p.shape == (batch_size,)
     recovered_token_ids = None
     if not all_greedy and num_tokens > 0:
         if sample_recovered_tokens is not _SAMPLE_RECOVERED_TOKENS:
+            if top_k is not None or top_p is not None:
+                raise NotImplementedError(
+                    "a replaced sample_recovered_tokens needs processed logits: apply "
+                    "apply_sampling_constraints first instead of apply_top_k_top_p=True")
             # a caller replaced the seam: give it materialised probabilities, as the
             # reference does, and use the ids it returns
             target_probs = _softmax_rows(target_logits, target_rows,
@@ -301,9 +322,50 @@ def rejection_sample(
         max_spec_len=max_spec_len,
         workspace=workspace.data_ptr(),
         workspace_bytes=workspace.numel(),
+        top_k=nat.ptr(top_k),
+        top_p=nat.ptr(top_p),
     )
     nat.check(handle.mvsd_rejection_sample(args, nat.stream_of(device)), "mvsd_rejection_sample")
     return output_token_ids
+
+
+def sampling_masks(target_logits: torch.Tensor, cu_num_draft_tokens: torch.Tensor,
+                   sampling_metadata: SamplingMetadata, *,
+                   target_rows: torch.Tensor | None = None,
+                   apply_temperature: bool = True) -> torch.Tensor:
+    """The per-row masks ``rejection_sample(..., apply_top_k_top_p=True)`` applies.
+
+    Returns ``[P, 4]`` fp32: row j holds (A, B, J, 0) with J's int32 bits in the third column,
+    and entry i of verify row j (raw value x, before the temperature divide) is masked iff
+    ``x < A or (x < B and i <= J)`` -- the entries ``apply_sampling_constraints`` (:537-571)
+    would set to -inf.  Rows without constraints get (-inf, -inf, -1)."""
+    device = target_logits.device
+    nat.require_device_tensor(target_logits, "target_logits")
+    if target_logits.stride(1) != 1:
+        target_logits = target_logits.contiguous()
+    batch_size = cu_num_draft_tokens.shape[0]
+    num_tokens = (target_rows.shape[0] if target_rows is not None
+                  else target_logits.shape[0])
+    all_greedy = bool(sampling_metadata.all_greedy)
+    temperature = None if all_greedy else _as(sampling_metadata.temperature, torch.float32, device)
+    top_k = (None if sampling_metadata.top_k is None
+             else _as(sampling_metadata.top_k, torch.int64, device))
+    top_p = (None if sampling_metadata.top_p is None
+             else _as(sampling_metadata.top_p, torch.float32, device))
+    cu = _as(cu_num_draft_tokens, torch.int32, device)
+    rows = None if target_rows is None else _as(target_rows, torch.int32, device)
+    masks = torch.empty((num_tokens, 4), dtype=torch.float32, device=device)
+    args = nat.RejectionArgs(
+        target_logits=target_logits.data_ptr(), target_dtype=nat.dtype_code(target_logits.dtype),
+        target_stride=target_logits.stride(0), target_rows=nat.ptr(rows),
+        target_num_rows=target_logits.shape[0], cu_num_draft_tokens=cu.data_ptr(),
+        temperature=nat.ptr(temperature), all_greedy=int(all_greedy),
+        apply_temperature=int(bool(apply_temperature)), batch_size=batch_size,
+        num_tokens=num_tokens, vocab_size=target_logits.shape[-1], top_k=nat.ptr(top_k),
+        top_p=nat.ptr(top_p))
+    nat.check(nat.lib().mvsd_sampling_masks(args, masks.data_ptr(), nat.stream_of(device)),
+              "mvsd_sampling_masks")
+    return masks
 
 
 def apply_sampling_constraints(
