@@ -254,6 +254,8 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   p.max_spec_len = (int)a->max_spec_len;
   p.chunk = plan.chunk;
   p.nc = plan.nc;
+  p.split = 0;
+  p.arg_stride = plan.nc;
   p.G = plan.g;
   const int esz = elem_size(a->target_dtype);
   p.target_aligned = aligned16(a->target_logits, a->target_stride * esz);
@@ -299,6 +301,12 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
       p.lag = lag < 1 ? 1 : (lag > 4096 ? 4096 : lag);
       const int64_t step = p.two_phase ? 2 * plan.nc : plan.nc;
       tasks = (groups + (p.two_phase ? p.lag * p.nq : 0)) * step;
+      // Epilogue split (one queue): the score tasks of the last `lag` groups use the empty
+      // stats slots of their steps as a second half-chunk task each (MVSD_VERIFY_SPLIT=0
+      // turns it off).
+      p.split = p.two_phase && p.nq == 1 && 2 * plan.nc <= size_plan.nsub ? 1 : 0;
+      if (const char* env = getenv("MVSD_VERIFY_SPLIT")) p.split = p.split && atoi(env) != 0;
+      if (p.split) p.arg_stride = 2 * plan.nc;
     }
     if (tasks > 0x7fffffff - 2 * (int64_t)cap) return MVSD_E_RANGE;
   }

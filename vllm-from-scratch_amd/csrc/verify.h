@@ -52,8 +52,9 @@ struct VerifyParams {
   // workspace
   int* ctrl;             // [0] ticket, [1] sticky spin-limit flag, [2] exit counter
   int* grp_off;          // [B + 1] exclusive scan of groups per request
-  int4* grp_desc;        // [P] per group: request, first row, rows | groups << 8 | flags << 16,
-                         //     bits of log2(e) / T   (flags: 1 greedy, 2 needs recovered scores)
+  int4* grp_desc;        // [P] per group: request, first row, rows | groups << 8 | flags << 16
+                         //     | index within the request << 24, bits of log2(e) / T
+                         //     (flags: 1 greedy, 2 needs recovered scores)
   int* req_cnt;          // [B] finished tasks per request (zero between calls)
   // Work queues of the split kernel: request r belongs to queue r % nq, and workgroup w
   // serves queue w % nq (workgroups are dispatched round-robin over the XCDs, so a queue's
@@ -64,7 +65,11 @@ struct VerifyParams {
   int* qoff;             // [nq] offset of each queue's list in qgi
   int* qgi;              // [groups] group indices, queue-major
   uint64_t* stat_slots;  // [P * nc] packed (chunk max, chunk sumexp); 0 = empty
-  uint64_t* arg_slots;   // [P * nc] packed (chunk argmax value, index + 1); 0 = empty
+  uint64_t* arg_slots;   // [P * arg_stride] packed (chunk argmax value, index + 1); 0 = empty
+  // Epilogue split of the split kernel: the score tasks of the last `lag` groups (whose steps
+  // hold no stats tasks) cover half chunks, 2 * nc per row, so the final tasks are short.
+  int split;
+  int arg_stride;  // arg slots per row: 2 * nc with the split, else nc
   // Sampling constraints (top-k / top-p per request, either may be null).  When set, the
   // constraints kernel writes one row mask per verify row, (A, B, J as bits, 0): entry i of
   // the row, raw value x, is masked iff x < A || (x < B && i <= J).

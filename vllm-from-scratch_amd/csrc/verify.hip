@@ -122,8 +122,8 @@ __global__ __launch_bounds__(1024) void verify_init_kernel(VerifyParams p) {
         const int flags = (greedy ? kGreedy : 0) | (!greedy && !p.recovered ? kFull : 0);
         const int c1 = __float_as_int(exp2_scale(req_temperature(p, r)));
         for (int g = 0; g < ng; ++g)
-          p.grp_desc[first + g] =
-              make_int4(r, b + g * p.G, min(p.G, k - g * p.G) | ng << 8 | flags << 16, c1);
+          p.grp_desc[first + g] = make_int4(
+              r, b + g * p.G, min(p.G, k - g * p.G) | ng << 8 | flags << 16 | g << 24, c1);
       }
     }
     __syncthreads();
@@ -243,20 +243,24 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
   req_range(p, r, begin, K);
   const int lane = lane_id();
   const int nc = p.nc;
+  // first group scored in half chunks (2 * nc arg slots per row)
+  const int split_from = p.split && full ? p.grp_off[p.B] - p.lag : 0x7fffffff;
+  const int gfirst = p.grp_off[r];
   for (int k = wave_id(); k < K; k += kVWaves) {
     const int64_t row = begin + k;
-    uint64_t* aslots = p.arg_slots + row * nc;
+    uint64_t* aslots = p.arg_slots + row * p.arg_stride;
     uint64_t* sslots = p.stat_slots + row * nc;
     if (greedy || full) {
-      if (!wave_wait_slots(aslots, nc, kSpinLimit, &p.ctrl[1]) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
+      const int na = gfirst + k / p.G >= split_from ? 2 * nc : nc;
+      if (!wave_wait_slots(aslots, na, kSpinLimit, &p.ctrl[1]) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
       uint64_t best = 0;
-      for (int c = lane; c < nc; c += kWave) {
+      for (int c = lane; c < na; c += kWave) {
         const uint64_t k = slot_load(aslots + c);
         best = k > best ? k : best;
       }
       best = wave_max_u64(best);
       if (lane == 0) sm.tok[k] = min(max(key_index(best), 0), p.V - 1);
-      for (int c = lane; c < nc; c += kWave) slot_store(aslots + c, 0);
+      for (int c = lane; c < na; c += kWave) slot_store(aslots + c, 0);
     } else if (lane == 0) {
       sm.tok[k] = p.recovered[row];
     }
@@ -472,6 +476,9 @@ __device__ inline void pipeline(int64_t v0, int64_t vend, bool aligned, Load&& l
         if (++j == nfull) break;
       }
     } else {
+      // Sub-chunks 0 and 1 are both in flight before the hook (which may wait for the
+      // group's statistics); afterwards a buffer is reloaded with sub-chunk j + 2 as soon as
+      // sub-chunk j has been consumed.
       Buf a, b;
       load(a, at(0), Fast<true>());
       hook();
@@ -592,7 +599,7 @@ __device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int n
 #pragma unroll
   for (int g = 0; g < G; ++g) key[g] = argmax_key(bv[g], bi[g]);
   const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
-  if ((int)threadIdx.x < nrows) slot_store(p.arg_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c, best);
+  if ((int)threadIdx.x < nrows) slot_store(p.arg_slots + (int64_t)(row0 + threadIdx.x) * p.arg_stride + c, best);
 }
 
 // A-task: per row of the group, the chunk's raw max mx and sum of exp2((x - mx) * c1), kept
@@ -759,7 +766,7 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
 #pragma unroll
   for (int g = 0; g < G; ++g) key[g] = argmax_key(bv[g], bi[g]);
   const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
-  if ((int)threadIdx.x < nrows) slot_store(p.arg_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c, best);
+  if ((int)threadIdx.x < nrows) slot_store(p.arg_slots + (int64_t)(row0 + threadIdx.x) * p.arg_stride + c, best);
 }
 
 // ------------------------------------------------------------------ main kernel ------
@@ -796,26 +803,38 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
 // or the argmax for greedy groups) of group s; when the batch has random requests the next nc
 // are the B-chunks (scores) of group s - lag.  Slots of absent groups are claimed and skipped.
 struct TaskDecode {
-  int total, step_size, nc, lag, groups, two_phase;
+  int total, step_size, nc, lag, groups, two_phase, split;
   const int* qgi;  // queue position -> group index (nullptr: identity)
 };
 
-// Thread 0: decode ticket t and fetch its group descriptor into dst[0..6]
-// = {t, chunk, valid | phase_b << 1, request, first row, rows | groups << 8 | flags << 16,
-// bits of c1}.
+// Thread 0: decode ticket t and fetch its group descriptor into dst[0..7]
+// = {t, arg slot, valid | phase_b << 1 | half << 2, request, first row,
+// rows | groups << 8 | flags << 16 | index in request << 24, bits of c1, split groups of the
+// request}.  The arg slot is the chunk, or for a half-chunk task (the epilogue split) the half
+// index 2 * chunk + {0, 1}.
 __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, int t, int* dst) {
-  int c = 0, flags = 0;
+  int c = 0, flags = 0, nsplit = 0;
   int4 d = make_int4(0, 0, 0, 0);
   if (t < td.total) {
     const int step = t / td.step_size;
     const int w = t - step * td.step_size;
-    const bool phase_b = w >= td.nc;
-    c = phase_b ? w - td.nc : w;
+    // Steps past the last group hold no stats tasks: with the split, all 2 * nc of their
+    // tickets are half-chunk score tasks of group step - lag.
+    const bool half = td.split && step >= td.groups;
+    const bool phase_b = half || w >= td.nc;
+    c = (phase_b && !half) ? w - td.nc : w;
     const int li = phase_b ? step - td.lag : step;
     if (li >= 0 && li < td.groups) {
       d = p.grp_desc[td.qgi ? td.qgi[li] : li];
       const bool full = (d.z >> 16) & kFull;
-      flags = (!phase_b || full ? 1 : 0) | (phase_b ? 2 : 0);
+      flags = (!phase_b || full ? 1 : 0) | (phase_b ? 2 : 0) | (half ? 4 : 0);
+      if (td.split && full) {
+        // groups of this request at or past groups - lag score in half chunks
+        const int first = li - ((d.z >> 24) & 0xff);
+        const int ngr = (d.z >> 8) & 0xff;
+        const int lo = max(first, td.groups - td.lag);
+        nsplit = min(max(first + ngr - lo, 0), ngr);
+      }
     }
   }
   dst[0] = t;
@@ -825,6 +844,7 @@ __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, i
   dst[4] = d.y;
   dst[5] = d.z;
   dst[6] = d.w;
+  dst[7] = nsplit;
 }
 
 template <int DT, int EPT, int G, bool HAS_DRAFT, bool MASKED>
@@ -848,6 +868,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   td.groups = p.qcount[queue];
   td.qgi = p.nq > 1 ? p.qgi + p.qoff[queue] : nullptr;
   td.two_phase = p.two_phase;
+  td.split = p.split;
   td.step_size = p.two_phase ? 2 * td.nc : td.nc;
   td.total = (td.groups + (p.two_phase ? td.lag : 0)) * td.step_size;
 
@@ -889,12 +910,24 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
     const int row0 = info[4];
     const int nrows = info[5] & 0xff;
     const int ngr = (info[5] >> 8) & 0xff;
-    const int gflags = info[5] >> 16;
+    const int gflags = (info[5] >> 16) & 0xff;
     const float c1 = __int_as_float(info[6]);
+    const int nsplit = info[7];
     const bool greedy = gflags & kGreedy;
     const bool full = gflags & kFull;
-    const int64_t v0 = (int64_t)c * p.chunk;
-    const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
+    int64_t v0, vend;
+    if (tflags & 4) {
+      // half chunk: the first or second half of chunk c / 2, split at a sub-chunk boundary
+      const int64_t cs = (int64_t)(c >> 1) * p.chunk;
+      const int64_t ce = min((int64_t)p.V, cs + p.chunk);
+      constexpr int64_t SUB = (int64_t)kVThreads * EPT;
+      const int64_t mid = min(ce, cs + (((ce - cs + SUB - 1) / SUB + 1) / 2) * SUB);
+      v0 = (c & 1) ? mid : cs;
+      vend = (c & 1) ? ce : mid;
+    } else {
+      v0 = (int64_t)c * p.chunk;
+      vend = min((int64_t)p.V, v0 + p.chunk);
+    }
     if (greedy) {
       task_argmax<DT, EPT, G, MASKED>(p, c, row0, nrows, v0, vend, s_key, prefetch);
     } else if (!phase_b) {
@@ -910,7 +943,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
     if (full == phase_b) {
       if (tid == 0) pend_cnt = atomic_add_relaxed(&p.req_cnt[r], 1);
       pend_r = r;
-      pend_target = ngr * td.nc;
+      pend_target = (ngr + nsplit) * td.nc;  // half-chunk groups count 2 * nc tasks
       pend_greedy = greedy;
       pend_full = full;
     }
@@ -1006,7 +1039,7 @@ __device__ inline FusedTask ring_task(const TaskRing<G>& ring, int i) {
   t.row0 = a.z;
   t.nrows = a.w & 0xff;
   t.ngr = (a.w >> 8) & 0xff;
-  t.flags = a.w >> 16;
+  t.flags = (a.w >> 16) & 0xff;
   t.c1 = ring.c1[i % kRing];
   return t;
 }
@@ -1355,6 +1388,9 @@ template <int DT>
 constexpr int ept_of() {
   return DT == MVSD_F32 ? MVSD_VERIFY_EPT_F32 : MVSD_VERIFY_EPT_16;
 }
+#ifndef MVSD_VERIFY_MIN_SUBS
+#define MVSD_VERIFY_MIN_SUBS 5
+#endif
 #ifndef MVSD_VERIFY_TASKS_PER_WG
 #define MVSD_VERIFY_TASKS_PER_WG 16
 #endif
@@ -1366,10 +1402,14 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int
   plan.sub = kVThreads * plan.ept;
   plan.nsub = (int)((vocab_size + plan.sub - 1) / plan.sub);
   // Chunks per row: enough tasks for about MVSD_VERIFY_TASKS_PER_WG per resident workgroup,
-  // each task as long as possible (fewer ticket claims, longer load pipelines).
+  // each task as long as possible (fewer ticket claims, longer load pipelines), and at least
+  // MVSD_VERIFY_MIN_SUBS sub-chunks per task so that small batches do not shred the rows into
+  // tasks too short to amortise their start and end.
   int64_t nc = plan.nsub;
   if (groups > 0 && cap > 0) {
     nc = ((int64_t)MVSD_VERIFY_TASKS_PER_WG * cap + phases * groups - 1) / (phases * groups);
+    const int64_t nc_max = plan.nsub / MVSD_VERIFY_MIN_SUBS;
+    if (nc > nc_max) nc = nc_max;
     if (const char* env = getenv("MVSD_VERIFY_NC")) nc = atoi(env);
     nc = nc < 1 ? 1 : (nc > plan.nsub ? plan.nsub : nc);
   }
