@@ -44,18 +44,20 @@ constexpr int kMaxDevices = 64;
 
 // Resident-workgroup capacity of a verify kernel per device, dtype and kernel kind
 // (CUs x occupancy).
-int verify_capacity(int device, int dtype, bool fused, bool has_draft, bool masked) {
+int verify_capacity(int device, int dtype, int mode, bool has_draft, bool masked) {
   static std::mutex mu;
-  static int cache[kMaxDevices][3][8];
-  if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2) return 0;
-  if (fused && masked) return 0;
+  static int cache[kMaxDevices][3][2][4];
+  if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2 || mode < 0 || mode > 1)
+    return 0;
+  if (mode == mvsd::kModeFused && masked) return 0;
   std::lock_guard<std::mutex> lock(mu);
-  int& slot = cache[device][dtype][(masked ? 4 : 0) + (fused ? 2 : 0) + (has_draft ? 1 : 0)];
+  int& slot = cache[device][dtype][mode][(masked ? 2 : 0) + (has_draft ? 1 : 0)];
   if (slot > 0) return slot;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     return 0;
-  const void* fn = mvsd::verify_kernel_ptr(dtype, fused, has_draft, masked);
+  const void* fn = mvsd::verify_kernel_ptr(dtype, mode, has_draft, masked);
+  if (!fn) return 0;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, mvsd::kVThreads, 0) != hipSuccess)
     return 0;
@@ -193,7 +195,7 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   // Sampling constraints apply only when some request samples (rejection_sampler.py:549-550).
   const bool masked = !a->all_greedy && (a->top_k || a->top_p);
   int cap = 0;
-  bool fused = false;
+  int kmode = mvsd::kModeSplit;
   if (P > 0) {
     int device = 0;
     hipError_t err = hipGetDevice(&device);
@@ -207,22 +209,22 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
                         V % (16 / esz) == 0;
     const char* mode = getenv("MVSD_VERIFY_MODE");
     if (two_phase && vec_ok && !masked && mode && strcmp(mode, "fused") == 0) {
-      const int fcap = verify_capacity(device, a->target_dtype, true, a->draft_probs != nullptr,
-                                       false);
+      const int fcap = verify_capacity(device, a->target_dtype, mvsd::kModeFused,
+                                       a->draft_probs != nullptr, false);
       if (fcap >= size_plan.nsub && fcap > 0) {
-        fused = true;
+        kmode = mvsd::kModeFused;
         cap = fcap;
       }
     }
-    if (!fused)
-      cap = verify_capacity(device, a->target_dtype, false, a->draft_probs != nullptr, masked);
+    if (kmode != mvsd::kModeFused)
+      cap = verify_capacity(device, a->target_dtype, kmode, a->draft_probs != nullptr, masked);
     if (cap <= 0) return hip_status(hipErrorInvalidDevice);
   }
   // Upper bound on groups: min(P, B * ceil(max_spec_len / G)).
   int64_t groups = B * ((a->max_spec_len + size_plan.g - 1) / size_plan.g);
   if (groups > P) groups = P;
   mvsd::VerifyPlan plan = size_plan;
-  if (!fused)
+  if (kmode == mvsd::kModeSplit)
     plan = mvsd::verify_plan(a->target_dtype, V, groups > 0 ? groups : 1, two_phase ? 2 : 1, cap);
 
   char* ws = static_cast<char*>(a->workspace);
@@ -283,7 +285,7 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   int grid = 0;
   if (P > 0) {
     int64_t tasks;
-    if (fused) {
+    if (kmode == mvsd::kModeFused) {
       tasks = groups * plan.nc;
       grid = (int)(tasks < cap ? tasks : cap);
     } else {
@@ -308,9 +310,10 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
       if (const char* env = getenv("MVSD_VERIFY_SPLIT")) p.split = p.split && atoi(env) != 0;
       if (p.split) p.arg_stride = 2 * plan.nc;
     }
+    // every workgroup may claim two tickets past the last task
     if (tasks > 0x7fffffff - 2 * (int64_t)cap) return MVSD_E_RANGE;
   }
-  return hip_status(mvsd::launch_verify(p, a->target_dtype, fused, grid, (hipStream_t)stream));
+  return hip_status(mvsd::launch_verify(p, a->target_dtype, kmode, grid, (hipStream_t)stream));
 }
 
 int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream) {

@@ -111,16 +111,20 @@ struct VerifyPlan {
   int nc;     // chunks per row
 };
 
+// Verify kernels: the split kernel (stats tasks, then score tasks that re-read the target) and
+// the single-read fused kernel (one sub-chunk per task, scores computed by the workgroup that
+// loaded the target chunk).
+constexpr int kModeSplit = 0;
+constexpr int kModeFused = 1;
+
 // groups = 0 gives the workspace-sizing plan (nc = nsub).  phases is 2 when the batch needs
 // recovered scores (stats and score tasks per chunk), else 1; cap = resident workgroups.
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int phases, int cap);
-// fused: the single-read kernel (one sub-chunk per task, scores computed by the workgroup that
-// loaded the target chunk); otherwise the split kernel (stats tasks, then score tasks that
-// re-read the target).  masked: the variant that applies the row masks (split kernel only;
-// null for the fused kernel).
-const void* verify_kernel_ptr(int target_dtype, bool fused, bool has_draft, bool masked);
+
+// masked: the variant that applies the row masks (null for the fused kernel).
+const void* verify_kernel_ptr(int target_dtype, int mode, bool has_draft, bool masked);
 hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream);
-hipError_t launch_verify(const VerifyParams& params, int target_dtype, bool fused, int grid,
+hipError_t launch_verify(const VerifyParams& params, int target_dtype, int mode, int grid,
                          hipStream_t stream);
 // One workgroup per verify row: writes params.masks from top_k / top_p (constraints.hip).
 hipError_t launch_constraints(const VerifyParams& params, int target_dtype, hipStream_t stream);

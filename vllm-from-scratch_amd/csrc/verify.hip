@@ -236,43 +236,102 @@ struct FinalizeSmem {
   int first_reject;
 };
 
+// One wave: reduce verify row `row`'s slots (argmax over its na arg slots, softmax statistics
+// over its nc stats slots) and clear them.  tok: the argmax (greedy / in-kernel recovered) or
+// the supplied recovered id; M, S: the statistics (random rows).
+__device__ inline void finalize_row(const VerifyParams& p, int r, int64_t row, bool greedy,
+                                    bool full, int na, int& tok, float& M, float& S) {
+  const int lane = lane_id();
+  const int nc = p.nc;
+  uint64_t* aslots = p.arg_slots + row * p.arg_stride;
+  uint64_t* sslots = p.stat_slots + row * nc;
+  if (greedy || full) {
+    if (!wave_wait_slots(aslots, na, kSpinLimit, &p.ctrl[1]) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
+    uint64_t best = 0;
+    for (int c = lane; c < na; c += kWave) {
+      const uint64_t k = slot_load(aslots + c);
+      best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    tok = min(max(key_index(best), 0), p.V - 1);
+    for (int c = lane; c < na; c += kWave) slot_store(aslots + c, 0);
+  } else {
+    tok = p.recovered[row];
+  }
+  M = 0.f;
+  S = 1.f;
+  if (!greedy) {
+    const float c1 = exp2_scale(req_temperature(p, r));
+    if (!wave_row_stats(sslots, nc, c1, &p.ctrl[1], M, S) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
+    for (int c = lane; c < nc; c += kWave) slot_store(sslots + c, 0);
+  }
+}
+
+// Arg slots of a verify row: 2 * nc for rows of groups scored in half chunks.
+__device__ inline int row_arg_slots(const VerifyParams& p, bool full, int gfirst, int k) {
+  const int split_from = p.split && full ? p.grp_off[p.B] - p.lag : 0x7fffffff;
+  return gfirst + k / p.G >= split_from ? 2 * p.nc : p.nc;
+}
+
+// Accept / reject decision at position pos (verify row `row`) of request r, given the row's
+// argmax or recovered id tok and statistics (M, S).
+__device__ inline void decide_position(const VerifyParams& p, int r, bool greedy, int pos,
+                                       int64_t row, int tok, float M, float S, bool& accepted,
+                                       int& token) {
+  const bool synthetic = p.synth != nullptr;
+  const int d = p.draft_ids[row];
+  if (greedy) {
+    // rejection_sampler.py:715-732
+    if (synthetic) {
+      accepted = p.uniforms[row] < (double)p.synth[pos] && d >= 0;
+      token = accepted ? d : tok;
+    } else {
+      token = tok;
+      accepted = d == token;
+    }
+    return;
+  }
+  // rejection_sampler.py:782-814
+  const double u = p.uniforms[row];
+  if (d < 0) {
+    accepted = false;
+  } else if (synthetic) {
+    accepted = u < (double)p.synth[pos];
+  } else if (d >= p.V) {
+    accepted = false;  // the reference would index out of bounds here
+  } else {
+    const float q = p.draft ? p.draft[row * p.draft_stride + d] : 1.f;
+    const int64_t trow = target_row(p, (int)row);
+    float x;
+    if (p.target_dtype == MVSD_F32) {
+      x = static_cast<const float*>(p.target)[trow * p.target_stride + d];
+    } else if (p.target_dtype == MVSD_BF16) {
+      x = Elem<MVSD_BF16>::cvt(static_cast<const uint16_t*>(p.target)[trow * p.target_stride + d]);
+    } else {
+      x = Elem<MVSD_F16>::cvt(static_cast<const _Float16*>(p.target)[trow * p.target_stride + d]);
+    }
+    const float temp = req_temperature(p, r);
+    float pd = expf(x / temp - M / temp) / S;
+    if (p.masks && row_masked(p.masks[row], x, d)) pd = 0.f;  // -inf after the constraints
+    accepted = q > 0.f && (double)(pd / q) >= u;
+  }
+  token = accepted ? d : tok;
+}
+
 // Executed by the whole block that completed request r's last task.
 __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool full,
                                  FinalizeSmem& sm) {
   int begin, K;
   req_range(p, r, begin, K);
-  const int lane = lane_id();
-  const int nc = p.nc;
-  // first group scored in half chunks (2 * nc arg slots per row)
-  const int split_from = p.split && full ? p.grp_off[p.B] - p.lag : 0x7fffffff;
   const int gfirst = p.grp_off[r];
   for (int k = wave_id(); k < K; k += kVWaves) {
-    const int64_t row = begin + k;
-    uint64_t* aslots = p.arg_slots + row * p.arg_stride;
-    uint64_t* sslots = p.stat_slots + row * nc;
-    if (greedy || full) {
-      const int na = gfirst + k / p.G >= split_from ? 2 * nc : nc;
-      if (!wave_wait_slots(aslots, na, kSpinLimit, &p.ctrl[1]) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
-      uint64_t best = 0;
-      for (int c = lane; c < na; c += kWave) {
-        const uint64_t k = slot_load(aslots + c);
-        best = k > best ? k : best;
-      }
-      best = wave_max_u64(best);
-      if (lane == 0) sm.tok[k] = min(max(key_index(best), 0), p.V - 1);
-      for (int c = lane; c < na; c += kWave) slot_store(aslots + c, 0);
-    } else if (lane == 0) {
-      sm.tok[k] = p.recovered[row];
-    }
-    if (!greedy) {
-      const float c1 = exp2_scale(req_temperature(p, r));
-      float MX, S;
-      if (!wave_row_stats(sslots, nc, c1, &p.ctrl[1], MX, S) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
-      if (lane == 0) {
-        sm.M[k] = MX;
-        sm.S[k] = S;
-      }
-      for (int c = lane; c < nc; c += kWave) slot_store(sslots + c, 0);
+    int tok;
+    float M, S;
+    finalize_row(p, r, begin + k, greedy, full, row_arg_slots(p, full, gfirst, k), tok, M, S);
+    if (lane_id() == 0) {
+      sm.tok[k] = tok;
+      sm.M[k] = M;
+      sm.S[k] = S;
     }
   }
   if (threadIdx.x == 0) atomic_store_relaxed(&p.req_cnt[r], 0);
@@ -280,48 +339,11 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
 
   // every position's decision in parallel; the chain keeps the prefix up to the first reject
   const int tid = threadIdx.x;
-  const bool synthetic = p.synth != nullptr;
   for (int pos = tid; pos < K; pos += kVThreads) {
-    const int64_t row = begin + pos;
-    const int d = p.draft_ids[row];
     bool accepted;
     int token;
-    if (greedy) {
-      // rejection_sampler.py:715-732
-      if (synthetic) {
-        accepted = p.uniforms[row] < (double)p.synth[pos] && d >= 0;
-        token = accepted ? d : sm.tok[pos];
-      } else {
-        token = sm.tok[pos];
-        accepted = d == token;
-      }
-    } else {
-      // rejection_sampler.py:782-814
-      const double u = p.uniforms[row];
-      if (d < 0) {
-        accepted = false;
-      } else if (synthetic) {
-        accepted = u < (double)p.synth[pos];
-      } else if (d >= p.V) {
-        accepted = false;  // the reference would index out of bounds here
-      } else {
-        const float q = p.draft ? p.draft[row * p.draft_stride + d] : 1.f;
-        const int64_t trow = target_row(p, (int)row);
-        float x;
-        if (p.target_dtype == MVSD_F32) {
-          x = static_cast<const float*>(p.target)[trow * p.target_stride + d];
-        } else if (p.target_dtype == MVSD_BF16) {
-          x = Elem<MVSD_BF16>::cvt(static_cast<const uint16_t*>(p.target)[trow * p.target_stride + d]);
-        } else {
-          x = Elem<MVSD_F16>::cvt(static_cast<const _Float16*>(p.target)[trow * p.target_stride + d]);
-        }
-        const float temp = req_temperature(p, r);
-        float pd = expf(x / temp - sm.M[pos] / temp) / sm.S[pos];
-        if (p.masks && row_masked(p.masks[row], x, d)) pd = 0.f;  // -inf after the constraints
-        accepted = q > 0.f && (double)(pd / q) >= u;
-      }
-      token = accepted ? d : sm.tok[pos];
-    }
+    decide_position(p, r, greedy, pos, begin + pos, sm.tok[pos], sm.M[pos], sm.S[pos], accepted,
+                    token);
     sm.accepted[pos] = accepted;
     sm.out_tok[pos] = token;
   }
@@ -1389,7 +1411,7 @@ constexpr int ept_of() {
   return DT == MVSD_F32 ? MVSD_VERIFY_EPT_F32 : MVSD_VERIFY_EPT_16;
 }
 #ifndef MVSD_VERIFY_MIN_SUBS
-#define MVSD_VERIFY_MIN_SUBS 5
+#define MVSD_VERIFY_MIN_SUBS 8
 #endif
 #ifndef MVSD_VERIFY_TASKS_PER_WG
 #define MVSD_VERIFY_TASKS_PER_WG 16
@@ -1420,9 +1442,9 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int
 }
 
 template <int DT>
-const void* kernel_for(bool fused, bool has_draft, bool masked) {
+const void* kernel_for(int mode, bool has_draft, bool masked) {
   constexpr int E = ept_of<DT>();
-  if (!fused) {
+  if (mode == kModeSplit) {
     if (masked)
       return has_draft ? reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, true, true>)
                        : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false, true>);
@@ -1434,16 +1456,16 @@ const void* kernel_for(bool fused, bool has_draft, bool masked) {
                    : reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, false>);
 }
 
-const void* verify_kernel_ptr(int target_dtype, bool fused, bool has_draft, bool masked) {
+const void* verify_kernel_ptr(int target_dtype, int mode, bool has_draft, bool masked) {
   switch (target_dtype) {
-    case MVSD_F32: return kernel_for<MVSD_F32>(fused, has_draft, masked);
-    case MVSD_BF16: return kernel_for<MVSD_BF16>(fused, has_draft, masked);
-    case MVSD_F16: return kernel_for<MVSD_F16>(fused, has_draft, masked);
+    case MVSD_F32: return kernel_for<MVSD_F32>(mode, has_draft, masked);
+    case MVSD_BF16: return kernel_for<MVSD_BF16>(mode, has_draft, masked);
+    case MVSD_F16: return kernel_for<MVSD_F16>(mode, has_draft, masked);
     default: return nullptr;
   }
 }
 
-hipError_t launch_verify(const VerifyParams& params, int target_dtype, bool fused, int grid,
+hipError_t launch_verify(const VerifyParams& params, int target_dtype, int mode, int grid,
                          hipStream_t stream) {
   hipLaunchKernelGGL(verify_init_kernel, dim3(1), dim3(1024), 0, stream, params);
   hipError_t err = hipGetLastError();
@@ -1452,7 +1474,7 @@ hipError_t launch_verify(const VerifyParams& params, int target_dtype, bool fuse
     err = launch_constraints(params, target_dtype, stream);
     if (err != hipSuccess) return err;
   }
-  const void* fn = verify_kernel_ptr(target_dtype, fused, params.draft != nullptr,
+  const void* fn = verify_kernel_ptr(target_dtype, mode, params.draft != nullptr,
                                      params.masks != nullptr);
   if (!fn) return hipErrorInvalidValue;
   void* args[] = {const_cast<VerifyParams*>(&params)};
