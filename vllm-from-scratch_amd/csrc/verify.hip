@@ -1414,7 +1414,7 @@ constexpr int ept_of() {
 #define MVSD_VERIFY_MIN_SUBS 8
 #endif
 #ifndef MVSD_VERIFY_TASKS_PER_WG
-#define MVSD_VERIFY_TASKS_PER_WG 16
+#define MVSD_VERIFY_TASKS_PER_WG 10
 #endif
 
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int phases, int cap) {
