@@ -276,6 +276,10 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   int nq = 1;
   if (const char* env = getenv("MVSD_VERIFY_QUEUES")) nq = atoi(env);
   p.nq = nq < 1 ? 1 : (nq > mvsd::kMaxQueues ? mvsd::kMaxQueues : nq);
+  // Without the init kernel (group offsets built in each workgroup's LDS) when one queue
+  // serves the batch and its requests fit (MVSD_VERIFY_LDS_GROUPS=0 keeps the init kernel).
+  p.lds_groups = kmode == mvsd::kModeSplit && p.nq == 1 && B <= mvsd::kMaxLdsRequests && P > 0;
+  if (const char* env = getenv("MVSD_VERIFY_LDS_GROUPS")) p.lds_groups = p.lds_groups && atoi(env) != 0;
   p.top_k = masked ? a->top_k : nullptr;
   p.top_p = masked ? a->top_p : nullptr;
   p.masks = masked ? reinterpret_cast<float4*>(ws + lay.masks) : nullptr;

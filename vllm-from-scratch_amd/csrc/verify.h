@@ -8,6 +8,7 @@ namespace mvsd {
 
 constexpr int kMaxSpecLen = 128;  // reference MAX_SPEC_LEN, rejection_sampler.py:83
 constexpr int kMaxQueues = 16;    // work queues of the split verify kernel
+constexpr int kMaxLdsRequests = 4096;  // requests whose group offsets fit the kernel's LDS
 #ifndef MVSD_VERIFY_THREADS
 #define MVSD_VERIFY_THREADS 512
 #endif
@@ -70,6 +71,10 @@ struct VerifyParams {
   // hold no stats tasks) cover half chunks, 2 * nc per row, so the final tasks are short.
   int split;
   int arg_stride;  // arg slots per row: 2 * nc with the split, else nc
+  // Split kernel without the init kernel: every workgroup builds the requests' group offsets
+  // in its own LDS and derives group descriptors from them (one queue, B <= kMaxLdsRequests);
+  // grp_off / grp_desc are then unused.
+  int lds_groups;
   // Sampling constraints (top-k / top-p per request, either may be null).  When set, the
   // constraints kernel writes one row mask per verify row, (A, B, J as bits, 0): entry i of
   // the row, raw value x, is masked iff x < A || (x < B && i <= J).

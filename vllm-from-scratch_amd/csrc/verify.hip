@@ -268,8 +268,9 @@ __device__ inline void finalize_row(const VerifyParams& p, int r, int64_t row, b
 }
 
 // Arg slots of a verify row: 2 * nc for rows of groups scored in half chunks.
-__device__ inline int row_arg_slots(const VerifyParams& p, bool full, int gfirst, int k) {
-  const int split_from = p.split && full ? p.grp_off[p.B] - p.lag : 0x7fffffff;
+__device__ inline int row_arg_slots(const VerifyParams& p, const int* goff, bool full, int gfirst,
+                                    int k) {
+  const int split_from = p.split && full ? goff[p.B] - p.lag : 0x7fffffff;
   return gfirst + k / p.G >= split_from ? 2 * p.nc : p.nc;
 }
 
@@ -318,16 +319,17 @@ __device__ inline void decide_position(const VerifyParams& p, int r, bool greedy
   token = accepted ? d : tok;
 }
 
-// Executed by the whole block that completed request r's last task.
-__device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool full,
-                                 FinalizeSmem& sm) {
+// Executed by the whole block that completed request r's last task.  goff: the requests'
+// first group indices (global or LDS).  Writes the request's whole output row.
+__device__ void finalize_request(const VerifyParams& p, const int* goff, int r, bool greedy,
+                                 bool full, FinalizeSmem& sm) {
   int begin, K;
   req_range(p, r, begin, K);
-  const int gfirst = p.grp_off[r];
+  const int gfirst = goff[r];
   for (int k = wave_id(); k < K; k += kVWaves) {
     int tok;
     float M, S;
-    finalize_row(p, r, begin + k, greedy, full, row_arg_slots(p, full, gfirst, k), tok, M, S);
+    finalize_row(p, r, begin + k, greedy, full, row_arg_slots(p, goff, full, gfirst, k), tok, M, S);
     if (lane_id() == 0) {
       sm.tok[k] = tok;
       sm.M[k] = M;
@@ -361,9 +363,11 @@ __device__ void finalize_request(const VerifyParams& p, int r, bool greedy, bool
   __syncthreads();
   const int first = sm.first_reject;
   int32_t* out = p.out + (int64_t)r * p.out_stride;
-  for (int pos = tid; pos <= K; pos += kVThreads) {
-    if (pos < K && pos <= first) out[pos] = sm.out_tok[pos];
-    else if (pos == K && first == K) out[K] = p.bonus[r];
+  for (int pos = tid; pos <= p.max_spec_len; pos += kVThreads) {
+    int v = -1;
+    if (pos < K && pos <= first) v = sm.out_tok[pos];
+    else if (pos == K && first == K) v = p.bonus[r];
+    out[pos] = v;
   }
 }
 
@@ -827,7 +831,27 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
 struct TaskDecode {
   int total, step_size, nc, lag, groups, two_phase, split;
   const int* qgi;  // queue position -> group index (nullptr: identity)
+  const int* goff;  // requests' group offsets in LDS (descriptors derived), or nullptr
 };
+
+// Descriptor of group li derived from the requests' group offsets (the layout of grp_desc).
+__device__ inline int4 group_desc(const VerifyParams& p, const int* goff, int li) {
+  int lo = 0, hi = p.B - 1;  // the last request whose first group is <= li owns it
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (goff[mid] <= li) lo = mid;
+    else hi = mid - 1;
+  }
+  const int r = lo;
+  int b, k;
+  req_range(p, r, b, k);
+  const int g = li - goff[r];
+  const int ng = goff[r + 1] - goff[r];
+  const bool greedy = req_is_greedy(p, r);
+  const int flags = (greedy ? kGreedy : 0) | (!greedy && !p.recovered ? kFull : 0);
+  return make_int4(r, b + g * p.G, min(p.G, k - g * p.G) | ng << 8 | flags << 16 | g << 24,
+                   __float_as_int(exp2_scale(req_temperature(p, r))));
+}
 
 // Thread 0: decode ticket t and fetch its group descriptor into dst[0..7]
 // = {t, arg slot, valid | phase_b << 1 | half << 2, request, first row,
@@ -847,7 +871,7 @@ __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, i
     c = (phase_b && !half) ? w - td.nc : w;
     const int li = phase_b ? step - td.lag : step;
     if (li >= 0 && li < td.groups) {
-      d = p.grp_desc[td.qgi ? td.qgi[li] : li];
+      d = td.goff ? group_desc(p, td.goff, li) : p.grp_desc[td.qgi ? td.qgi[li] : li];
       const bool full = (d.z >> 16) & kFull;
       flags = (!phase_b || full ? 1 : 0) | (phase_b ? 2 : 0) | (half ? 4 : 0);
       if (td.split && full) {
@@ -880,15 +904,55 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   __shared__ int s_last;
   __shared__ FinalizeSmem fsm;
 
+  __shared__ int s_goff[kMaxLdsRequests + 1];
+
   const int tid = threadIdx.x;
   const int queue = blockIdx.x % p.nq;
   int* ticket = &p.qticket[queue];
-  const int groups = p.grp_off[p.B];
+  const int* goff = p.grp_off;
+  if (p.lds_groups) {
+    // Group offsets of the requests (groups of ceil(K / G) rows), built by every workgroup;
+    // each thread scans a run of consecutive requests.  Requests without drafts get their
+    // output row here (bonus, then -1); every other row is written by its finalisation.
+    const int per = (p.B + kVThreads - 1) / kVThreads;
+    const int r0 = tid * per, r1 = min(p.B, r0 + per);
+    int run = 0;
+    for (int r = r0; r < r1; ++r) {
+      int b, k;
+      req_range(p, r, b, k);
+      run += (k + p.G - 1) / p.G;
+    }
+    __shared__ int s_scan[kVThreads];
+    s_scan[tid] = run;
+    __syncthreads();
+    for (int off = 1; off < kVThreads; off <<= 1) {
+      const int add = tid >= off ? s_scan[tid - off] : 0;
+      __syncthreads();
+      s_scan[tid] += add;
+      __syncthreads();
+    }
+    int acc = s_scan[tid] - run;
+    for (int r = r0; r < r1; ++r) {
+      int b, k;
+      req_range(p, r, b, k);
+      s_goff[r] = acc;
+      acc += (k + p.G - 1) / p.G;
+      if (k == 0 && (r % (int)gridDim.x) == (int)blockIdx.x) {
+        int32_t* out = p.out + (int64_t)r * p.out_stride;
+        for (int c = 0; c <= p.max_spec_len; ++c) out[c] = c == 0 ? p.bonus[r] : -1;
+      }
+    }
+    if (tid == kVThreads - 1) s_goff[p.B] = s_scan[kVThreads - 1];
+    __syncthreads();
+    goff = s_goff;
+  }
+  const int groups = goff[p.B];
   TaskDecode td;
   td.nc = p.nc;
   td.lag = p.lag;
-  td.groups = p.qcount[queue];
+  td.groups = p.lds_groups ? groups : p.qcount[queue];
   td.qgi = p.nq > 1 ? p.qgi + p.qoff[queue] : nullptr;
+  td.goff = p.lds_groups ? s_goff : nullptr;
   td.two_phase = p.two_phase;
   td.split = p.split;
   td.step_size = p.two_phase ? 2 * td.nc : td.nc;
@@ -901,7 +965,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
     if (pend_r >= 0) {
       if (tid == 0) s_last = pend_cnt == pend_target - 1;
       __syncthreads();
-      if (s_last) finalize_request(p, pend_r, pend_greedy, pend_full, fsm);
+      if (s_last) finalize_request(p, goff, pend_r, pend_greedy, pend_full, fsm);
       __syncthreads();
       pend_r = -1;
     }
@@ -979,10 +1043,12 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   if (tid == 0) s_last = atomic_add_relaxed(&p.ctrl[2], 1) == (int)gridDim.x - 1;
   __syncthreads();
   if (s_last) {
-    for (int i = tid; i <= p.B; i += kVThreads) p.grp_off[i] = 0;
-    for (int i = tid; i < groups; i += kVThreads) {
-      p.grp_desc[i] = make_int4(0, 0, 0, 0);
-      p.qgi[i] = 0;
+    if (!p.lds_groups) {
+      for (int i = tid; i <= p.B; i += kVThreads) p.grp_off[i] = 0;
+      for (int i = tid; i < groups; i += kVThreads) {
+        p.grp_desc[i] = make_int4(0, 0, 0, 0);
+        p.qgi[i] = 0;
+      }
     }
     for (int q = tid; q < p.nq; q += kVThreads) {
       atomic_store_relaxed(&p.qticket[q], 0);
@@ -1169,7 +1235,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_FUSED_ATTRS void verify_fused_kerne
     if (pd.r >= 0) {
       if (tid == 0) s_last = pd.cnt == pd.target - 1;
       __syncthreads();
-      if (s_last) finalize_request(p, pd.r, pd.greedy, pd.full, fsm);
+      if (s_last) finalize_request(p, p.grp_off, pd.r, pd.greedy, pd.full, fsm);
       __syncthreads();
       pd.r = -1;
     }
@@ -1467,8 +1533,11 @@ const void* verify_kernel_ptr(int target_dtype, int mode, bool has_draft, bool m
 
 hipError_t launch_verify(const VerifyParams& params, int target_dtype, int mode, int grid,
                          hipStream_t stream) {
-  hipLaunchKernelGGL(verify_init_kernel, dim3(1), dim3(1024), 0, stream, params);
-  hipError_t err = hipGetLastError();
+  hipError_t err = hipSuccess;
+  if (!params.lds_groups) {
+    hipLaunchKernelGGL(verify_init_kernel, dim3(1), dim3(1024), 0, stream, params);
+    err = hipGetLastError();
+  }
   if (err != hipSuccess || params.P == 0) return err;
   if (params.masks) {
     err = launch_constraints(params, target_dtype, stream);
