@@ -420,6 +420,30 @@ __device__ inline u32x4 load_target16(const void* p) {
 }
 
 // DT row sub-chunk, full and aligned.
+__device__ inline uint32_t bits16(uint16_t v) { return v; }
+__device__ inline uint32_t bits16(_Float16 v) { return __builtin_bit_cast(uint16_t, v); }
+
+// The 16-byte vector of DT entries at col, entries at or past vend replaced by fill; packed in
+// registers (no local array).
+template <int DT>
+__device__ inline u32x4 load_vec_checked(const typename Elem<DT>::storage* __restrict__ base,
+                                         int64_t col, int64_t vend,
+                                         typename Elem<DT>::storage fill) {
+  u32x4 v;
+  if constexpr (Elem<DT>::kVec == 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = __float_as_uint(col + j < vend ? base[col + j] : fill);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = bits16(col + 2 * j < vend ? base[col + 2 * j] : fill);
+      const uint32_t hi = bits16(col + 2 * j + 1 < vend ? base[col + 2 * j + 1] : fill);
+      v[j] = lo | hi << 16;
+    }
+  }
+  return v;
+}
+
 template <int DT, int EPT, bool NT>
 __device__ inline void load_raw(const typename Elem<DT>::storage* __restrict__ base, int64_t s0,
                                 u32x4 (&out)[EPT / Elem<DT>::kVec]) {
@@ -439,14 +463,8 @@ __device__ inline void load_raw_checked(const typename Elem<DT>::storage* __rest
 #pragma unroll
   for (int i = 0; i < EPT / VEC; ++i) {
     const int64_t col = vec_col<DT>(s0, i);
-    if (aligned && col + VEC <= vend) {
-      out[i] = load_target16<NT>(base + col);
-    } else {
-      S tmp[VEC];
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) tmp[j] = col + j < vend ? base[col + j] : fill;
-      out[i] = *reinterpret_cast<const u32x4*>(tmp);
-    }
+    if (aligned && col + VEC <= vend) out[i] = load_target16<NT>(base + col);
+    else out[i] = load_vec_checked<DT>(base, col, vend, fill);
   }
 }
 
@@ -458,14 +476,10 @@ __device__ inline void load_raw_f32(const float* __restrict__ base, int64_t s0, 
 #pragma unroll
   for (int m = 0; m < EPT / 4; ++m) {
     const int64_t col = vec_col<DT>(s0, m / (VEC / 4)) + (m % (VEC / 4)) * 4;
-    if (FAST || (aligned && col + 4 <= vend)) {
+    if (FAST || (aligned && col + 4 <= vend))
       out[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + col));
-    } else {
-      float tmp[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) tmp[j] = col + j < vend ? base[col + j] : fill;
-      out[m] = *reinterpret_cast<const u32x4*>(tmp);
-    }
+    else
+      out[m] = load_vec_checked<MVSD_F32>(base, col, vend, fill);
   }
 }
 
@@ -635,7 +649,8 @@ __device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int n
 // largest value of a row is never masked).
 template <int DT, int EPT, int G, bool MASKED, typename Hook>
 __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int row0, int nrows,
-                                  int64_t v0, int64_t vend, float* s_red, Hook&& after_loads) {
+                                  int64_t v0, int64_t vend, float* s_red, float* s_M,
+                                  Hook&& after_loads) {
   using S = typename Elem<DT>::storage;
   const S* tb[G];
   target_bases<DT, G>(p, row0, nrows, tb);
@@ -684,9 +699,15 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
 #pragma unroll
   for (int g = 0; g < G; ++g)
     s[g] = m[g] == -INFINITY ? 0.f : s[g] * __builtin_amdgcn_exp2f((m[g] - M[g]) * c1);
+  // row maxima for the row threads through LDS (ordered by the barrier of the sum below), so
+  // that no thread indexes the register array M by its thread index
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) s_M[g] = M[g];
+  }
   const float srow = block_sum_to_row_thread<G, kVWaves>(s, s_red);
   if ((int)threadIdx.x < nrows) {
-    const float mrow = row_of_thread<G>(M);
+    const float mrow = s_M[threadIdx.x];
     slot_store(p.stat_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c,
                pack_stats(mrow, mrow == -INFINITY ? 0.f : srow));
   }
@@ -1017,7 +1038,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
     if (greedy) {
       task_argmax<DT, EPT, G, MASKED>(p, c, row0, nrows, v0, vend, s_key, prefetch);
     } else if (!phase_b) {
-      task_stats<DT, EPT, G, MASKED>(p, c, c1, row0, nrows, v0, vend, s_red, prefetch);
+      task_stats<DT, EPT, G, MASKED>(p, c, c1, row0, nrows, v0, vend, s_red, s_M, prefetch);
     } else {
       task_scores<DT, EPT, G, HAS_DRAFT, MASKED>(p, c, r, c1, row0, nrows, v0, vend, s_key, s_M,
                                                  s_L, prefetch);
