@@ -82,9 +82,13 @@ def test_c4_masks_match_processed_path_and_oracle(device, B):
                           "c4 in-kernel masks")
 
 
-def test_c4_in_kernel_constraints_then_verify(device):
+@pytest.mark.parametrize("mode", ["split", "fused"])
+def test_c4_in_kernel_constraints_then_verify(device, monkeypatch, mode):
     """rejection_sample on the raw bf16 rows with the divide and the constraints in the
-    kernels, against the oracle sampler on the same rows masked by the processed path."""
+    kernels, against the oracle sampler on the same rows masked by the processed path (split
+    kernel, and the single-read kernel's masked variant)."""
+    if mode == "fused":
+        monkeypatch.setenv("MVSD_VERIFY_MODE", "fused")
     w = configs.ragged_c4(device, B=128, seed=2024)
     sm = _metadata(w)
     out = rejection_sample(w.draft_token_ids, w.num_draft_tokens, w.max_spec_len,
@@ -99,7 +103,7 @@ def test_c4_in_kernel_constraints_then_verify(device):
                                uniforms=w.uniforms.cpu(), exp_noise=w.exp_noise.cpu(),
                                apply_temperature=False)
     rep = orc.compare(out.cpu().numpy(), ref, w.draft_token_ids.cpu(), w.num_draft_tokens)
-    print(f"[c4 in-kernel constraints] requests={rep.requests} mismatched={rep.mismatched} "
+    print(f"[c4 in-kernel constraints {mode}] requests={rep.requests} mismatched={rep.mismatched} "
           f"accept_flips={rep.accept_flips} recovered_flips={rep.recovered_flips}", flush=True)
     assert not rep.unexplained, rep.unexplained[:5]
 

@@ -253,21 +253,57 @@ def test_synthetic_mode_parity(device):
     check_parity(w, out, ref, "synthetic")
 
 
-@pytest.mark.parametrize("case", ["c2", "headline", "point_mass", "bf16_ragged", "odd_v"])
+@pytest.mark.parametrize("case", ["c2", "headline", "point_mass", "bf16_ragged", "odd_v",
+                                  "c5_rows", "one_request", "one_subchunk", "two_subchunks"])
 def test_fused_kernel_parity(device, monkeypatch, case):
     """The single-read kernel (MVSD_VERIFY_MODE=fused; the default is the split kernel).  Odd
-    V (unaligned rows) makes the host fall back to the split kernel."""
+    V (unaligned rows) makes the host fall back to the split kernel; one_request has fewer
+    tasks than workgroups, one_subchunk / two_subchunks rows of 1 and 2 sub-chunks."""
     monkeypatch.setenv("MVSD_VERIFY_MODE", "fused")
     draft_none = case == "point_mass"
     w = {"c2": lambda: configs.random_c2(device),
          "headline": lambda: configs.headline(device),
          "point_mass": lambda: configs.random_c2(device, B=32, k=4, seed=4243),
          "bf16_ragged": lambda: configs.ragged_c4(device, B=64),
-         "odd_v": lambda: configs.random_c2(device, B=16, k=3, V=4097, seed=11)}[case]()
+         "odd_v": lambda: configs.random_c2(device, B=16, k=3, V=4097, seed=11),
+         "c5_rows": lambda: configs.eagle_c5(device, B=40),
+         "one_request": lambda: configs.random_c2(device, B=1, k=7, seed=12),
+         "one_subchunk": lambda: configs.random_c2(device, B=24, k=5, V=1000, seed=13),
+         "two_subchunks": lambda: configs.random_c2(device, B=24, k=5, V=4000, seed=14)}[case]()
     rep = check_parity(w, run_workload(w, draft_none=draft_none),
                        oracle_for(w, draft_none=draft_none), f"fused {case}")
     assert rep.mismatched <= 4
     assert rs.workspace_error_flag(w.target_logits.device) == 0
+
+
+@pytest.mark.parametrize("case", ["c1", "c1_large", "c4_mixed"])
+def test_fused_kernel_greedy_bit_exact(device, monkeypatch, case):
+    """Greedy rows through the single-read kernel (argmax at stage 1, target_rows gathers)."""
+    monkeypatch.setenv("MVSD_VERIFY_MODE", "fused")
+    w = {"c1": lambda: configs.greedy_c1(device),
+         "c1_large": lambda: configs.greedy_c1(device, B=64, k=6, seed=77),
+         "c4_mixed": lambda: configs.ragged_c4(device, B=96, seed=31)}[case]()
+    out = run_workload(w)
+    if case == "c4_mixed":
+        check_parity(w, out, oracle_for(w), "fused c4 mixed")
+    else:
+        assert np.array_equal(out.cpu().numpy(), oracle_for(w).output_token_ids)
+    assert rs.workspace_error_flag(w.target_logits.device) == 0
+
+
+def test_fused_kernel_repeated_calls(device, monkeypatch):
+    """Calls of different shapes in a row leave the workspace zeroed for the next one."""
+    monkeypatch.setenv("MVSD_VERIFY_MODE", "fused")
+    big = configs.random_c2(device, B=96, k=4, seed=51)
+    small = configs.random_c2(device, B=5, k=2, seed=52)
+    a = run_workload(big)
+    b = run_workload(small)
+    c = run_workload(big)
+    d = run_workload(small)
+    assert torch.equal(a, c) and torch.equal(b, d)
+    check_parity(big, a, oracle_for(big), "fused repeated big")
+    check_parity(small, b, oracle_for(small), "fused repeated small")
+    assert rs.workspace_error_flag(big.target_logits.device) == 0
 
 
 @pytest.mark.parametrize("V", [5, 1001, 4097, 8193])

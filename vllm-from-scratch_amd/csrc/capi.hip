@@ -49,7 +49,6 @@ int verify_capacity(int device, int dtype, int mode, bool has_draft, bool masked
   static int cache[kMaxDevices][3][2][4];
   if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2 || mode < 0 || mode > 1)
     return 0;
-  if (mode == mvsd::kModeFused && masked) return 0;
   std::lock_guard<std::mutex> lock(mu);
   int& slot = cache[device][dtype][mode][(masked ? 2 : 0) + (has_draft ? 1 : 0)];
   if (slot > 0) return slot;
@@ -188,9 +187,9 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   if ((uintptr_t)a->workspace % 256 != 0) return MVSD_E_ALIGN;
 
   // Kernel choice: the split kernel (stats tasks, then score tasks that re-read the target
-  // chunk) by default.  MVSD_VERIFY_MODE=fused selects the single-read kernel for batches
-  // that need recovered scores, when its progress condition (resident workgroups >= chunks
-  // per row) and its load-width requirements hold.
+  // chunk) by default.  MVSD_VERIFY_MODE=fused selects the single-read kernel when its
+  // requirements hold: 16-byte loads (below), the request metadata in LDS
+  // (B <= kMaxFusedRequests) and at most fused_max_chunks() sub-chunks per row.
   const int two_phase = (!a->all_greedy && !a->recovered_token_ids) ? 1 : 0;
   // Sampling constraints apply only when some request samples (rejection_sampler.py:549-550).
   const bool masked = !a->all_greedy && (a->top_k || a->top_p);
@@ -208,10 +207,11 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
                         (!a->draft_probs || aligned16(a->draft_probs, a->draft_stride * 4)) &&
                         V % (16 / esz) == 0;
     const char* mode = getenv("MVSD_VERIFY_MODE");
-    if (two_phase && vec_ok && !masked && mode && strcmp(mode, "fused") == 0) {
+    if (vec_ok && B <= mvsd::kMaxFusedRequests && size_plan.nsub <= mvsd::fused_max_chunks() &&
+        mode && strcmp(mode, "fused") == 0) {
       const int fcap = verify_capacity(device, a->target_dtype, mvsd::kModeFused,
-                                       a->draft_probs != nullptr, false);
-      if (fcap >= size_plan.nsub && fcap > 0) {
+                                       a->draft_probs != nullptr, masked);
+      if (fcap > 0) {
         kmode = mvsd::kModeFused;
         cap = fcap;
       }
@@ -280,6 +280,10 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   // serves the batch and its requests fit (MVSD_VERIFY_LDS_GROUPS=0 keeps the init kernel).
   p.lds_groups = kmode == mvsd::kModeSplit && p.nq == 1 && B <= mvsd::kMaxLdsRequests && P > 0;
   if (const char* env = getenv("MVSD_VERIFY_LDS_GROUPS")) p.lds_groups = p.lds_groups && atoi(env) != 0;
+  if (kmode == mvsd::kModeFused) {
+    p.nq = 1;  // one ticket; the group offsets always in LDS
+    p.lds_groups = 1;
+  }
   p.top_k = masked ? a->top_k : nullptr;
   p.top_p = masked ? a->top_p : nullptr;
   p.masks = masked ? reinterpret_cast<float4*>(ws + lay.masks) : nullptr;
@@ -314,8 +318,8 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
       if (const char* env = getenv("MVSD_VERIFY_SPLIT")) p.split = p.split && atoi(env) != 0;
       if (p.split) p.arg_stride = 2 * plan.nc;
     }
-    // every workgroup may claim two tickets past the last task
-    if (tasks > 0x7fffffff - 2 * (int64_t)cap) return MVSD_E_RANGE;
+    // every workgroup may claim up to three tickets past the last task
+    if (tasks > 0x7fffffff - 4 * (int64_t)cap) return MVSD_E_RANGE;
   }
   return hip_status(mvsd::launch_verify(p, a->target_dtype, kmode, grid, (hipStream_t)stream));
 }

@@ -9,6 +9,7 @@ namespace mvsd {
 constexpr int kMaxSpecLen = 128;  // reference MAX_SPEC_LEN, rejection_sampler.py:83
 constexpr int kMaxQueues = 16;    // work queues of the split verify kernel
 constexpr int kMaxLdsRequests = 4096;  // requests whose group offsets fit the kernel's LDS
+constexpr int kMaxFusedRequests = 2048;  // requests whose metadata fit the fused kernel's LDS
 #ifndef MVSD_VERIFY_THREADS
 #define MVSD_VERIFY_THREADS 512
 #endif
@@ -117,8 +118,8 @@ struct VerifyPlan {
 };
 
 // Verify kernels: the split kernel (stats tasks, then score tasks that re-read the target) and
-// the single-read fused kernel (one sub-chunk per task, scores computed by the workgroup that
-// loaded the target chunk).
+// the single-read fused kernel (one sub-chunk per task; the workgroup that loaded a target
+// sub-chunk parks it in LDS and scores it once the row's statistics are complete).
 constexpr int kModeSplit = 0;
 constexpr int kModeFused = 1;
 
@@ -126,8 +127,10 @@ constexpr int kModeFused = 1;
 // recovered scores (stats and score tasks per chunk), else 1; cap = resident workgroups.
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int phases, int cap);
 
-// masked: the variant that applies the row masks (null for the fused kernel).
+// masked: the variant that applies the row masks.
 const void* verify_kernel_ptr(int target_dtype, int mode, bool has_draft, bool masked);
+// Largest sub-chunks per row (nc) the fused kernel accepts (stats polls, FIFO bound).
+int fused_max_chunks();
 hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream);
 hipError_t launch_verify(const VerifyParams& params, int target_dtype, int mode, int grid,
                          hipStream_t stream);

@@ -914,6 +914,44 @@ __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, i
   dst[7] = nsplit;
 }
 
+// Group offsets of the requests (groups of ceil(K / G) rows) into goff[0..B] in LDS, built by
+// every workgroup; each thread scans a run of consecutive requests.  Requests without drafts
+// get their output row here (bonus, then -1), from workgroup r mod grid; every other row is
+// written by its finalisation.
+__device__ inline void build_lds_groups(const VerifyParams& p, int* goff) {
+  __shared__ int s_scan[kVThreads];
+  const int tid = threadIdx.x;
+  const int per = (p.B + kVThreads - 1) / kVThreads;
+  const int r0 = tid * per, r1 = min(p.B, r0 + per);
+  int run = 0;
+  for (int r = r0; r < r1; ++r) {
+    int b, k;
+    req_range(p, r, b, k);
+    run += (k + p.G - 1) / p.G;
+  }
+  s_scan[tid] = run;
+  __syncthreads();
+  for (int off = 1; off < kVThreads; off <<= 1) {
+    const int add = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += add;
+    __syncthreads();
+  }
+  int acc = s_scan[tid] - run;
+  for (int r = r0; r < r1; ++r) {
+    int b, k;
+    req_range(p, r, b, k);
+    goff[r] = acc;
+    acc += (k + p.G - 1) / p.G;
+    if (k == 0 && (r % (int)gridDim.x) == (int)blockIdx.x) {
+      int32_t* out = p.out + (int64_t)r * p.out_stride;
+      for (int c = 0; c <= p.max_spec_len; ++c) out[c] = c == 0 ? p.bonus[r] : -1;
+    }
+  }
+  if (tid == kVThreads - 1) goff[p.B] = s_scan[kVThreads - 1];
+  __syncthreads();
+}
+
 template <int DT, int EPT, int G, bool HAS_DRAFT, bool MASKED>
 __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(VerifyParams p) {
   static_assert(EPT % Elem<DT>::kVec == 0, "EPT must be a multiple of the vector width");
@@ -932,39 +970,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   int* ticket = &p.qticket[queue];
   const int* goff = p.grp_off;
   if (p.lds_groups) {
-    // Group offsets of the requests (groups of ceil(K / G) rows), built by every workgroup;
-    // each thread scans a run of consecutive requests.  Requests without drafts get their
-    // output row here (bonus, then -1); every other row is written by its finalisation.
-    const int per = (p.B + kVThreads - 1) / kVThreads;
-    const int r0 = tid * per, r1 = min(p.B, r0 + per);
-    int run = 0;
-    for (int r = r0; r < r1; ++r) {
-      int b, k;
-      req_range(p, r, b, k);
-      run += (k + p.G - 1) / p.G;
-    }
-    __shared__ int s_scan[kVThreads];
-    s_scan[tid] = run;
-    __syncthreads();
-    for (int off = 1; off < kVThreads; off <<= 1) {
-      const int add = tid >= off ? s_scan[tid - off] : 0;
-      __syncthreads();
-      s_scan[tid] += add;
-      __syncthreads();
-    }
-    int acc = s_scan[tid] - run;
-    for (int r = r0; r < r1; ++r) {
-      int b, k;
-      req_range(p, r, b, k);
-      s_goff[r] = acc;
-      acc += (k + p.G - 1) / p.G;
-      if (k == 0 && (r % (int)gridDim.x) == (int)blockIdx.x) {
-        int32_t* out = p.out + (int64_t)r * p.out_stride;
-        for (int c = 0; c <= p.max_spec_len; ++c) out[c] = c == 0 ? p.bonus[r] : -1;
-      }
-    }
-    if (tid == kVThreads - 1) s_goff[p.B] = s_scan[kVThreads - 1];
-    __syncthreads();
+    build_lds_groups(p, s_goff);
     goff = s_goff;
   }
   const int groups = goff[p.B];
@@ -1081,398 +1087,643 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
 }
 
 // ------------------------------------------------------------------ fused kernel -----
-// Single-read kernel for batches that need recovered scores.  One task per (group, chunk)
-// with a chunk of exactly kVThreads * EPT columns; workgroup w takes tasks w, w + grid,
-// w + 2 grid, ... (static assignment, no ticket atomics).  Iteration i of a workgroup:
-//   1. issues the stats-slot loads of task i-L's rows (L = kLag), then task i's target chunk
-//      and task i-L's draft / noise chunks;
-//   2. reduces task i's target chunk into per-row stats (or the argmax for greedy groups),
-//      publishes them and parks the chunk in LDS;
-//   3. scores task i-L (target from LDS) against its group's combined stats and publishes
-//      the chunk-local recovered candidate.
-// Every input byte is read once.  Latency is hidden by running several small workgroups per
-// CU; within a workgroup the loads of one iteration are issued together, with the polls
-// first so that waiting for them never waits for the data loads.  Loads are unconditional
-// 16-byte loads (rows past a group's end and absent tasks load duplicates of valid
-// addresses), so every path issues the same loads and the in-order load counters stay exact.
+// Single-read kernel.  A task is one sub-chunk (kVThreads * EPT columns) of a row group;
+// tickets go out in group-major order, so the nc sub-chunks of a group hold consecutive
+// tickets.  In each iteration a workgroup
+//   * issues the draft / noise loads (and the stats-slot polls of its group) of the oldest
+//     task of its FIFO when that task is due, then the target loads of its next task;
+//   * reduces the current task's target sub-chunk, loaded during the previous iteration:
+//     per-row chunk stats (greedy groups: the chunk argmax) are published, and for random
+//     rows the sub-chunk is parked in LDS and the task joins the FIFO;
+//   * once the FIFO holds kDepth tasks, retires the oldest: the group's stats are combined
+//     and the parked sub-chunk is scored against the draft and noise sub-chunks, publishing
+//     the chunk-local recovered candidate.
+// Every input byte is read once; a task that finds no free parking slot (only when the FIFO
+// has grown past kDepth, see below) re-reads its target sub-chunk when it is scored.
 //
-// Progress: scoring task i-L waits for the stats of its group, whose tasks t' satisfy
-// t' <= t_{i-L} + nc - 1 < t_{i-L} + grid when grid >= nc, so they belong to iterations
-// <= i-L+1 <= i of their workgroups and are published in step 2 before any wait there.
-// Ordering events by (iteration, step), every wait is on an earlier event, hence no cycle,
-// provided all workgroups are resident: the host launches at most the resident capacity and
-// only when it is >= nc.
+// One ticket atomic per iteration, issued after the stage-1 reduction by thread 0, is read
+// and decoded one iteration later (group descriptors come from the LDS group offsets and
+// scalar loads), and the ticket's target loads go out in the iteration after that: no wave
+// waits on an atomic it has just issued, and every vector load is unconditional (absent
+// tasks load one line), so the in-order load counters wait for exactly the data needed.
+//
+// Progress.  A workgroup waits for a group's stats only when retiring its oldest task, of
+// group g, and only if every ticket it holds without having published its stats lies past
+// g.  Those tickets are all newer than the one whose loads are in flight, so checking that
+// one suffices; otherwise the retirement is postponed and the FIFO grows.  Take the lowest
+// group g* that some workgroup waits for: a workgroup holding an unpublished ticket of g* is
+// not waiting (it could only wait for a group below g*), so it publishes it.  If every
+// resident workgroup waits, one of them holds a ticket past g*, so every ticket of g* has been
+// claimed, hence published, and the workgroups waiting for g* proceed.  Workgroups not yet
+// resident hold no tickets.  The waits are bounded all the same (kSpinLimit, flag ctrl[1]).
+// While the FIFO holds tasks of one group only, it holds fewer than nc of them, so kFifo >
+// nc + kDepth + 4 bounds it (checked by the host).
 
-constexpr int kRing = 64;  // task descriptors cached per workgroup (LDS ring)
-#ifndef MVSD_FUSED_LAG
-#define MVSD_FUSED_LAG 2
+#ifndef MVSD_FUSED_DEPTH
+#define MVSD_FUSED_DEPTH 3
 #endif
-// Iterations between a task's stats step and its score step: its group's other chunks are
-// reduced by other workgroups in the same iteration, and the lag gives the slowest of them
-// time to publish before the scores need the combined stats.
-constexpr int kLag = MVSD_FUSED_LAG;
-static_assert(kLag >= 1 && kLag < kRing / 2, "lag must fit the descriptor ring");
+constexpr int kDepth = MVSD_FUSED_DEPTH;  // parking slots (target sub-chunks) per workgroup
+static_assert(kDepth >= 2 && kDepth <= 8, "parking depth");
+constexpr int kFifo = 128;     // FIFO records (a power of two)
+constexpr int kTaskInts = 16;  // LDS words of a task record
 
-template <int DT, int EPT, int G>
-struct FusedBuf {
-  u32x4 x[G][EPT / Elem<DT>::kVec];  // target chunk of task i
-  u32x4 q[G][EPT / 4];               // draft chunk of task i-L
-  u32x4 e[EPT / 4];                  // noise chunk of task i-L
-};
+// Load of a read-only kernel input at a wave-uniform index through the constant address
+// space: a scalar load, which leaves the vector-memory counters alone.
+template <typename T>
+__device__ inline T ld_const(const T* base, int64_t i) {
+  return ((const __attribute__((address_space(4))) T*)base)[i];
+}
+__device__ inline float4 ld_const(const float4* base, int64_t i) {
+  const float* f = reinterpret_cast<const float*>(base) + 4 * i;
+  return make_float4(ld_const(f, 0), ld_const(f, 1), ld_const(f, 2), ld_const(f, 3));
+}
 
+template <int G>
 struct FusedTask {
-  int c;      // chunk, or -1 when absent
-  int r;      // request
-  int row0;   // first verify row
-  int nrows;  // rows in the group
-  int ngr;    // groups of the request
-  int flags;  // kGreedy | kFull
-  float c1;   // log2(e) / T
-};
-
-// Per-workgroup LDS ring of task descriptors and target-row indices, so that issuing an
-// iteration's loads never waits on a descriptor load.
-template <int G>
-struct TaskRing {
-  int4 d[kRing];
-  float c1[kRing];
-  int trow[kRing][G];
+  int t;        // ticket, < 0: none
+  int c;        // sub-chunk of the row
+  int r;        // request
+  int row0;     // first verify row of the group
+  int nrows;    // rows in the group
+  int ngr;      // groups of the request
+  int flags;    // kGreedy | kFull
+  int slot;     // parking slot of a FIFO record, -1: not parked
+  float c1;     // log2(e) / T
+  int trow[G];  // target rows of the group's rows (the last one repeated)
 };
 
 template <int G>
-__device__ inline FusedTask ring_task(const TaskRing<G>& ring, int i) {
-  const int4 a = ring.d[i % kRing];
-  FusedTask t;
-  t.c = a.x;
-  t.r = a.y;
-  t.row0 = a.z;
-  t.nrows = a.w & 0xff;
-  t.ngr = (a.w >> 8) & 0xff;
-  t.flags = (a.w >> 16) & 0xff;
-  t.c1 = ring.c1[i % kRing];
+__device__ inline FusedTask<G> no_task() {
+  FusedTask<G> d;
+  d.t = -1;
+  d.c = 0;
+  d.r = 0;
+  d.row0 = 0;
+  d.nrows = 1;
+  d.ngr = 1;
+  d.flags = 0;
+  d.slot = -1;
+  d.c1 = 1.f;
+#pragma unroll
+  for (int g = 0; g < G; ++g) d.trow[g] = 0;
+  return d;
+}
+
+template <int G>
+__device__ inline void task_put(int* d, const FusedTask<G>& t) {
+  d[0] = t.t;
+  d[1] = t.c;
+  d[2] = t.r;
+  d[3] = t.row0;
+  d[4] = t.nrows;
+  d[5] = t.ngr;
+  d[6] = t.flags;
+  d[7] = t.slot;
+  d[8] = __float_as_int(t.c1);
+#pragma unroll
+  for (int g = 0; g < G; ++g) d[9 + g] = t.trow[g];
+}
+
+// A task record in LDS, read by every thread into wave-uniform (scalar) registers.
+template <int G>
+__device__ inline FusedTask<G> task_get(const int* d) {
+  FusedTask<G> t;
+  t.t = __builtin_amdgcn_readfirstlane(d[0]);
+  t.c = __builtin_amdgcn_readfirstlane(d[1]);
+  t.r = __builtin_amdgcn_readfirstlane(d[2]);
+  t.row0 = __builtin_amdgcn_readfirstlane(d[3]);
+  t.nrows = __builtin_amdgcn_readfirstlane(d[4]);
+  t.ngr = __builtin_amdgcn_readfirstlane(d[5]);
+  t.flags = __builtin_amdgcn_readfirstlane(d[6]);
+  t.slot = __builtin_amdgcn_readfirstlane(d[7]);
+  t.c1 = __int_as_float(__builtin_amdgcn_readfirstlane(d[8]));
+#pragma unroll
+  for (int g = 0; g < G; ++g) t.trow[g] = __builtin_amdgcn_readfirstlane(d[9 + g]);
   return t;
 }
 
-// Wave 0 fills the entries of iterations [i0, i0 + n) (n <= 64) of this workgroup.
-template <int G>
-__device__ inline void ring_fill(const VerifyParams& p, TaskRing<G>& ring, int i0, int n, int total) {
-  const int lane = lane_id();
-  if (wave_id() == 0 && lane < n) {
-    const int i = i0 + lane;
-    const int64_t t = (int64_t)blockIdx.x + (int64_t)i * gridDim.x;
-    int4 a = make_int4(-1, 0, 0, 1 | 1 << 8);
-    float c1 = 1.f;
-    if (t < total) {
-      const int gi = (int)(t / p.nc);
-      const int4 d = p.grp_desc[gi];
-      a = make_int4((int)(t - (int64_t)gi * p.nc), d.x, d.y, d.z);
-      c1 = __int_as_float(d.w);
-    }
-    const int slot = i % kRing;
-    ring.d[slot] = a;
-    ring.c1[slot] = c1;
-    const int nrows = a.w & 0xff;
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-      ring.trow[slot][g] = a.x < 0 ? 0 : (int)target_row(p, a.z + min(g, nrows - 1));
+// Per-request metadata in LDS for the fused kernel: first verify row, rows (clamped as by
+// req_range) with the flags above bit 16, and log2(e) / T.
+struct RequestMeta {
+  int* begin;
+  int* kflags;
+  float* c1;
+};
+
+// Group offsets (build_lds_groups) and the request metadata, built by every workgroup.
+__device__ inline void build_lds_requests(const VerifyParams& p, int* goff, const RequestMeta& m) {
+  build_lds_groups(p, goff);
+  for (int r = threadIdx.x; r < p.B; r += kVThreads) {
+    int b, k;
+    req_range(p, r, b, k);
+    const bool greedy = req_is_greedy(p, r);
+    const int flags = (greedy ? kGreedy : 0) | (!greedy && !p.recovered ? kFull : 0);
+    m.begin[r] = b;
+    m.kflags[r] = k | flags << 16;
+    m.c1[r] = exp2_scale(req_temperature(p, r));
   }
+  __syncthreads();
 }
 
-template <int DT, int EPT, int G, bool HAS_DRAFT>
+// Ticket t -> task, run by a whole wave with t wave-uniform: the request comes from the LDS
+// group offsets (scanning forward from this workgroup's previous decode, `scan`, since its
+// tickets only rise), its metadata from LDS; target rows from scalar loads.  The fields
+// follow group_desc.
+template <int G>
+__device__ inline FusedTask<G> fused_decode(const VerifyParams& p, const int* goff,
+                                            const RequestMeta& m, int total, int t, int& scan) {
+  FusedTask<G> d = no_task<G>();
+  if (t < 0 || t >= total) return d;
+  const int li = t / p.nc;
+  int r = goff[scan] <= li ? scan : 0;
+  while (goff[r + 1] <= li) ++r;  // goff[B] = groups > li ends the scan
+  r = __builtin_amdgcn_readfirstlane(r);
+  scan = r;
+  const int b = __builtin_amdgcn_readfirstlane(m.begin[r]);
+  const int kf = __builtin_amdgcn_readfirstlane(m.kflags[r]);
+  const int g0 = __builtin_amdgcn_readfirstlane(goff[r]);
+  const int g1 = __builtin_amdgcn_readfirstlane(goff[r + 1]);
+  const int k = kf & 0xffff;
+  const int g = li - g0;
+  d.t = t;
+  d.c = t - li * p.nc;
+  d.r = r;
+  d.row0 = b + g * G;
+  d.nrows = min(G, k - g * G);
+  d.ngr = g1 - g0;
+  d.flags = kf >> 16;
+  d.c1 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m.c1[r])));
+  int tr[G];
+#pragma unroll
+  for (int gg = 0; gg < G; ++gg) tr[gg] = d.row0 + min(gg, d.nrows - 1);
+  if (p.target_rows) {
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) tr[gg] = ld_const(p.target_rows, tr[gg]);
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg)
+      tr[gg] = tr[gg] < 0 ? 0 : (tr[gg] >= p.target_num_rows ? (int)p.target_num_rows - 1 : tr[gg]);
+  }
+#pragma unroll
+  for (int gg = 0; gg < G; ++gg) d.trow[gg] = tr[gg];
+  return d;
+}
+
+template <int DT, int EPT, int G>
+struct FusedX {
+  u32x4 x[G][EPT / Elem<DT>::kVec];  // target sub-chunk of a task
+};
+
+template <int DT, int EPT, int G>
+struct FusedQ {
+  u32x4 q[G][EPT / 4];  // draft sub-chunk
+  u32x4 e[EPT / 4];     // noise sub-chunk
+};
+
+template <int DT, int EPT, int G, bool HAS_DRAFT, bool MASKED>
 __global__ __launch_bounds__(kVThreads) MVSD_FUSED_ATTRS void verify_fused_kernel(VerifyParams p) {
   static_assert(EPT % Elem<DT>::kVec == 0, "EPT must be a multiple of the vector width");
+  static_assert(9 + G <= kTaskInts, "task record size");
+  static_assert(kVWaves % G == 0, "the stats polls give every row whole waves");
+  static_assert(G <= kWave, "one lane per row combines the row statistics");
   using S = typename Elem<DT>::storage;
-  constexpr int NV = EPT / Elem<DT>::kVec;
+  using Task = FusedTask<G>;
+  using XBuf = FusedX<DT, EPT, G>;
+  using QBuf = FusedQ<DT, EPT, G>;
+  constexpr int VEC = Elem<DT>::kVec;
+  constexpr int NV = EPT / VEC;
   constexpr int N32 = EPT / 4;
-  constexpr int R = 4;  // stats slots per lane held from one poll (nc <= 256 on the fast path)
-  __shared__ u32x4 s_x[kLag + 1][G][NV][kVThreads];  // parked target chunks
-  __shared__ TaskRing<G> s_ring;
-  __shared__ float s_red[G * kVWaves];
-  __shared__ uint64_t s_key[G * kVWaves];
-  __shared__ float s_M[G];
-  __shared__ float s_L[G];
+  constexpr int SUB = kVThreads * EPT;
+  constexpr int PR = kVThreads / G;  // poll threads per row: a row's nc <= PR stats slots
+  constexpr int WPR = kVWaves / G;   // waves per row
+  __shared__ u32x4 s_park[kDepth][G][NV][kVThreads];
+  __shared__ int s_fifo[kFifo][kTaskInts];
+  __shared__ int s_dec[2][kTaskInts];
+  __shared__ int s_fin[2][2][2];
+  __shared__ float s_pm[kVWaves], s_ps[kVWaves];
+  __shared__ int s_rdy[kVWaves];
+  __shared__ float s_wm[G * kVWaves], s_ws[G * kVWaves];
+  __shared__ uint64_t s_keyD[G * kVWaves], s_keyF[G * kVWaves];
   __shared__ int s_last;
   __shared__ FinalizeSmem fsm;
+  __shared__ int s_goff[kMaxFusedRequests + 1];
+  __shared__ int s_rbegin[kMaxFusedRequests], s_rkf[kMaxFusedRequests];
+  __shared__ float s_rc1[kMaxFusedRequests];
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wid = wave_id();
   const int nc = p.nc;
-  const int total = p.grp_off[p.B] * nc;
   const S* target = static_cast<const S*>(p.target);
+  const float* dummy = reinterpret_cast<const float*>(p.stat_slots);  // 16-byte aligned, valid
+  int* ticket = &p.qticket[0];
+  const RequestMeta meta{s_rbegin, s_rkf, s_rc1};
 
-  ring_fill<G>(p, s_ring, 0, kRing, total);
-  __syncthreads();
-  // tasks of this workgroup: blockIdx.x + k * grid < total
-  const int n_iter = (int)((total - (int64_t)blockIdx.x + gridDim.x - 1) / gridDim.x);
+  build_lds_requests(p, s_goff, meta);
+  const int total = s_goff[p.B] * nc;
 
-  // Loads of an iteration's data: target chunk of task tx, draft / noise of task tq.
-  // Every load is an unconditional 16-byte load at a clamped in-bounds address (the host
-  // uses this kernel only for aligned rows with V a multiple of the vector width); absent
-  // tasks and rows past a group's end load duplicates.  Columns past vend are masked where
-  // the data is consumed.
-  auto issue = [&](FusedBuf<DT, EPT, G>& b, const FusedTask& tx, int ix, const FusedTask& tq) {
-    {
-      const int64_t v0 = tx.c < 0 ? 0 : (int64_t)tx.c * p.chunk;
-      const int64_t vlast = min((int64_t)p.V, v0 + p.chunk) - Elem<DT>::kVec;
+  // ---- loads (unconditional; a task that is absent loads one line with every lane) ----
+  auto issue_x = [&](XBuf& b, const Task& t) {
+    const bool live = t.t >= 0;
+    const int64_t v0 = (int64_t)t.c * SUB;
+    const int64_t vlast = min((int64_t)p.V, v0 + SUB) - VEC;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const S* base = target + (int64_t)t.trow[g] * p.target_stride;
+#pragma unroll
+      for (int n = 0; n < NV; ++n)
+        b.x[g][n] = load_target16<true>(base + (live ? min(vec_col<DT>(v0, n), vlast) : 0));
+    }
+  };
+  // Draft / noise sub-chunks of task o.
+  auto issue_q = [&](QBuf& b, const Task& o, bool live) {
+    const int64_t v0 = (int64_t)o.c * SUB;
+    const int64_t vlast4 = min((int64_t)p.V, v0 + SUB) - 4;
+    auto col32 = [&](int m) -> int64_t {
+      return live ? min(vec_col<DT>(v0, m / (VEC / 4)) + (m % (VEC / 4)) * 4, vlast4) : 0;
+    };
+    if constexpr (HAS_DRAFT) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const S* base = target + (int64_t)s_ring.trow[ix % kRing][g] * p.target_stride;
+        const float* base = live ? p.draft + (int64_t)(o.row0 + min(g, o.nrows - 1)) * p.draft_stride : dummy;
 #pragma unroll
-        for (int n = 0; n < NV; ++n)
-          b.x[g][n] = load_target16<true>(base + min(vec_col<DT>(v0, n), vlast));
+        for (int m = 0; m < N32; ++m)
+          b.q[g][m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + col32(m)));
       }
     }
-    {
-      const bool absent = tq.c < 0 || !(tq.flags & kFull);
-      const int64_t v0 = absent ? 0 : (int64_t)tq.c * p.chunk;
-      const int64_t vlast = min((int64_t)p.V, v0 + p.chunk) - 4;
-      constexpr int VEC = Elem<DT>::kVec;
-      if constexpr (HAS_DRAFT) {
+    const float* eb = live ? p.noise + (int64_t)o.r * p.noise_stride : dummy;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float* base = p.draft + (int64_t)(absent ? 0 : tq.row0 + min(g, tq.nrows - 1)) * p.draft_stride;
+    for (int m = 0; m < N32; ++m)
+      b.e[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(eb + col32(m)));
+  };
+  // Stats polls of task o's group: thread tid covers slot tid % PR of row tid / PR (rows past
+  // the group's end, and no task, poll one line).
+  auto issue_poll = [&](const Task& o, bool live) -> uint64_t {
+    const int g = tid / PR, c = tid % PR;
+    const uint64_t* sl = p.stat_slots;
+    if (live) sl += (int64_t)(o.row0 + min(g, o.nrows - 1)) * nc + (g < o.nrows ? min(c, nc - 1) : 0);
+    return slot_load(sl);
+  };
+
+  // ---- stage 1 of task t (target sub-chunk in xb): stats or greedy argmax; park ----
+  auto stage_one = [&](const XBuf& xb, const Task& t, int slot) {
+    const int64_t v0 = (int64_t)t.c * SUB;
+    const int64_t vend = min((int64_t)p.V, v0 + SUB);
+    float4 mk[G];
 #pragma unroll
-          for (int m = 0; m < N32; ++m)
-            b.q[g][m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-                base + min(vec_col<DT>(v0, m / (VEC / 4)) + (m % (VEC / 4)) * 4, vlast)));
-        }
-      }
-      const float* eb = p.noise + (int64_t)(absent ? 0 : tq.r) * p.noise_stride;
-#pragma unroll
-      for (int m = 0; m < N32; ++m)
-        b.e[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-            eb + min(vec_col<DT>(v0, m / (VEC / 4)) + (m % (VEC / 4)) * 4, vlast)));
+    for (int g = 0; g < G; ++g) {
+      mk[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (MASKED) mk[g] = ld_const(p.masks, t.row0 + min(g, t.nrows - 1));
     }
-  };
-
-  // Deferred request-completion counts (one from the stats / argmax step, one from the score
-  // step): each atomic's result is examined one iteration later.
-  struct Pending {
-    int cnt, r, target, greedy, full;
-  };
-  Pending pa{0, -1, 0, 0, 0}, pb{0, -1, 0, 0, 0};
-  auto settle_one = [&](Pending& pd) {
-    if (pd.r >= 0) {
-      if (tid == 0) s_last = pd.cnt == pd.target - 1;
-      __syncthreads();
-      if (s_last) finalize_request(p, p.grp_off, pd.r, pd.greedy, pd.full, fsm);
-      __syncthreads();
-      pd.r = -1;
-    }
-  };
-  auto count = [&](Pending& pd, const FusedTask& t, bool greedy, bool full) {
-    if (tid == 0) pd.cnt = atomic_add_relaxed(&p.req_cnt[t.r], 1);
-    pd.r = t.r;
-    pd.target = t.ngr * nc;
-    pd.greedy = greedy;
-    pd.full = full;
-  };
-
-  // One iteration (task i's stats, task i-L's scores).  Returns false when this workgroup is
-  // done.
-  auto iteration = [&](int i) -> bool {
-    if (i >= n_iter + kLag) return false;
-    FusedTask tp = ring_task<G>(s_ring, i + kRing - kLag);  // task i - kLag
-    const FusedTask tc = ring_task<G>(s_ring, i);
-    const bool b_live = i >= kLag && tp.c >= 0 && (tp.flags & kFull);
-    if (!b_live) tp.c = -1;
-    FusedBuf<DT, EPT, G> cur;
-
-    // ---- 1. stats-slot polls and draft ids for task i - kLag, then this iteration's data ----
-    uint64_t pv[R];
-    int dp[G];
-    {
-      if (b_live && wid < tp.nrows) {
-        const uint64_t* slots = p.stat_slots + (int64_t)(tp.row0 + wid) * nc;
-#pragma unroll
-        for (int j = 0; j < R; ++j) pv[j] = slot_load(slots + min(lane + j * kWave, nc - 1));
-      }
+    if (slot >= 0) {
 #pragma unroll
       for (int g = 0; g < G; ++g)
-        dp[g] = HAS_DRAFT ? -1 : p.draft_ids[b_live ? tp.row0 + min(g, tp.nrows - 1) : 0];
-    }
-    issue(cur, tc, i, tp);
-    settle_one(pa);
-    settle_one(pb);
-    // Ring refill at i = 32 k + kLag (k >= 1): entries [32 k + 32, 32 k + 64) replace
-    // entries [32 k - 32, 32 k), all older than the oldest one still needed (i - kLag).
-    if (i >= kRing / 2 + kLag && (i - kLag) % (kRing / 2) == 0) {
-      __syncthreads();
-      ring_fill<G>(p, s_ring, i - kLag + kRing / 2, kRing / 2, total);
-    }
-
-    // ---- 2. task i: stats (or greedy argmax), park the chunk in LDS ----
-    if (tc.c >= 0) {
-      const int64_t v0 = (int64_t)tc.c * p.chunk;
-      const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
-      const bool greedy = tc.flags & kGreedy;
-      const bool full = tc.flags & kFull;
-      // target value k of row g, -inf past vend (FAST: the chunk is full)
-      auto xval = [&](int g, int k, auto fast) {
-        const float v = raw_elem<DT>(cur.x[g], k);
-        if constexpr (decltype(fast)::value) return v;
-        else return elem_index<DT, EPT>(v0, k) < vend ? v : -INFINITY;
-      };
-      auto reduce = [&](auto fast) {
-        if (greedy) {
-          uint64_t key[G];
+        if (g < t.nrows) {
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            float bv = -INFINITY;
-            int bi = (int)v0;
-            if (g < tc.nrows) {
-#pragma unroll
-              for (int k = 0; k < EPT; ++k) {
-                const float v = xval(g, k, fast);
-                const bool take = (v > bv) | ((v != v) & (bv == bv));
-                bv = take ? v : bv;
-                bi = take ? elem_index<DT, EPT>(v0, k) : bi;
-              }
-            }
-            key[g] = argmax_key(bv, bi);
-          }
-          const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
-          if (tid < tc.nrows) slot_store(p.arg_slots + (int64_t)(tc.row0 + tid) * nc + tc.c, best);
-        } else {
-          float M[G];
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            float mm = -INFINITY;
-            if (g < tc.nrows) {
-#pragma unroll
-              for (int k = 0; k < EPT; ++k) mm = fmaxf(mm, xval(g, k, fast));
-            }
-            M[g] = mm;
-          }
-          block_max<G, kVWaves>(M, s_red);
-          float sm[G];
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const float ref = M[g] == -INFINITY ? 0.f : M[g];
-            float acc = 0.f;
-            if (g < tc.nrows) {
-#pragma unroll
-              for (int k = 0; k < EPT; ++k)
-                acc += __builtin_amdgcn_exp2f((xval(g, k, fast) - ref) * tc.c1);
-            }
-            sm[g] = acc;
-          }
-          const float srow = block_sum_to_row_thread<G, kVWaves>(sm, s_red);
-          if (tid < tc.nrows) {
-            const float mrow = row_of_thread<G>(M);
-            slot_store(p.stat_slots + (int64_t)(tc.row0 + tid) * nc + tc.c,
-                       pack_stats(mrow, mrow == -INFINITY ? 0.f : srow));
-          }
+          for (int n = 0; n < NV; ++n) s_park[slot][g][n][tid] = xb.x[g][n];
         }
-      };
-      if (vend - v0 == p.chunk) reduce(Fast<true>());
-      else reduce(Fast<false>());
-      if (full) {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int n = 0; n < NV; ++n) s_x[i % (kLag + 1)][g][n][tid] = cur.x[g][n];
-      }
-      if (!full) count(pa, tc, greedy, false);
     }
-
-    // ---- 3. task i - kLag: recovered-token scores ----
-    if (b_live) {
-      if (wid < tp.nrows) {
-        bool ready = true;
-#pragma unroll
-        for (int j = 0; j < R; ++j) ready &= pv[j] != 0;
-        float mx, sum;
-        if (__all(ready) && nc <= R * kWave) {
-          float m = -INFINITY;
-#pragma unroll
-          for (int j = 0; j < R; ++j)
-            if (lane + j * kWave < nc) m = fmaxf(m, unpack_stats(pv[j]).x);
-          mx = wave_max(m);
-          float acc = 0.f;
-#pragma unroll
-          for (int j = 0; j < R; ++j) {
-            const float2 st = unpack_stats(pv[j]);
-            if (lane + j * kWave < nc && st.x != -INFINITY)
-              acc += st.y * exp2f((st.x - mx) * tp.c1);
-          }
-          sum = wave_sum(acc);
-        } else if (!wave_row_stats(p.stat_slots + (int64_t)(tp.row0 + wid) * nc, nc, tp.c1, &p.ctrl[1], mx, sum) &&
-                   lane == 0) {
-          atomic_store_relaxed(&p.ctrl[1], 1);
-        }
-        if (lane == 0) {
-          s_M[wid] = mx;
-          s_L[wid] = (float)(-log2((double)sum));
-        }
-      }
-      __syncthreads();
-      const int64_t v0 = (int64_t)tp.c * p.chunk;
-      const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
-      float inv[EPT];
-#pragma unroll
-      for (int k = 0; k < EPT; ++k) inv[k] = recip_rn(raw_f32(cur.e, k));
+    if (t.flags & kGreedy) {
       uint64_t key[G];
-      auto score_rows = [&](auto fast) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float bv = 0.f;  // scores are >= 0: the clamp is folded into the strict compare
-          int bi = (int)v0;
-          if (g < tp.nrows) {
-            const float MX = s_M[g];
-            const float NL = s_L[g];
-            const int d = dp[g];
-            u32x4 xr[NV];
+      for (int g = 0; g < G; ++g) {
+        float bv = -INFINITY;
+        int bi = (int)v0;
+        if (g < t.nrows) {
 #pragma unroll
-            for (int n = 0; n < NV; ++n) xr[n] = s_x[(i - kLag) % (kLag + 1)][g][n][tid];
-#pragma unroll
-            for (int k = 0; k < EPT; ++k) {
-              const int idx = elem_index<DT, EPT>(v0, k);
-              const float prob = __builtin_amdgcn_exp2f(fmaf(raw_elem<DT>(xr, k) - MX, tp.c1, NL));
-              float w;
-              if constexpr (HAS_DRAFT) w = prob - raw_f32(cur.q[g], k);
-              else w = idx == d ? 0.f : prob;
-              const float score = w * inv[k];
-              // columns rise with k, so a strict compare keeps the first maximum
-              bool take = score > bv;
-              if constexpr (!decltype(fast)::value) take &= idx < vend;
-              bv = take ? score : bv;
-              bi = take ? idx : bi;
-            }
+          for (int k = 0; k < EPT; ++k) {
+            const int idx = elem_index<DT, EPT>(v0, k);
+            float v = raw_elem<DT>(xb.x[g], k);
+            if constexpr (MASKED) v = row_masked(mk[g], v, idx) ? -INFINITY : v;
+            // columns rise with k: a strict compare keeps the first maximum; NaN wins
+            const bool take = ((v > bv) | ((v != v) & (bv == bv))) & (idx < vend);
+            bv = take ? v : bv;
+            bi = take ? idx : bi;
           }
-          key[g] = argmax_key(bv, bi);
         }
-      };
-      if (vend - v0 == p.chunk) score_rows(Fast<true>());
-      else score_rows(Fast<false>());
-      const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
-      if (tid < tp.nrows) slot_store(p.arg_slots + (int64_t)(tp.row0 + tid) * nc + tp.c, best);
-      count(pb, tp, false, true);
+        key[g] = argmax_key(bv, bi);
+      }
+      const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_keyD);
+      if (tid < t.nrows) slot_store(p.arg_slots + (int64_t)(t.row0 + tid) * p.arg_stride + t.c, best);
+      return;
+    }
+    // per wave and row: the raw max m and sum of exp2((x - m) c1) (masked entries add
+    // nothing; the max runs over every entry, which only moves the reference point), then
+    // the row threads combine the waves' pairs
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (g < t.nrows) {
+        float x[EPT];
+        float m = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+          x[k] = elem_index<DT, EPT>(v0, k) < vend ? raw_elem<DT>(xb.x[g], k) : -INFINITY;
+          m = fmaxf(m, x[k]);
+        }
+        m = wave_max(m);
+        const float ref = m == -INFINITY ? 0.f : m;
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+          const float e = __builtin_amdgcn_exp2f((x[k] - ref) * t.c1);
+          if constexpr (MASKED) acc += row_masked(mk[g], x[k], elem_index<DT, EPT>(v0, k)) ? 0.f : e;
+          else acc += e;
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) {
+          s_wm[g * kVWaves + wid] = m;
+          s_ws[g * kVWaves + wid] = acc;
+        }
+      }
     }
     __syncthreads();
+    if (tid < t.nrows) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kVWaves; ++w) M = fmaxf(M, s_wm[tid * kVWaves + w]);
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kVWaves; ++w) {
+        const float mw = s_wm[tid * kVWaves + w];
+        if (mw != -INFINITY) sum += s_ws[tid * kVWaves + w] * __builtin_amdgcn_exp2f((mw - M) * t.c1);
+      }
+      slot_store(p.stat_slots + (int64_t)(t.row0 + tid) * nc + t.c,
+                 pack_stats(M, M == -INFINITY ? 0.f : sum));
+    }
+  };
+
+  // ---- stage 2 of task o: combine its group's stats, score, publish ----
+  auto partial = [&](uint64_t v, bool live, float c1) {
+    float m = live ? unpack_stats(v).x : -INFINITY;
+    m = wave_max(m);
+    const float2 st = unpack_stats(v);
+    float a = (live && st.x != -INFINITY) ? st.y * exp2f((st.x - m) * c1) : 0.f;
+    a = wave_sum(a);
+    if (lane == 0) {
+      s_pm[wid] = m;
+      s_ps[wid] = a;
+    }
+  };
+  // qb: o's draft / noise sub-chunks (loaded for ticket qtag: reloaded here when that is not o,
+  // after a postponed retirement); poll: this iteration's stats-slot poll of o's group.
+  auto stage_two = [&](QBuf& qb, int qtag, uint64_t poll, const Task& o) {
+    const int g = wid / WPR, c = tid % PR;
+    const bool live = g < o.nrows && c < nc;
+    partial(poll, live, o.c1);
+    const int rdy = __all(!live || poll != 0);  // the vote needs every lane active
+    if (lane == 0) s_rdy[wid] = rdy;
+    if (qtag != o.t) issue_q(qb, o, true);
+    XBuf xr;  // the target sub-chunk of a task that was not parked
+    if (o.slot < 0) issue_x(xr, o);
+    __syncthreads();
+    bool ready = true;
+#pragma unroll
+    for (int w = 0; w < kVWaves; ++w) ready &= s_rdy[w] != 0;
+    if (!ready) {  // some chunk of the group has not published yet: each wave waits for its slots
+      if (g < o.nrows) {
+        const uint64_t* sl = p.stat_slots + (int64_t)(o.row0 + g) * nc + min(c, nc - 1);
+        uint64_t v = 0;
+        for (int spins = 0;; ++spins) {
+          v = slot_load(sl);
+          if (__all(c >= nc || v != 0)) break;
+          if (spins >= kSpinLimit || ((spins & 255) == 255 && atomic_load_relaxed(&p.ctrl[1]) != 0)) {
+            if (lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+        partial(v, c < nc, o.c1);
+      }
+      __syncthreads();
+    }
+    // lane gg < nrows of every wave combines row gg's partials; the values are broadcast
+    float myM = 0.f, myL = 0.f;
+    if (lane < o.nrows) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < WPR; ++w) M = fmaxf(M, s_pm[lane * WPR + w]);
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < WPR; ++w) {
+        const float mw = s_pm[lane * WPR + w];
+        if (mw != -INFINITY) sum += s_ps[lane * WPR + w] * exp2f((mw - M) * o.c1);
+      }
+      myM = M;
+      myL = (float)(-log2((double)sum));
+    }
+    const int64_t v0 = (int64_t)o.c * SUB;
+    const int64_t vend = min((int64_t)p.V, v0 + SUB);
+    float inv[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) inv[k] = recip_rn(raw_f32(qb.e, k));
+    uint64_t key[G];
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) {
+      float bv = 0.f;  // scores are >= 0: the clamp is folded into the strict compare
+      int bi = (int)v0;
+      if (gg < o.nrows) {
+        const int row = o.row0 + gg;
+        const float MX = readlane_f32(myM, gg);
+        const float NL = readlane_f32(myL, gg);
+        float4 mk = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (MASKED) mk = ld_const(p.masks, row);
+        int d = -1;
+        if constexpr (!HAS_DRAFT) d = ld_const(p.draft_ids, row);
+        u32x4 xv[NV];
+        if (o.slot >= 0) {
+#pragma unroll
+          for (int n = 0; n < NV; ++n) xv[n] = s_park[o.slot][gg][n][tid];
+        } else {
+#pragma unroll
+          for (int n = 0; n < NV; ++n) xv[n] = xr.x[gg][n];
+        }
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+          const int idx = elem_index<DT, EPT>(v0, k);
+          const float x = raw_elem<DT>(xv, k);
+          float prob = __builtin_amdgcn_exp2f(fmaf(x - MX, o.c1, NL));  // softmax
+          if constexpr (MASKED) prob = row_masked(mk, x, idx) ? 0.f : prob;
+          float w;
+          if constexpr (HAS_DRAFT) w = prob - raw_f32(qb.q[gg], k);
+          else w = idx == d ? 0.f : prob;
+          const float score = w * inv[k];
+          // columns rise with k, so a strict compare keeps the first maximum
+          const bool take = (score > bv) & (idx < vend);
+          bv = take ? score : bv;
+          bi = take ? idx : bi;
+        }
+      }
+      key[gg] = argmax_key(bv, bi);
+    }
+    const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_keyF);
+    if (tid < o.nrows) slot_store(p.arg_slots + (int64_t)(o.row0 + tid) * p.arg_stride + o.c, best);
+  };
+
+  // ---- uniform pipeline state ----
+  int head = 0, size = 0, free_mask = (1 << kDepth) - 1;
+  bool claims_done = false;
+  bool x_claim = false;               // a claim issued at the last mid point
+  int x_r0 = -1, x_t0 = 0, x_f0 = 0;  // counts issued at the last mid point: request, tasks
+  int x_r1 = -1, x_t1 = 0, x_f1 = 0;  // of the request, greedy | full << 1
+  int pd_r = -1, pd_t = 0, pd_f = 0;  // count of this iteration's stage 1
+  int pf_r = -1, pf_t = 0;            // count of the last retirement (full tasks)
+  int res_claim = 0, res_c0 = 0, res_c1 = 0;  // thread 0: results of the mid-point atomics
+  int scan = 0;                               // wave 0: request cursor of the decodes
+  int qtag_a = -1, qtag_b = -1;               // tickets whose draft / noise are in qa / qb
+
+  // first two tickets, decoded before the loop; the third claim is in flight
+  if (wid == 0) {
+    int ta = 0, tb = 0;
+    if (lane == 0) {
+      ta = atomic_add_relaxed(ticket, 1);
+      tb = atomic_add_relaxed(ticket, 1);
+    }
+    ta = __builtin_amdgcn_readfirstlane(ta);
+    tb = __builtin_amdgcn_readfirstlane(tb);
+    const Task a = fused_decode<G>(p, s_goff, meta, total, ta, scan);
+    const Task b = fused_decode<G>(p, s_goff, meta, total, tb, scan);
+    if (lane == 0) {
+      task_put<G>(s_fifo[0], a);
+      task_put<G>(s_fifo[1], b);
+    }
+  }
+  __syncthreads();
+  Task cur = task_get<G>(s_fifo[0]);
+  Task nxt = task_get<G>(s_fifo[1]);
+  __syncthreads();
+  claims_done = nxt.t < 0;
+  x_claim = !claims_done;
+  if (tid == 0 && x_claim) res_claim = atomic_add_relaxed(ticket, 1);
+
+  XBuf xa, xb;
+  QBuf qa, qb;
+  issue_x(xa, cur);
+
+  // xc: the current task's target (loaded last iteration), xn: receives the next task's;
+  // qc: draft / noise of the task due now (tag qtc), qn: receives those of the next due task.
+  auto iteration = [&](XBuf& xc, XBuf& xn, QBuf& qc, int& qtc, QBuf& qn, int& qtn,
+                       const int par) -> bool {
+    if (cur.t < 0 && nxt.t < 0 && size == 0 && !x_claim && x_r0 < 0 && x_r1 < 0 && pf_r < 0)
+      return false;
+    // ---- plan: retire the FIFO's oldest task once it holds kDepth (or when draining) ----
+    const bool push = cur.t >= 0 && (cur.flags & kFull);
+    const bool due = size + (push ? 1 : 0) >= kDepth || (cur.t < 0 && size > 0);
+    const Task o = due ? task_get<G>(s_fifo[head]) : no_task<G>();
+    // the task due next iteration, assuming this retirement goes ahead: prefetch its draft /
+    // noise now (a postponed retirement makes stage 2 reload them)
+    const int size_next = size + (push ? 1 : 0) - (due ? 1 : 0);
+    const bool push_next = nxt.t >= 0 && (nxt.flags & kFull);
+    const bool due_next = size_next + (push_next ? 1 : 0) >= kDepth || (nxt.t < 0 && size_next > 0);
+    Task on = no_task<G>();
+    if (due_next) {
+      const int k = due ? 1 : 0;  // position of the next oldest task
+      if (k < size) on = task_get<G>(s_fifo[(head + k) & (kFifo - 1)]);
+      else on = cur;  // the task pushed by this iteration
+    }
+
+    // ---- loads: o's stats polls, the next due task's draft / noise, the next task's target ----
+    const uint64_t poll = issue_poll(o, due);
+    issue_q(qn, on, due_next);
+    qtn = due_next ? on.t : -1;
+    issue_x(xn, nxt);
+
+    // ---- stage 1 of the current task ----
+    if (cur.t >= 0) {
+      int slot = -1;
+      if (push && free_mask) {
+        slot = __builtin_ctz(free_mask);
+        free_mask &= ~(1 << slot);
+      }
+      stage_one(xc, cur, slot);
+      if (push) {
+        if (tid == 0) {
+          Task e = cur;
+          e.slot = slot;
+          task_put<G>(s_fifo[(head + size) & (kFifo - 1)], e);
+        }
+        ++size;
+      } else {
+        pd_r = cur.r;
+        pd_t = cur.ngr * nc;
+        pd_f = (cur.flags & kGreedy) ? 1 : 0;
+      }
+    }
+
+    // ---- mid point (wave 0): read the last mid point's atomics, issue this one's ----
+    const bool claim = !claims_done && size + 4 < kFifo;
+    if (wid == 0) {
+      const int rc = __builtin_amdgcn_readfirstlane(res_claim);
+      const int r0v = __builtin_amdgcn_readfirstlane(res_c0);
+      const int r1v = __builtin_amdgcn_readfirstlane(res_c1);
+      if (lane == 0) {
+        if (claim) res_claim = atomic_add_relaxed(ticket, 1);
+        if (pd_r >= 0) res_c0 = atomic_add_relaxed(&p.req_cnt[pd_r], 1);
+        if (pf_r >= 0) res_c1 = atomic_add_relaxed(&p.req_cnt[pf_r], 1);
+      }
+      const Task d = x_claim ? fused_decode<G>(p, s_goff, meta, total, rc, scan) : no_task<G>();
+      if (lane == 0) {
+        task_put<G>(s_dec[par], d);
+        s_fin[par][0][0] = x_r0 >= 0 && r0v == x_t0 - 1 ? x_r0 : -1;
+        s_fin[par][0][1] = x_f0;
+        s_fin[par][1][0] = x_r1 >= 0 && r1v == x_t1 - 1 ? x_r1 : -1;
+        s_fin[par][1][1] = x_f1;
+        if (!claims_done && !claim) atomic_store_relaxed(&p.ctrl[1], 1);  // FIFO bound broken
+      }
+    }
+    const bool had_claim = x_claim;
+    x_claim = claim;
+    x_r0 = pd_r;
+    x_t0 = pd_t;
+    x_f0 = pd_f;
+    x_r1 = pf_r;
+    x_t1 = pf_t;
+    x_f1 = 2;
+    pd_r = -1;
+    pf_r = -1;
+    if (!claim) claims_done = true;
+
+    // ---- stage 2 of the due task, unless this workgroup holds an unpublished ticket of its
+    // group (the next task's, whose loads are in flight; later ones are newer) ----
+    if (due && (nxt.t < 0 || nxt.t >= (o.t / nc + 1) * nc)) {
+      stage_two(qc, qtc, poll, o);
+      head = (head + 1) & (kFifo - 1);
+      --size;
+      if (o.slot >= 0) free_mask |= 1 << o.slot;
+      pf_r = o.r;
+      pf_t = o.ngr * nc;
+    } else if (due) {
+      qtn = -1;  // postponed: the next iteration retires o again and reloads its data
+    }
+
+    // ---- end: completions found at the mid point, the decoded claim becomes the next task ----
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int fr = __builtin_amdgcn_readfirstlane(s_fin[par][k][0]);
+      if (fr >= 0) {
+        const int ff = __builtin_amdgcn_readfirstlane(s_fin[par][k][1]);
+        finalize_request(p, s_goff, fr, ff & 1, ff & 2, fsm);
+        __syncthreads();
+      }
+    }
+    const Task d = task_get<G>(s_dec[par]);
+    if (had_claim && d.t < 0) claims_done = true;
+    cur = nxt;
+    nxt = had_claim ? d : no_task<G>();
     return true;
   };
 
-  for (int i = 0; iteration(i); ++i) {
+  for (;;) {
+    if (!iteration(xa, xb, qa, qtag_a, qb, qtag_b, 0)) break;
+    if (!iteration(xb, xa, qb, qtag_b, qa, qtag_a, 1)) break;
   }
-  settle_one(pa);
-  settle_one(pb);
 
-  // The last workgroup out returns the group tables and exit counter to zero.
+  // The last workgroup out (every other one has made its final claim) returns the ticket and
+  // the exit counter to zero.
   if (tid == 0) s_last = atomic_add_relaxed(&p.ctrl[2], 1) == (int)gridDim.x - 1;
   __syncthreads();
-  if (s_last) {
-    for (int i = tid; i <= p.B; i += kVThreads) p.grp_off[i] = 0;
-    for (int i = tid; i < total / nc; i += kVThreads) {
-      p.grp_desc[i] = make_int4(0, 0, 0, 0);
-      p.qgi[i] = 0;
-    }
-    for (int q = tid; q < p.nq; q += kVThreads) {
-      p.qcount[q] = 0;
-      p.qoff[q] = 0;
-    }
-    if (tid == 0) atomic_store_relaxed(&p.ctrl[2], 0);
+  if (s_last && tid == 0) {
+    atomic_store_relaxed(ticket, 0);
+    atomic_store_relaxed(&p.ctrl[2], 0);
   }
 }
 
@@ -1538,9 +1789,17 @@ const void* kernel_for(int mode, bool has_draft, bool masked) {
     return has_draft ? reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, true, false>)
                      : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false, false>);
   }
-  if (masked) return nullptr;  // the single-read kernel does not apply sampling constraints
-  return has_draft ? reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, true>)
-                   : reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, false>);
+  if (masked)
+    return has_draft ? reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, true, true>)
+                     : reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, false, true>);
+  return has_draft ? reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, true, false>)
+                   : reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, false, false>);
+}
+
+int fused_max_chunks() {
+  const int by_poll = kVThreads / kGroup;
+  const int by_fifo = kFifo - kDepth - 5;
+  return by_poll < by_fifo ? by_poll : by_fifo;
 }
 
 const void* verify_kernel_ptr(int target_dtype, int mode, bool has_draft, bool masked) {
