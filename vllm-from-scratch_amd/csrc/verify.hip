@@ -67,6 +67,14 @@ __device__ inline float exp2_scale(float temp) {
 constexpr int kGreedy = 1;
 constexpr int kFull = 2;  // random request whose recovered ids come from in-kernel scores
 
+// Per-request metadata in LDS: first verify row, rows (clamped as by req_range) with the group
+// flags above bit 16, and log2(e) / T.
+struct RequestMeta {
+  int* begin;
+  int* kflags;
+  float* c1;
+};
+
 // ------------------------------------------------------------------ loads ------------
 // Column of element k of this thread in the sub-chunk starting at v0: 16-byte vectors of kVec
 // elements, consecutive lanes on consecutive vectors.
@@ -853,25 +861,26 @@ struct TaskDecode {
   int total, step_size, nc, lag, groups, two_phase, split;
   const int* qgi;  // queue position -> group index (nullptr: identity)
   const int* goff;  // requests' group offsets in LDS (descriptors derived), or nullptr
+  RequestMeta meta;  // request metadata in LDS (with goff)
+  int B, G;
 };
 
-// Descriptor of group li derived from the requests' group offsets (the layout of grp_desc).
-__device__ inline int4 group_desc(const VerifyParams& p, const int* goff, int li) {
-  int lo = 0, hi = p.B - 1;  // the last request whose first group is <= li owns it
+// Descriptor of group li (the layout of grp_desc) from the requests' group offsets and
+// metadata in LDS.
+__device__ inline int4 group_desc(const int* goff, const RequestMeta& m, int B, int G, int li) {
+  int lo = 0, hi = B - 1;  // the last request whose first group is <= li owns it
   while (lo < hi) {
     const int mid = (lo + hi + 1) / 2;
     if (goff[mid] <= li) lo = mid;
     else hi = mid - 1;
   }
   const int r = lo;
-  int b, k;
-  req_range(p, r, b, k);
+  const int kf = m.kflags[r];
+  const int k = kf & 0xffff;
   const int g = li - goff[r];
   const int ng = goff[r + 1] - goff[r];
-  const bool greedy = req_is_greedy(p, r);
-  const int flags = (greedy ? kGreedy : 0) | (!greedy && !p.recovered ? kFull : 0);
-  return make_int4(r, b + g * p.G, min(p.G, k - g * p.G) | ng << 8 | flags << 16 | g << 24,
-                   __float_as_int(exp2_scale(req_temperature(p, r))));
+  return make_int4(r, m.begin[r] + g * G, min(G, k - g * G) | ng << 8 | (kf >> 16) << 16 | g << 24,
+                   __float_as_int(m.c1[r]));
 }
 
 // Thread 0: decode ticket t and fetch its group descriptor into dst[0..7]
@@ -892,7 +901,7 @@ __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, i
     c = (phase_b && !half) ? w - td.nc : w;
     const int li = phase_b ? step - td.lag : step;
     if (li >= 0 && li < td.groups) {
-      d = td.goff ? group_desc(p, td.goff, li) : p.grp_desc[td.qgi ? td.qgi[li] : li];
+      d = td.goff ? group_desc(td.goff, td.meta, td.B, td.G, li) : p.grp_desc[td.qgi ? td.qgi[li] : li];
       const bool full = (d.z >> 16) & kFull;
       flags = (!phase_b || full ? 1 : 0) | (phase_b ? 2 : 0) | (half ? 4 : 0);
       if (td.split && full) {
@@ -914,11 +923,12 @@ __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, i
   dst[7] = nsplit;
 }
 
-// Group offsets of the requests (groups of ceil(K / G) rows) into goff[0..B] in LDS, built by
-// every workgroup; each thread scans a run of consecutive requests.  Requests without drafts
-// get their output row here (bonus, then -1), from workgroup r mod grid; every other row is
-// written by its finalisation.
-__device__ inline void build_lds_groups(const VerifyParams& p, int* goff) {
+// Group offsets of the requests (groups of ceil(K / G) rows) into goff[0..B] in LDS, and the
+// request metadata, built by every workgroup: each thread reads the metadata of a run of
+// consecutive requests once (the group counts wait in goff for the scan).  Requests without
+// drafts get their output row here (bonus, then -1), from workgroup r mod grid; every other
+// row is written by its finalisation.
+__device__ inline void build_lds_tables(const VerifyParams& p, int* goff, const RequestMeta& m) {
   __shared__ int s_scan[kVThreads];
   const int tid = threadIdx.x;
   const int per = (p.B + kVThreads - 1) / kVThreads;
@@ -927,7 +937,13 @@ __device__ inline void build_lds_groups(const VerifyParams& p, int* goff) {
   for (int r = r0; r < r1; ++r) {
     int b, k;
     req_range(p, r, b, k);
-    run += (k + p.G - 1) / p.G;
+    const int ng = (k + p.G - 1) / p.G;
+    goff[r] = ng;
+    run += ng;
+    const bool greedy = req_is_greedy(p, r);
+    m.begin[r] = b;
+    m.kflags[r] = k | ((greedy ? kGreedy : 0) | (!greedy && !p.recovered ? kFull : 0)) << 16;
+    m.c1[r] = exp2_scale(req_temperature(p, r));
   }
   s_scan[tid] = run;
   __syncthreads();
@@ -939,11 +955,10 @@ __device__ inline void build_lds_groups(const VerifyParams& p, int* goff) {
   }
   int acc = s_scan[tid] - run;
   for (int r = r0; r < r1; ++r) {
-    int b, k;
-    req_range(p, r, b, k);
+    const int ng = goff[r];
     goff[r] = acc;
-    acc += (k + p.G - 1) / p.G;
-    if (k == 0 && (r % (int)gridDim.x) == (int)blockIdx.x) {
+    acc += ng;
+    if (ng == 0 && (r % (int)gridDim.x) == (int)blockIdx.x) {
       int32_t* out = p.out + (int64_t)r * p.out_stride;
       for (int c = 0; c <= p.max_spec_len; ++c) out[c] = c == 0 ? p.bonus[r] : -1;
     }
@@ -964,13 +979,19 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   __shared__ FinalizeSmem fsm;
 
   __shared__ int s_goff[kMaxLdsRequests + 1];
+  __shared__ int s_rbegin[kMaxLdsRequests], s_rkf[kMaxLdsRequests];
+  __shared__ float s_rc1[kMaxLdsRequests];
 
   const int tid = threadIdx.x;
   const int queue = blockIdx.x % p.nq;
   int* ticket = &p.qticket[queue];
+  // the first ticket is claimed before the tables are built, so its round trip overlaps them
+  int tfirst = 0;
+  if (tid == 0) tfirst = atomic_add_relaxed(ticket, 1);
   const int* goff = p.grp_off;
+  const RequestMeta meta{s_rbegin, s_rkf, s_rc1};
   if (p.lds_groups) {
-    build_lds_groups(p, s_goff);
+    build_lds_tables(p, s_goff, meta);
     goff = s_goff;
   }
   const int groups = goff[p.B];
@@ -980,6 +1001,9 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   td.groups = p.lds_groups ? groups : p.qcount[queue];
   td.qgi = p.nq > 1 ? p.qgi + p.qoff[queue] : nullptr;
   td.goff = p.lds_groups ? s_goff : nullptr;
+  td.meta = meta;
+  td.B = p.B;
+  td.G = p.G;
   td.two_phase = p.two_phase;
   td.split = p.split;
   td.step_size = p.two_phase ? 2 * td.nc : td.nc;
@@ -1000,7 +1024,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
 
   // The next ticket is claimed when a task starts and decoded once the task's loads are in
   // flight, so the atomic and the descriptor fetch overlap with HBM traffic.
-  if (tid == 0) fetch_task(p, td, atomic_add_relaxed(ticket, 1), s_info[0]);
+  if (tid == 0) fetch_task(p, td, tfirst, s_info[0]);
   __syncthreads();
   for (int par = 0;; par ^= 1) {
     const int* info = s_info[par];
@@ -1202,29 +1226,6 @@ __device__ inline FusedTask<G> task_get(const int* d) {
   return t;
 }
 
-// Per-request metadata in LDS for the fused kernel: first verify row, rows (clamped as by
-// req_range) with the flags above bit 16, and log2(e) / T.
-struct RequestMeta {
-  int* begin;
-  int* kflags;
-  float* c1;
-};
-
-// Group offsets (build_lds_groups) and the request metadata, built by every workgroup.
-__device__ inline void build_lds_requests(const VerifyParams& p, int* goff, const RequestMeta& m) {
-  build_lds_groups(p, goff);
-  for (int r = threadIdx.x; r < p.B; r += kVThreads) {
-    int b, k;
-    req_range(p, r, b, k);
-    const bool greedy = req_is_greedy(p, r);
-    const int flags = (greedy ? kGreedy : 0) | (!greedy && !p.recovered ? kFull : 0);
-    m.begin[r] = b;
-    m.kflags[r] = k | flags << 16;
-    m.c1[r] = exp2_scale(req_temperature(p, r));
-  }
-  __syncthreads();
-}
-
 // Ticket t -> task, run by a whole wave with t wave-uniform: the request comes from the LDS
 // group offsets (scanning forward from this workgroup's previous decode, `scan`, since its
 // tickets only rise), its metadata from LDS; target rows from scalar loads.  The fields
@@ -1318,7 +1319,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_FUSED_ATTRS void verify_fused_kerne
   int* ticket = &p.qticket[0];
   const RequestMeta meta{s_rbegin, s_rkf, s_rc1};
 
-  build_lds_requests(p, s_goff, meta);
+  build_lds_tables(p, s_goff, meta);
   const int total = s_goff[p.B] * nc;
 
   // ---- loads (unconditional; a task that is absent loads one line with every lane) ----
