@@ -306,6 +306,24 @@ def test_fused_kernel_repeated_calls(device, monkeypatch):
     assert rs.workspace_error_flag(big.target_logits.device) == 0
 
 
+@pytest.mark.parametrize("env", [{"MVSD_VERIFY_QUARTER": "0"}, {"MVSD_VERIFY_QUARTER": "1"},
+                                 {"MVSD_VERIFY_QUARTER": "4096"}, {"MVSD_VERIFY_SPLIT": "0"},
+                                 {"MVSD_VERIFY_LAG": "3", "MVSD_VERIFY_QUARTER": "2"},
+                                 {"MVSD_VERIFY_LDS_GROUPS": "0"}],
+                         ids=["no_quarter", "quarter_1", "quarter_all_lag", "no_split",
+                              "lag3_quarter2", "init_kernel"])
+@pytest.mark.parametrize("case", ["c2", "c4_mixed"])
+def test_split_kernel_epilogue_settings(device, monkeypatch, env, case):
+    """The split kernel's epilogue (half-chunk and quarter-chunk score tasks of the last
+    groups), its lag and its group tables under non-default settings."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    w = {"c2": lambda: configs.random_c2(device, seed=61),
+         "c4_mixed": lambda: configs.ragged_c4(device, B=96, seed=62)}[case]()
+    check_parity(w, run_workload(w), oracle_for(w), f"split {case} {env}")
+    assert rs.workspace_error_flag(w.target_logits.device) == 0
+
+
 @pytest.mark.parametrize("V", [5, 1001, 4097, 8193])
 def test_odd_vocab_sizes(device, V):
     """Unaligned rows (scalar loads) and partial last chunks."""

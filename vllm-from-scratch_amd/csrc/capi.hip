@@ -310,13 +310,18 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
       if (const char* env = getenv("MVSD_VERIFY_LAG")) lag = atoi(env);
       p.lag = lag < 1 ? 1 : (lag > 4096 ? 4096 : lag);
       const int64_t step = p.two_phase ? 2 * plan.nc : plan.nc;
-      tasks = (groups + (p.two_phase ? p.lag * p.nq : 0)) * step;
       // Epilogue split (one queue): the score tasks of the last `lag` groups use the empty
       // stats slots of their steps as a second half-chunk task each (MVSD_VERIFY_SPLIT=0
-      // turns it off).
+      // turns it off).  MVSD_VERIFY_QUARTER=n runs the score tasks of the last n groups in
+      // quarter chunks instead (off by default: no gain measured on MI355X, the end of the
+      // launch is set by the last requests' finalisation rather than by the task length).
       p.split = p.two_phase && p.nq == 1 && 2 * plan.nc <= size_plan.nsub ? 1 : 0;
       if (const char* env = getenv("MVSD_VERIFY_SPLIT")) p.split = p.split && atoi(env) != 0;
-      if (p.split) p.arg_stride = 2 * plan.nc;
+      int quarter = 0;
+      if (const char* env = getenv("MVSD_VERIFY_QUARTER")) quarter = atoi(env);
+      p.quarter = p.split && 4 * plan.nc <= size_plan.nsub ? (quarter < 0 ? 0 : (quarter > p.lag ? p.lag : quarter)) : 0;
+      if (p.split) p.arg_stride = (p.quarter > 0 ? 4 : 2) * plan.nc;
+      tasks = (groups + (p.two_phase ? p.lag * p.nq : 0) + p.quarter) * step;
     }
     // every workgroup may claim up to three tickets past the last task
     if (tasks > 0x7fffffff - 4 * (int64_t)cap) return MVSD_E_RANGE;

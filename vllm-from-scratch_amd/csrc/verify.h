@@ -71,7 +71,10 @@ struct VerifyParams {
   // Epilogue split of the split kernel: the score tasks of the last `lag` groups (whose steps
   // hold no stats tasks) cover half chunks, 2 * nc per row, so the final tasks are short.
   int split;
-  int arg_stride;  // arg slots per row: 2 * nc with the split, else nc
+  // With the split, the score tasks of the last `quarter` groups (<= lag) cover quarter chunks,
+  // 4 * nc per row, so the very last tasks are shorter still.
+  int quarter;
+  int arg_stride;  // arg slots per row: 4 * nc with quarters, 2 * nc with the split, else nc
   // Split kernel without the init kernel: every workgroup builds the requests' group offsets
   // in its own LDS and derives group descriptors from them (one queue, B <= kMaxLdsRequests);
   // grp_off / grp_desc are then unused.

@@ -235,64 +235,146 @@ __device__ inline bool wave_row_stats(const uint64_t* slots, int n, float c1, co
 }
 
 // ------------------------------------------------------------------ finalisation -----
+// The finalisation is latency-bound (a few dependent memory round trips, nothing else in
+// flight for its workgroup), so it overlaps them: each position's decision inputs load while
+// the waves poll the rows' slots, and one poll covers both slot sets of a row.
 struct FinalizeSmem {
   int tok[kMaxSpecLen];
   float M[kMaxSpecLen];
   float S[kMaxSpecLen];
   int out_tok[kMaxSpecLen];
-  int accepted[kMaxSpecLen];
-  int first_reject;
+  int first[2];
 };
 
-// One wave: reduce verify row `row`'s slots (argmax over its na arg slots, softmax statistics
-// over its nc stats slots) and clear them.  tok: the argmax (greedy / in-kernel recovered) or
-// the supplied recovered id; M, S: the statistics (random rows).
+constexpr int kKeep = 2;  // slots per lane kept from the last poll (rows of up to 128 slots)
+
+// One wave: wait until verify row `row`'s slots are written (its na arg slots when the row
+// needs an argmax, its nc stats slots when it is random), then reduce and clear them.  tok:
+// the argmax (greedy rows and in-kernel recovered ids; untouched otherwise); M, S: the
+// statistics (random rows).
 __device__ inline void finalize_row(const VerifyParams& p, int r, int64_t row, bool greedy,
                                     bool full, int na, int& tok, float& M, float& S) {
   const int lane = lane_id();
   const int nc = p.nc;
   uint64_t* aslots = p.arg_slots + row * p.arg_stride;
   uint64_t* sslots = p.stat_slots + row * nc;
-  if (greedy || full) {
-    if (!wave_wait_slots(aslots, na, kSpinLimit, &p.ctrl[1]) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
+  const int nA = (greedy || full) ? na : 0;
+  const int nS = greedy ? 0 : nc;
+  uint64_t av[kKeep], sv[kKeep];
+  for (int spins = 0;; ++spins) {
+    int ready = 1;
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j) {
+      const int c = lane + j * kWave;
+      av[j] = c < nA ? slot_load(aslots + c) : 0;
+      sv[j] = c < nS ? slot_load(sslots + c) : 0;
+      ready &= (c >= nA || av[j] != 0) & (c >= nS || sv[j] != 0);
+    }
+    for (int c = lane + kKeep * kWave; c < nA; c += kWave) ready &= slot_load(aslots + c) != 0;
+    for (int c = lane + kKeep * kWave; c < nS; c += kWave) ready &= slot_load(sslots + c) != 0;
+    if (__all(ready)) break;
+    if (spins >= kSpinLimit || ((spins & 255) == 255 && atomic_load_relaxed(&p.ctrl[1]) != 0)) {
+      if (lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (nA > 0) {
     uint64_t best = 0;
-    for (int c = lane; c < na; c += kWave) {
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j) best = av[j] > best ? av[j] : best;
+    for (int c = lane + kKeep * kWave; c < nA; c += kWave) {
       const uint64_t k = slot_load(aslots + c);
       best = k > best ? k : best;
     }
     best = wave_max_u64(best);
     tok = min(max(key_index(best), 0), p.V - 1);
-    for (int c = lane; c < na; c += kWave) slot_store(aslots + c, 0);
-  } else {
-    tok = p.recovered[row];
+    for (int c = lane; c < nA; c += kWave) slot_store(aslots + c, 0);
   }
   M = 0.f;
   S = 1.f;
-  if (!greedy) {
+  if (nS > 0) {
+    // (raw max MX, S = sum_c s_c * 2^((mx_c - MX) * c1)), as in wave_row_stats
     const float c1 = exp2_scale(req_temperature(p, r));
-    if (!wave_row_stats(sslots, nc, c1, &p.ctrl[1], M, S) && lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
-    for (int c = lane; c < nc; c += kWave) slot_store(sslots + c, 0);
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j)
+      if (lane + j * kWave < nS) m = fmaxf(m, unpack_stats(sv[j]).x);
+    for (int c = lane + kKeep * kWave; c < nS; c += kWave) m = fmaxf(m, unpack_stats(slot_load(sslots + c)).x);
+    M = wave_max(m);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j) {
+      const float2 st = unpack_stats(sv[j]);
+      if (lane + j * kWave < nS && st.x != -INFINITY) sum += st.y * exp2f((st.x - M) * c1);
+    }
+    for (int c = lane + kKeep * kWave; c < nS; c += kWave) {
+      const float2 st = unpack_stats(slot_load(sslots + c));
+      if (st.x != -INFINITY) sum += st.y * exp2f((st.x - M) * c1);
+    }
+    S = wave_sum(sum);
+    for (int c = lane; c < nS; c += kWave) slot_store(sslots + c, 0);
   }
 }
 
-// Arg slots of a verify row: 2 * nc for rows of groups scored in half chunks.
+// Arg slots of a verify row: 2 * nc (4 * nc) for rows of groups scored in half (quarter)
+// chunks.
 __device__ inline int row_arg_slots(const VerifyParams& p, const int* goff, bool full, int gfirst,
                                     int k) {
-  const int split_from = p.split && full ? goff[p.B] - p.lag : 0x7fffffff;
-  return gfirst + k / p.G >= split_from ? 2 * p.nc : p.nc;
+  if (!(p.split && full)) return p.nc;
+  const int li = gfirst + k / p.G;
+  if (li >= goff[p.B] - p.quarter) return 4 * p.nc;
+  return li >= goff[p.B] - p.lag ? 2 * p.nc : p.nc;
 }
 
-// Accept / reject decision at position pos (verify row `row`) of request r, given the row's
-// argmax or recovered id tok and statistics (M, S).
-__device__ inline void decide_position(const VerifyParams& p, int r, bool greedy, int pos,
-                                       int64_t row, int tok, float M, float S, bool& accepted,
-                                       int& token) {
+// Inputs of one position's decision: the draft id and uniform, and for a random row q[d],
+// the target logit x[d], the row mask and the supplied recovered id.
+struct PosInputs {
+  int d;
+  double u;
+  float q;
+  float x;
+  float4 mk;
+  int rec;
+};
+
+__device__ inline PosInputs load_position(const VerifyParams& p, bool greedy, int64_t row) {
+  PosInputs in;
+  in.d = p.draft_ids[row];
+  in.u = 0.0;
+  in.q = 1.f;
+  in.x = 0.f;
+  in.mk = make_float4(-INFINITY, -INFINITY, __int_as_float(-1), 0.f);
+  in.rec = 0;
   const bool synthetic = p.synth != nullptr;
-  const int d = p.draft_ids[row];
+  if (!greedy || synthetic) in.u = p.uniforms[row];
+  if (!greedy && !synthetic && in.d >= 0 && in.d < p.V) {
+    if (p.draft) in.q = p.draft[row * p.draft_stride + in.d];
+    const int64_t trow = target_row(p, (int)row);
+    if (p.target_dtype == MVSD_F32) {
+      in.x = static_cast<const float*>(p.target)[trow * p.target_stride + in.d];
+    } else if (p.target_dtype == MVSD_BF16) {
+      in.x = Elem<MVSD_BF16>::cvt(static_cast<const uint16_t*>(p.target)[trow * p.target_stride + in.d]);
+    } else {
+      in.x = Elem<MVSD_F16>::cvt(static_cast<const _Float16*>(p.target)[trow * p.target_stride + in.d]);
+    }
+    if (p.masks) in.mk = p.masks[row];
+  }
+  if (!greedy && p.recovered) in.rec = p.recovered[row];
+  return in;
+}
+
+// Accept / reject decision at position pos of request r, given the row's argmax or recovered
+// id tok and statistics (M, S).
+__device__ inline void decide_position(const VerifyParams& p, int r, bool greedy, int pos,
+                                       const PosInputs& in, int tok, float M, float S,
+                                       bool& accepted, int& token) {
+  const bool synthetic = p.synth != nullptr;
+  const int d = in.d;
   if (greedy) {
     // rejection_sampler.py:715-732
     if (synthetic) {
-      accepted = p.uniforms[row] < (double)p.synth[pos] && d >= 0;
+      accepted = in.u < (double)p.synth[pos] && d >= 0;
       token = accepted ? d : tok;
     } else {
       token = tok;
@@ -301,28 +383,17 @@ __device__ inline void decide_position(const VerifyParams& p, int r, bool greedy
     return;
   }
   // rejection_sampler.py:782-814
-  const double u = p.uniforms[row];
   if (d < 0) {
     accepted = false;
   } else if (synthetic) {
-    accepted = u < (double)p.synth[pos];
+    accepted = in.u < (double)p.synth[pos];
   } else if (d >= p.V) {
     accepted = false;  // the reference would index out of bounds here
   } else {
-    const float q = p.draft ? p.draft[row * p.draft_stride + d] : 1.f;
-    const int64_t trow = target_row(p, (int)row);
-    float x;
-    if (p.target_dtype == MVSD_F32) {
-      x = static_cast<const float*>(p.target)[trow * p.target_stride + d];
-    } else if (p.target_dtype == MVSD_BF16) {
-      x = Elem<MVSD_BF16>::cvt(static_cast<const uint16_t*>(p.target)[trow * p.target_stride + d]);
-    } else {
-      x = Elem<MVSD_F16>::cvt(static_cast<const _Float16*>(p.target)[trow * p.target_stride + d]);
-    }
     const float temp = req_temperature(p, r);
-    float pd = expf(x / temp - M / temp) / S;
-    if (p.masks && row_masked(p.masks[row], x, d)) pd = 0.f;  // -inf after the constraints
-    accepted = q > 0.f && (double)(pd / q) >= u;
+    float pd = expf(in.x / temp - M / temp) / S;
+    if (p.masks && row_masked(in.mk, in.x, d)) pd = 0.f;  // -inf after the constraints
+    accepted = in.q > 0.f && (double)(pd / in.q) >= in.u;
   }
   token = accepted ? d : tok;
 }
@@ -334,42 +405,40 @@ __device__ void finalize_request(const VerifyParams& p, const int* goff, int r, 
   int begin, K;
   req_range(p, r, begin, K);
   const int gfirst = goff[r];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  // thread pos < K (K <= kMaxSpecLen <= kVThreads) owns position pos; its inputs load while
+  // the waves reduce the rows' slots
+  PosInputs in;
+  if (tid < K) in = load_position(p, greedy, begin + tid);
   for (int k = wave_id(); k < K; k += kVWaves) {
-    int tok;
+    int tok = 0;
     float M, S;
     finalize_row(p, r, begin + k, greedy, full, row_arg_slots(p, goff, full, gfirst, k), tok, M, S);
-    if (lane_id() == 0) {
+    if (lane == 0) {
       sm.tok[k] = tok;
       sm.M[k] = M;
       sm.S[k] = S;
     }
   }
-  if (threadIdx.x == 0) atomic_store_relaxed(&p.req_cnt[r], 0);
+  if (tid == 0) atomic_store_relaxed(&p.req_cnt[r], 0);
   __syncthreads();
 
   // every position's decision in parallel; the chain keeps the prefix up to the first reject
-  const int tid = threadIdx.x;
-  for (int pos = tid; pos < K; pos += kVThreads) {
-    bool accepted;
+  bool accepted = true;
+  if (tid < K) {
     int token;
-    decide_position(p, r, greedy, pos, begin + pos, sm.tok[pos], sm.M[pos], sm.S[pos], accepted,
-                    token);
-    sm.accepted[pos] = accepted;
-    sm.out_tok[pos] = token;
+    const int tok = (greedy || full) ? sm.tok[tid] : in.rec;
+    decide_position(p, r, greedy, tid, in, tok, sm.M[tid], sm.S[tid], accepted, token);
+    sm.out_tok[tid] = token;
+  }
+  static_assert(kMaxSpecLen <= 2 * kWave && kVWaves >= 2, "positions live in waves 0 and 1");
+  if (wave_id() < 2) {
+    const unsigned long long rej = __ballot(tid < K && !accepted);
+    if (lane == 0) sm.first[wave_id()] = rej ? wave_id() * kWave + __builtin_ctzll(rej) : K;
   }
   __syncthreads();
-  if (tid == 0) {
-    int first = K;
-    for (int pos = 0; pos < K; ++pos) {
-      if (!sm.accepted[pos]) {
-        first = pos;
-        break;
-      }
-    }
-    sm.first_reject = first;
-  }
-  __syncthreads();
-  const int first = sm.first_reject;
+  const int first = min(sm.first[0], sm.first[1]);
   int32_t* out = p.out + (int64_t)r * p.out_stride;
   for (int pos = tid; pos <= p.max_spec_len; pos += kVThreads) {
     int v = -1;
@@ -858,7 +927,7 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
 // or the argmax for greedy groups) of group s; when the batch has random requests the next nc
 // are the B-chunks (scores) of group s - lag.  Slots of absent groups are claimed and skipped.
 struct TaskDecode {
-  int total, step_size, nc, lag, groups, two_phase, split;
+  int total, step_size, nc, lag, groups, two_phase, split, quarter;
   const int* qgi;  // queue position -> group index (nullptr: identity)
   const int* goff;  // requests' group offsets in LDS (descriptors derived), or nullptr
   RequestMeta meta;  // request metadata in LDS (with goff)
@@ -884,32 +953,54 @@ __device__ inline int4 group_desc(const int* goff, const RequestMeta& m, int B, 
 }
 
 // Thread 0: decode ticket t and fetch its group descriptor into dst[0..7]
-// = {t, arg slot, valid | phase_b << 1 | half << 2, request, first row,
-// rows | groups << 8 | flags << 16 | index in request << 24, bits of c1, split groups of the
-// request}.  The arg slot is the chunk, or for a half-chunk task (the epilogue split) the half
-// index 2 * chunk + {0, 1}.
+// = {t, arg slot, valid | phase_b << 1 | half << 2 | quarter << 3, request, first row,
+// rows | groups << 8 | flags << 16 | index in request << 24, bits of c1, the request's groups
+// scored in half chunks | in quarter chunks << 16}.  The arg slot is the chunk, or for a
+// half-chunk (quarter-chunk) task of the epilogue split 2 * chunk + half (4 * chunk + quarter).
+//
+// With the split, tickets past the regular steps (groups * step_size of them) hold only score
+// tasks: lag - quarter steps of 2 * nc half-chunk tasks (one group each), then quarter steps
+// of 4 * nc quarter-chunk tasks (one group each).
 __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, int t, int* dst) {
   int c = 0, flags = 0, nsplit = 0;
   int4 d = make_int4(0, 0, 0, 0);
   if (t < td.total) {
-    const int step = t / td.step_size;
-    const int w = t - step * td.step_size;
-    // Steps past the last group hold no stats tasks: with the split, all 2 * nc of their
-    // tickets are half-chunk score tasks of group step - lag.
-    const bool half = td.split && step >= td.groups;
-    const bool phase_b = half || w >= td.nc;
-    c = (phase_b && !half) ? w - td.nc : w;
-    const int li = phase_b ? step - td.lag : step;
+    const int t_reg = td.groups * td.step_size;
+    const int t_half = (td.lag - td.quarter) * td.step_size;
+    int li, kind = 0;  // kind: 0 regular step, 1 half chunk, 2 quarter chunk
+    bool phase_b = true;
+    if (!td.split || t < t_reg) {
+      const int step = t / td.step_size;
+      const int w = t - step * td.step_size;
+      phase_b = w >= td.nc;
+      c = phase_b ? w - td.nc : w;
+      li = phase_b ? step - td.lag : step;
+    } else if (t < t_reg + t_half) {
+      const int u = t - t_reg;
+      const int s = u / td.step_size;
+      c = u - s * td.step_size;
+      li = td.groups + s - td.lag;
+      kind = 1;
+    } else {
+      const int u = t - t_reg - t_half;
+      const int s = u / (2 * td.step_size);
+      c = u - s * 2 * td.step_size;
+      li = td.groups - td.quarter + s;
+      kind = 2;
+    }
     if (li >= 0 && li < td.groups) {
       d = td.goff ? group_desc(td.goff, td.meta, td.B, td.G, li) : p.grp_desc[td.qgi ? td.qgi[li] : li];
       const bool full = (d.z >> 16) & kFull;
-      flags = (!phase_b || full ? 1 : 0) | (phase_b ? 2 : 0) | (half ? 4 : 0);
+      flags = (!phase_b || full ? 1 : 0) | (phase_b ? 2 : 0) | (kind == 1 ? 4 : 0) | (kind == 2 ? 8 : 0);
       if (td.split && full) {
-        // groups of this request at or past groups - lag score in half chunks
+        // the request's groups in [groups - lag, groups - quarter) score in half chunks,
+        // those in [groups - quarter, groups) in quarter chunks
         const int first = li - ((d.z >> 24) & 0xff);
-        const int ngr = (d.z >> 8) & 0xff;
-        const int lo = max(first, td.groups - td.lag);
-        nsplit = min(max(first + ngr - lo, 0), ngr);
+        const int end = first + ((d.z >> 8) & 0xff);
+        const int qlo = td.groups - td.quarter, hlo = td.groups - td.lag;
+        const int nq = max(0, end - max(first, qlo));
+        const int nh = max(0, min(end, qlo) - max(first, hlo));
+        nsplit = nh | nq << 16;
       }
     }
   }
@@ -1006,8 +1097,9 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   td.G = p.G;
   td.two_phase = p.two_phase;
   td.split = p.split;
+  td.quarter = p.split ? p.quarter : 0;
   td.step_size = p.two_phase ? 2 * td.nc : td.nc;
-  td.total = (td.groups + (p.two_phase ? td.lag : 0)) * td.step_size;
+  td.total = (td.groups + (p.two_phase ? td.lag : 0) + td.quarter) * td.step_size;
 
   // Deferred request-completion count (see below).
   int pend_cnt = 0, pend_r = -1, pend_target = 0;
@@ -1053,14 +1145,16 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
     const bool greedy = gflags & kGreedy;
     const bool full = gflags & kFull;
     int64_t v0, vend;
-    if (tflags & 4) {
-      // half chunk: the first or second half of chunk c / 2, split at a sub-chunk boundary
-      const int64_t cs = (int64_t)(c >> 1) * p.chunk;
+    if (tflags & 12) {
+      // part c % n (n = 2 halves or 4 quarters) of chunk c / n, split at sub-chunk boundaries
+      const int n = (tflags & 4) ? 2 : 4;
+      const int part = c & (n - 1);
+      const int64_t cs = (int64_t)(c / n) * p.chunk;
       const int64_t ce = min((int64_t)p.V, cs + p.chunk);
       constexpr int64_t SUB = (int64_t)kVThreads * EPT;
-      const int64_t mid = min(ce, cs + (((ce - cs + SUB - 1) / SUB + 1) / 2) * SUB);
-      v0 = (c & 1) ? mid : cs;
-      vend = (c & 1) ? ce : mid;
+      const int64_t nsc = (ce - cs + SUB - 1) / SUB;
+      v0 = min(ce, cs + (nsc * part + n - 1) / n * SUB);
+      vend = min(ce, cs + (nsc * (part + 1) + n - 1) / n * SUB);
     } else {
       v0 = (int64_t)c * p.chunk;
       vend = min((int64_t)p.V, v0 + p.chunk);
@@ -1080,7 +1174,8 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
     if (full == phase_b) {
       if (tid == 0) pend_cnt = atomic_add_relaxed(&p.req_cnt[r], 1);
       pend_r = r;
-      pend_target = (ngr + nsplit) * td.nc;  // half-chunk groups count 2 * nc tasks
+      // half-chunk groups count 2 * nc tasks, quarter-chunk groups 4 * nc
+      pend_target = (ngr + (nsplit & 0xffff) + 3 * (nsplit >> 16)) * td.nc;
       pend_greedy = greedy;
       pend_full = full;
     }
