@@ -253,13 +253,19 @@ def test_synthetic_mode_parity(device):
     check_parity(w, out, ref, "synthetic")
 
 
+SINGLE_READ_MODES = ["fused", "resident"]
+
+
+@pytest.mark.parametrize("mode", SINGLE_READ_MODES)
 @pytest.mark.parametrize("case", ["c2", "headline", "point_mass", "bf16_ragged", "odd_v",
                                   "c5_rows", "one_request", "one_subchunk", "two_subchunks"])
-def test_fused_kernel_parity(device, monkeypatch, case):
-    """The single-read kernel (MVSD_VERIFY_MODE=fused; the default is the split kernel).  Odd
-    V (unaligned rows) makes the host fall back to the split kernel; one_request has fewer
-    tasks than workgroups, one_subchunk / two_subchunks rows of 1 and 2 sub-chunks."""
-    monkeypatch.setenv("MVSD_VERIFY_MODE", "fused")
+def test_fused_kernel_parity(device, monkeypatch, case, mode):
+    """The single-read kernels (MVSD_VERIFY_MODE=fused: sub-chunks parked in LDS;
+    MVSD_VERIFY_MODE=resident: chunks held in registers).  Odd V (unaligned rows) makes the
+    host fall back to the split kernel; one_request has fewer tasks than workgroups,
+    one_subchunk / two_subchunks rows of 1 and 2 sub-chunks (resident: one chunk of 1000
+    columns, one of 4000)."""
+    monkeypatch.setenv("MVSD_VERIFY_MODE", mode)
     draft_none = case == "point_mass"
     w = {"c2": lambda: configs.random_c2(device),
          "headline": lambda: configs.headline(device),
@@ -271,29 +277,32 @@ def test_fused_kernel_parity(device, monkeypatch, case):
          "one_subchunk": lambda: configs.random_c2(device, B=24, k=5, V=1000, seed=13),
          "two_subchunks": lambda: configs.random_c2(device, B=24, k=5, V=4000, seed=14)}[case]()
     rep = check_parity(w, run_workload(w, draft_none=draft_none),
-                       oracle_for(w, draft_none=draft_none), f"fused {case}")
+                       oracle_for(w, draft_none=draft_none), f"{mode} {case}")
     assert rep.mismatched <= 4
     assert rs.workspace_error_flag(w.target_logits.device) == 0
 
 
+@pytest.mark.parametrize("mode", SINGLE_READ_MODES)
 @pytest.mark.parametrize("case", ["c1", "c1_large", "c4_mixed"])
-def test_fused_kernel_greedy_bit_exact(device, monkeypatch, case):
-    """Greedy rows through the single-read kernel (argmax at stage 1, target_rows gathers)."""
-    monkeypatch.setenv("MVSD_VERIFY_MODE", "fused")
+def test_fused_kernel_greedy_bit_exact(device, monkeypatch, case, mode):
+    """Greedy rows through the single-read kernels (argmax from the first read, target_rows
+    gathers)."""
+    monkeypatch.setenv("MVSD_VERIFY_MODE", mode)
     w = {"c1": lambda: configs.greedy_c1(device),
          "c1_large": lambda: configs.greedy_c1(device, B=64, k=6, seed=77),
          "c4_mixed": lambda: configs.ragged_c4(device, B=96, seed=31)}[case]()
     out = run_workload(w)
     if case == "c4_mixed":
-        check_parity(w, out, oracle_for(w), "fused c4 mixed")
+        check_parity(w, out, oracle_for(w), f"{mode} c4 mixed")
     else:
         assert np.array_equal(out.cpu().numpy(), oracle_for(w).output_token_ids)
     assert rs.workspace_error_flag(w.target_logits.device) == 0
 
 
-def test_fused_kernel_repeated_calls(device, monkeypatch):
+@pytest.mark.parametrize("mode", SINGLE_READ_MODES)
+def test_fused_kernel_repeated_calls(device, monkeypatch, mode):
     """Calls of different shapes in a row leave the workspace zeroed for the next one."""
-    monkeypatch.setenv("MVSD_VERIFY_MODE", "fused")
+    monkeypatch.setenv("MVSD_VERIFY_MODE", mode)
     big = configs.random_c2(device, B=96, k=4, seed=51)
     small = configs.random_c2(device, B=5, k=2, seed=52)
     a = run_workload(big)
@@ -301,8 +310,8 @@ def test_fused_kernel_repeated_calls(device, monkeypatch):
     c = run_workload(big)
     d = run_workload(small)
     assert torch.equal(a, c) and torch.equal(b, d)
-    check_parity(big, a, oracle_for(big), "fused repeated big")
-    check_parity(small, b, oracle_for(small), "fused repeated small")
+    check_parity(big, a, oracle_for(big), f"{mode} repeated big")
+    check_parity(small, b, oracle_for(small), f"{mode} repeated small")
     assert rs.workspace_error_flag(big.target_logits.device) == 0
 
 

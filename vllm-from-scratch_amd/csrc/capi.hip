@@ -46,8 +46,9 @@ constexpr int kMaxDevices = 64;
 // (CUs x occupancy).
 int verify_capacity(int device, int dtype, int mode, bool has_draft, bool masked) {
   static std::mutex mu;
-  static int cache[kMaxDevices][3][2][4];
-  if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2 || mode < 0 || mode > 1)
+  static int cache[kMaxDevices][3][mvsd::kModes][4];
+  if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2 || mode < 0 ||
+      mode >= mvsd::kModes)
     return 0;
   std::lock_guard<std::mutex> lock(mu);
   int& slot = cache[device][dtype][mode][(masked ? 2 : 0) + (has_draft ? 1 : 0)];
@@ -100,7 +101,7 @@ WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
   off = align_up(off + 3 * mvsd::kMaxQueues * 4, 256);
   l.qgi = off;
   off = align_up(off + (P > 0 ? P : 1) * 4, 256);
-  l.masks = off;  // row masks of the sampling constraints (written before use, not cleared)
+  l.masks = off;  // row masks of the sampling constraints (zeroed again by the verify kernel)
   off = align_up(off + (P > 0 ? P : 1) * 16, 256);
   l.stat_slots = off;
   off = align_up(off + P * nc * 8, 256);
@@ -190,6 +191,9 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   // chunk) by default.  MVSD_VERIFY_MODE=fused selects the single-read kernel when its
   // requirements hold: 16-byte loads (below), the request metadata in LDS
   // (B <= kMaxFusedRequests) and at most fused_max_chunks() sub-chunks per row.
+  // MVSD_VERIFY_MODE=resident selects the register-resident kernel when its requirements
+  // hold: 16-byte loads, B <= kMaxLdsRequests, and at least half as many resident workgroups
+  // as chunks per row (its progress argument).
   const int two_phase = (!a->all_greedy && !a->recovered_token_ids) ? 1 : 0;
   // Sampling constraints apply only when some request samples (rejection_sampler.py:549-550).
   const bool masked = !a->all_greedy && (a->top_k || a->top_p);
@@ -216,7 +220,16 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
         cap = fcap;
       }
     }
-    if (kmode != mvsd::kModeFused)
+    if (vec_ok && B <= mvsd::kMaxLdsRequests && mode && strcmp(mode, "resident") == 0) {
+      const int rcap = verify_capacity(device, a->target_dtype, mvsd::kModeResident,
+                                       a->draft_probs != nullptr, masked);
+      const mvsd::VerifyPlan rplan = mvsd::verify_resident_plan(a->target_dtype, V);
+      if (rcap > 0 && rplan.nc <= size_plan.nsub && rplan.nc <= 2 * rcap) {
+        kmode = mvsd::kModeResident;
+        cap = rcap;
+      }
+    }
+    if (kmode == mvsd::kModeSplit)
       cap = verify_capacity(device, a->target_dtype, kmode, a->draft_probs != nullptr, masked);
     if (cap <= 0) return hip_status(hipErrorInvalidDevice);
   }
@@ -226,6 +239,8 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   mvsd::VerifyPlan plan = size_plan;
   if (kmode == mvsd::kModeSplit)
     plan = mvsd::verify_plan(a->target_dtype, V, groups > 0 ? groups : 1, two_phase ? 2 : 1, cap);
+  else if (kmode == mvsd::kModeResident)
+    plan = mvsd::verify_resident_plan(a->target_dtype, V);
 
   char* ws = static_cast<char*>(a->workspace);
   mvsd::VerifyParams p;
@@ -280,7 +295,7 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   // serves the batch and its requests fit (MVSD_VERIFY_LDS_GROUPS=0 keeps the init kernel).
   p.lds_groups = kmode == mvsd::kModeSplit && p.nq == 1 && B <= mvsd::kMaxLdsRequests && P > 0;
   if (const char* env = getenv("MVSD_VERIFY_LDS_GROUPS")) p.lds_groups = p.lds_groups && atoi(env) != 0;
-  if (kmode == mvsd::kModeFused) {
+  if (kmode != mvsd::kModeSplit) {
     p.nq = 1;  // one ticket; the group offsets always in LDS
     p.lds_groups = 1;
   }
@@ -293,7 +308,7 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   int grid = 0;
   if (P > 0) {
     int64_t tasks;
-    if (kmode == mvsd::kModeFused) {
+    if (kmode != mvsd::kModeSplit) {
       tasks = groups * plan.nc;
       grid = (int)(tasks < cap ? tasks : cap);
     } else {

@@ -125,10 +125,18 @@ struct VerifyPlan {
 // sub-chunk parks it in LDS and scores it once the row's statistics are complete).
 constexpr int kModeSplit = 0;
 constexpr int kModeFused = 1;
+// The resident kernel: each task holds its target chunk in registers from the statistics to
+// the scores, so every input byte is read once.
+constexpr int kModeResident = 2;
+constexpr int kModes = 3;
 
 // groups = 0 gives the workspace-sizing plan (nc = nsub).  phases is 2 when the batch needs
 // recovered scores (stats and score tasks per chunk), else 1; cap = resident workgroups.
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int phases, int cap);
+
+// Chunking of the resident kernel: the fewest chunks of at most its per-task column count,
+// balanced and aligned to 64 columns.
+VerifyPlan verify_resident_plan(int target_dtype, int64_t vocab_size);
 
 // masked: the variant that applies the row masks.
 const void* verify_kernel_ptr(int target_dtype, int mode, bool has_draft, bool masked);

@@ -1058,6 +1058,14 @@ __device__ inline void build_lds_tables(const VerifyParams& p, int* goff, const 
   __syncthreads();
 }
 
+// The row masks of the sampling constraints live in the workspace; the last workgroup out
+// (every task and finalisation has read them) returns them to zero, like everything else the
+// call used, so that a later call whose slot arrays overlap them finds zeros.
+__device__ inline void clear_masks(const VerifyParams& p) {
+  if (p.masks)
+    for (int i = threadIdx.x; i < p.P; i += kVThreads) p.masks[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 template <int DT, int EPT, int G, bool HAS_DRAFT, bool MASKED>
 __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(VerifyParams p) {
   static_assert(EPT % Elem<DT>::kVec == 0, "EPT must be a multiple of the vector width");
@@ -1189,6 +1197,7 @@ __global__ __launch_bounds__(kVThreads) MVSD_VERIFY_ATTRS void verify_kernel(Ver
   if (tid == 0) s_last = atomic_add_relaxed(&p.ctrl[2], 1) == (int)gridDim.x - 1;
   __syncthreads();
   if (s_last) {
+    clear_masks(p);
     if (!p.lds_groups) {
       for (int i = tid; i <= p.B; i += kVThreads) p.grp_off[i] = 0;
       for (int i = tid; i < groups; i += kVThreads) {
@@ -1817,6 +1826,505 @@ __global__ __launch_bounds__(kVThreads) MVSD_FUSED_ATTRS void verify_fused_kerne
   // the exit counter to zero.
   if (tid == 0) s_last = atomic_add_relaxed(&p.ctrl[2], 1) == (int)gridDim.x - 1;
   __syncthreads();
+  if (s_last) clear_masks(p);
+  if (s_last && tid == 0) {
+    atomic_store_relaxed(ticket, 0);
+    atomic_store_relaxed(&p.ctrl[2], 0);
+  }
+}
+
+// ------------------------------------------------------------------ resident kernel --
+// Single-read kernel with register-resident tasks.  A task is one (row group, chunk) pair
+// holding both phases: the workgroup loads the group's target chunk into registers, publishes
+// the rows' chunk statistics (greedy groups: the chunk argmax), and, once the group's other
+// chunks have published theirs, scores the chunk from the same registers.  Each thread holds
+// kRVecs 16-byte vectors of each of the G rows, so a chunk is at most kVThreads * kRVecs
+// vectors wide.  A workgroup holds two tasks: the current one, whose statistics are
+// published, and the next one, whose target loads are in flight.  Per iteration:
+//   A. the first poll of the current group's statistics slots, then the draft, noise (and
+//      mask) loads of the current task;
+//   B. the next task's statistics from its target registers, published per row;
+//   C. the end of the wait for the current group's statistics (the poll was issued before
+//      A's side loads, so the in-order load counter does not hold it behind them);
+//   D. the claim of a new ticket, whose round trip overlaps E;
+//   E. the scores of the current task, its argmax published per row, its request counted;
+//   F. the decode of the new ticket, the previous task's completion check, and the new
+//      ticket's target loads into the freed registers.
+//
+// Progress.  A workgroup waits (C) only while both tickets it holds are published, and a
+// workgroup that has claimed a ticket publishes it before its next wait (F, A and B hold no
+// wait).  Take the lowest group g* anybody waits for.  If every ticket of g* is claimed, each
+// is published or about to be, so the waits for g* end.  Otherwise every claimed ticket lies
+// below g*'s unclaimed ones, so a workgroup holds tickets of g* or lower groups only, and those
+// holding a ticket of a lower group are not waiting; they finish and claim on.  Only if every
+// resident workgroup held two tickets of g* and nothing else could the claims stop; the host
+// keeps nc at most twice the resident workgroups, so then all of g* is claimed.  The waits are
+// bounded all the same (kSpinLimit, flag ctrl[1]).
+#ifndef MVSD_RESIDENT_VECS
+#define MVSD_RESIDENT_VECS 2
+#endif
+constexpr int kRVecs = MVSD_RESIDENT_VECS;  // 16-byte target vectors per thread and row
+template <int DT>
+constexpr int rcols() {  // columns per thread and row of a task
+  return kRVecs * Elem<DT>::kVec;
+}
+#ifndef MVSD_RESIDENT_WAVES_PER_EU
+#define MVSD_RESIDENT_WAVES_PER_EU 2
+#endif
+#if MVSD_RESIDENT_WAVES_PER_EU > 0
+#define MVSD_RESIDENT_ATTRS __attribute__((amdgpu_waves_per_eu(MVSD_RESIDENT_WAVES_PER_EU, 8)))
+#else
+#define MVSD_RESIDENT_ATTRS
+#endif
+
+// A decoded ticket, uniform over the workgroup: t < 0 for no task.  Absent tasks load row 0's
+// first columns so that every path issues the same loads.
+struct RTask {
+  int t, c, r, row0, nrows, flags;
+  float c1;
+};
+
+__device__ inline void resident_decode(const int* goff, const RequestMeta& m, int B, int G,
+                                       int nc, int total, int t, int* dst) {
+  int4 d = make_int4(0, 0, 1, 0);
+  int c = 0;
+  if (t >= 0 && t < total) {
+    const int li = t / nc;
+    c = t - li * nc;
+    d = group_desc(goff, m, B, G, li);
+  } else {
+    t = -1;
+  }
+  dst[0] = t;
+  dst[1] = c;
+  dst[2] = d.x;
+  dst[3] = d.y;
+  dst[4] = d.z;
+  dst[5] = d.w;
+}
+
+__device__ inline RTask resident_read(const int* s) {
+  RTask k;
+  k.t = __builtin_amdgcn_readfirstlane(s[0]);
+  k.c = __builtin_amdgcn_readfirstlane(s[1]);
+  k.r = __builtin_amdgcn_readfirstlane(s[2]);
+  k.row0 = __builtin_amdgcn_readfirstlane(s[3]);
+  const int z = __builtin_amdgcn_readfirstlane(s[4]);
+  k.nrows = max(z & 0xff, 1);
+  k.flags = k.t < 0 ? 0 : (z >> 16) & 0xff;
+  k.c1 = __int_as_float(__builtin_amdgcn_readfirstlane(s[5]));
+  return k;
+}
+
+template <int DT, int G>
+struct RBuf {
+  u32x4 x[G][kRVecs];
+};
+
+template <int DT, int G, bool HAS_DRAFT, bool MASKED>
+struct RSide {  // draft, noise and masks of a task
+  u32x4 q[HAS_DRAFT ? G : 1][rcols<DT>() / 4];
+  u32x4 e[rcols<DT>() / 4];
+  float4 mk[MASKED ? G : 1];
+  int d[HAS_DRAFT ? 1 : G];
+};
+
+// Column of the first element of this thread's target vector i in the chunk starting at v0.
+template <int DT>
+__device__ inline int64_t rcol(int64_t v0, int i) {
+  return v0 + ((int64_t)i * kVThreads + threadIdx.x) * Elem<DT>::kVec;
+}
+
+template <int DT, int G>
+__device__ inline void resident_load_x(const VerifyParams& p, const RTask& k, int64_t v0,
+                                       int64_t vend, RBuf<DT, G>& b) {
+  using S = typename Elem<DT>::storage;
+  constexpr int VEC = Elem<DT>::kVec;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const S* base = static_cast<const S*>(p.target) +
+                    target_row(p, k.row0 + min(g, k.nrows - 1)) * p.target_stride;
+#pragma unroll
+    for (int i = 0; i < kRVecs; ++i) {
+      const int64_t col = min(rcol<DT>(v0, i), vend - VEC);
+      b.x[g][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + col));
+    }
+  }
+}
+
+// fp32 vectors laid out like the target's: fp32 vector m holds the 4 columns starting at
+// column 4 (m % (VEC / 4)) of target vector m / (VEC / 4).
+template <int DT>
+__device__ inline void resident_load_f32(const float* base, int64_t v0, int64_t vend,
+                                         u32x4 (&out)[rcols<DT>() / 4]) {
+  constexpr int VEC = Elem<DT>::kVec;
+#pragma unroll
+  for (int m = 0; m < rcols<DT>() / 4; ++m) {
+    const int64_t col = min(rcol<DT>(v0, m / (VEC / 4)), vend - VEC) + (m % (VEC / 4)) * 4;
+    out[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + col));
+  }
+}
+
+template <int DT, int G, bool HAS_DRAFT, bool MASKED>
+__device__ inline void resident_load_side(const VerifyParams& p, const RTask& k, int64_t v0,
+                                          int64_t vend, RSide<DT, G, HAS_DRAFT, MASKED>& s) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int row = k.row0 + min(g, k.nrows - 1);
+    if constexpr (MASKED) s.mk[g] = p.masks[row];
+    if constexpr (HAS_DRAFT) resident_load_f32<DT>(p.draft + (int64_t)row * p.draft_stride, v0, vend, s.q[g]);
+    else s.d[g] = p.draft_ids[row];
+  }
+  resident_load_f32<DT>(p.noise + (int64_t)k.r * p.noise_stride, v0, vend, s.e);
+}
+
+// Row masks alone (the first read of a masked batch's tasks).
+template <bool MASKED, int G>
+__device__ inline void resident_masks(const VerifyParams& p, const RTask& k, float4 (&mk)[G]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    mk[g] = MASKED ? p.masks[k.row0 + min(g, k.nrows - 1)] : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// Element j (0 <= j < rcols) of row g: value and column.
+template <int DT, int G>
+__device__ inline float rx(const RBuf<DT, G>& b, int g, int j) {
+  return raw_elem<DT>(b.x[g], j);
+}
+template <int DT>
+__device__ inline int ridx(int64_t v0, int j) {
+  constexpr int VEC = Elem<DT>::kVec;
+  return (int)(rcol<DT>(v0, j / VEC) + j % VEC);
+}
+
+// Row statistics (max, sum of 2^((x - max) * c1)) of N rows over a block of NW waves,
+// combined for row thread g (< N), which receives them; other threads get (-inf, 0).  Each
+// wave rescales its lanes' sums to the wave maximum, so one barrier suffices.
+template <int N, int NW>
+__device__ inline float2 block_stats_to_row_thread(const float (&m)[N], const float (&s)[N],
+                                                   float c1, float2* scratch) {
+#pragma unroll
+  for (int g = 0; g < N; ++g) {
+    const float wm = wave_max(m[g]);
+    const float sc = m[g] == -INFINITY ? 0.f : s[g] * __builtin_amdgcn_exp2f((m[g] - wm) * c1);
+    const float ws = wave_sum(sc);
+    if (lane_id() == 0) scratch[g * NW + wave_id()] = make_float2(wm, ws);
+  }
+  __syncthreads();
+  float2 r = make_float2(-INFINITY, 0.f);
+  const int t = threadIdx.x;
+  if (t < N) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, scratch[t * NW + w].x);
+    float S = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float2 q = scratch[t * NW + w];
+      if (q.x != -INFINITY) S += q.y * exp2f((q.x - M) * c1);
+    }
+    r = make_float2(M, S);
+  }
+  return r;
+}
+
+// Chunk statistics of each row, published into the rows' stats slots.
+template <int DT, int G, bool MASKED>
+__device__ inline void resident_stats(const VerifyParams& p, const RTask& k, int64_t v0,
+                                      int64_t vend, const RBuf<DT, G>& b, const float4 (&mk)[G],
+                                      float2* s_pair) {
+  constexpr int VEC = Elem<DT>::kVec;
+  float m[G], s[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float lm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < rcols<DT>(); ++j) {
+      const bool valid = rcol<DT>(v0, j / VEC) < vend;
+      lm = valid ? fmaxf(lm, rx<DT, G>(b, g, j)) : lm;
+    }
+    const float ref = lm == -INFINITY ? 0.f : lm;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < rcols<DT>(); ++j) {
+      const float x = rx<DT, G>(b, g, j);
+      bool keep = rcol<DT>(v0, j / VEC) < vend;
+      if constexpr (MASKED) keep = keep & !row_masked(mk[g], x, ridx<DT>(v0, j));
+      const float e = __builtin_amdgcn_exp2f((x - ref) * k.c1);
+      acc += keep ? e : 0.f;
+    }
+    m[g] = lm;
+    s[g] = acc;
+  }
+  const float2 st = block_stats_to_row_thread<G, kVWaves>(m, s, k.c1, s_pair);
+  if ((int)threadIdx.x < k.nrows)
+    slot_store(p.stat_slots + (int64_t)(k.row0 + threadIdx.x) * p.nc + k.c,
+               pack_stats(st.x, st.x == -INFINITY ? 0.f : st.y));
+}
+
+// Chunk argmax of each row (NaN first, lowest index), published into the rows' arg slots.
+template <int DT, int G, bool MASKED>
+__device__ inline void resident_argmax(const VerifyParams& p, const RTask& k, int64_t v0,
+                                       int64_t vend, const RBuf<DT, G>& b, const float4 (&mk)[G],
+                                       uint64_t* s_key) {
+  constexpr int VEC = Elem<DT>::kVec;
+  uint64_t key[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float bv = -INFINITY;
+    int bi = (int)v0;
+#pragma unroll
+    for (int j = 0; j < rcols<DT>(); ++j) {
+      const int idx = ridx<DT>(v0, j);
+      float v = rx<DT, G>(b, g, j);
+      if constexpr (MASKED) v = row_masked(mk[g], v, idx) ? -INFINITY : v;
+      // columns rise with j: a strict compare keeps the first maximum; NaN wins
+      const bool take = ((v > bv) | ((v != v) & (bv == bv))) & (rcol<DT>(v0, j / VEC) < vend);
+      bv = take ? v : bv;
+      bi = take ? idx : bi;
+    }
+    key[g] = argmax_key(bv, bi);
+  }
+  const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
+  if ((int)threadIdx.x < k.nrows)
+    slot_store(p.arg_slots + (int64_t)(k.row0 + threadIdx.x) * p.arg_stride + k.c, best);
+}
+
+// Scores max(p - q, 0) * (1 / E) of the chunk from the registers (MX, NL: the rows' raw max
+// and -log2 of the softmax sum); the chunk argmax of each row goes into its arg slot.
+template <int DT, int G, bool HAS_DRAFT, bool MASKED>
+__device__ inline void resident_scores(const VerifyParams& p, const RTask& k, int64_t v0,
+                                       int64_t vend, const RBuf<DT, G>& b,
+                                       const RSide<DT, G, HAS_DRAFT, MASKED>& sd,
+                                       const float (&MX)[G], const float (&NL)[G],
+                                       uint64_t* s_key) {
+  constexpr int VEC = Elem<DT>::kVec;
+  float inv[rcols<DT>()];
+#pragma unroll
+  for (int j = 0; j < rcols<DT>(); ++j) inv[j] = recip_rn(raw_f32(sd.e, j));
+  uint64_t key[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    // scores are >= 0 after the clamp and ties keep the lowest index, so starting from
+    // (0, v0) and taking only strictly larger scores folds the clamp into the argmax
+    float bv = 0.f;
+    int bi = (int)v0;
+    if (g < k.nrows) {
+#pragma unroll
+      for (int j = 0; j < rcols<DT>(); ++j) {
+        const int idx = ridx<DT>(v0, j);
+        const float x = rx<DT, G>(b, g, j);
+        float prob = __builtin_amdgcn_exp2f(fmaf(x - MX[g], k.c1, NL[g]));  // softmax
+        if constexpr (MASKED) prob = row_masked(sd.mk[g], x, idx) ? 0.f : prob;
+        float w;
+        if constexpr (HAS_DRAFT) w = prob - raw_f32(sd.q[g], j);
+        else w = idx == sd.d[g] ? 0.f : prob;
+        const float score = w * inv[j];
+        const bool take = (score > bv) & (rcol<DT>(v0, j / VEC) < vend);
+        bv = take ? score : bv;
+        bi = take ? idx : bi;
+      }
+    }
+    key[g] = argmax_key(bv, bi);
+  }
+  const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
+  if ((int)threadIdx.x < k.nrows)
+    slot_store(p.arg_slots + (int64_t)(k.row0 + threadIdx.x) * p.arg_stride + k.c, best);
+}
+
+// The first poll of one row's nc stats slots (one wave; kPollKeep slots per lane kept).
+// Every lane loads kPollKeep slots (clamped), so every path issues the same loads.
+constexpr int kPollKeep = 2;
+__device__ inline void poll_issue(const uint64_t* slots, int n, uint64_t (&v)[kPollKeep]) {
+#pragma unroll
+  for (int j = 0; j < kPollKeep; ++j) v[j] = slot_load(slots + min(lane_id() + j * kWave, n - 1));
+}
+
+// The rest of the wait for the row's slots (polls again until all are written), then their
+// combination into the row's raw max MX and S = sum_c s_c * 2^((mx_c - MX) * c1), as
+// wave_row_stats.  Returns false when the bounded wait ran out.
+__device__ inline bool poll_finish(const uint64_t* slots, int n, float c1, const int* abort,
+                                   uint64_t (&v)[kPollKeep], float& MX, float& S) {
+  const int lane = lane_id();
+  bool ok = true;
+  for (int spins = 0;; ++spins) {
+    int ready = 1;
+#pragma unroll
+    for (int j = 0; j < kPollKeep; ++j) ready &= (lane + j * kWave >= n) | (v[j] != 0);
+    for (int c = lane + kPollKeep * kWave; c < n; c += kWave) ready &= slot_load(slots + c) != 0;
+    if (__all(ready)) break;
+    if (spins >= kSpinLimit || ((spins & 255) == 255 && atomic_load_relaxed(abort) != 0)) {
+      ok = false;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    poll_issue(slots, n, v);
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kPollKeep; ++j)
+    if (lane + j * kWave < n) m = fmaxf(m, unpack_stats(v[j]).x);
+  for (int c = lane + kPollKeep * kWave; c < n; c += kWave) m = fmaxf(m, unpack_stats(slot_load(slots + c)).x);
+  MX = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kPollKeep; ++j) {
+    const float2 st = unpack_stats(v[j]);
+    if (lane + j * kWave < n && st.x != -INFINITY) s += st.y * exp2f((st.x - MX) * c1);
+  }
+  for (int c = lane + kPollKeep * kWave; c < n; c += kWave) {
+    const float2 st = unpack_stats(slot_load(slots + c));
+    if (st.x != -INFINITY) s += st.y * exp2f((st.x - MX) * c1);
+  }
+  S = wave_sum(s);
+  return ok;
+}
+
+template <int DT, int G, bool HAS_DRAFT, bool MASKED>
+__global__ __launch_bounds__(kVThreads) MVSD_RESIDENT_ATTRS void verify_resident_kernel(VerifyParams p) {
+  __shared__ float2 s_pair[G * kVWaves];
+  __shared__ uint64_t s_key[G * kVWaves];
+  __shared__ float s_MX[G];  // the group's statistics (raw max, -log2 sum) from the wait
+  __shared__ float s_L[G];
+  __shared__ int s_info[3][8];
+  __shared__ int s_last;
+  __shared__ FinalizeSmem fsm;
+  __shared__ int s_goff[kMaxLdsRequests + 1];
+  __shared__ int s_rbegin[kMaxLdsRequests], s_rkf[kMaxLdsRequests];
+  __shared__ float s_rc1[kMaxLdsRequests];
+
+  const int tid = threadIdx.x;
+  int* ticket = &p.qticket[0];
+  int t0 = 0, t1 = 0;
+  if (tid == 0) {
+    t0 = atomic_add_relaxed(ticket, 1);
+    t1 = atomic_add_relaxed(ticket, 1);
+  }
+  const RequestMeta meta{s_rbegin, s_rkf, s_rc1};
+  build_lds_tables(p, s_goff, meta);
+  const int nc = p.nc;
+  const int total = s_goff[p.B] * nc;
+  if (tid == 0) {
+    resident_decode(s_goff, meta, p.B, p.G, nc, total, t0, s_info[0]);
+    resident_decode(s_goff, meta, p.B, p.G, nc, total, t1, s_info[1]);
+  }
+  __syncthreads();
+  auto span = [&](const RTask& k, int64_t& v0, int64_t& vend) {
+    v0 = (int64_t)k.c * p.chunk;
+    vend = min((int64_t)p.V, v0 + p.chunk);
+  };
+
+  // Request completion: a task's count is examined one iteration later (F), so the counter's
+  // round trip is never waited for on the task path; the last task of a request finalises it.
+  int pend_cnt = 0, pend_r = -1, pend_target = 0;
+  bool pend_greedy = false, pend_full = false;
+
+  RTask cur = resident_read(s_info[0]);
+  RTask nxt = resident_read(s_info[1]);
+  int slot = 2;  // s_info slot of the next decode
+  RBuf<DT, G> xa, xb;
+  // The first-read step of a task: its statistics (greedy: its argmax), published per row.
+  auto first_read = [&](const RTask& k, const RBuf<DT, G>& b) {
+    if (k.t < 0) return;
+    int64_t v0, vend;
+    span(k, v0, vend);
+    float4 mk[G];
+    resident_masks<MASKED, G>(p, k, mk);
+    if (k.flags & kGreedy) resident_argmax<DT, G, MASKED>(p, k, v0, vend, b, mk, s_key);
+    else resident_stats<DT, G, MASKED>(p, k, v0, vend, b, mk, s_pair);
+  };
+  {
+    int64_t v0, vend;
+    span(cur, v0, vend);
+    resident_load_x<DT, G>(p, cur, v0, vend, xa);
+    first_read(cur, xa);
+    span(nxt, v0, vend);
+    resident_load_x<DT, G>(p, nxt, v0, vend, xb);
+    __syncthreads();  // the row threads have read s_pair / s_key
+  }
+
+  // X holds the current task (statistics published), Y the next task's target (loads in
+  // flight).
+  auto iteration = [&](RBuf<DT, G>& X, RBuf<DT, G>& Y) -> bool {
+    if (cur.t < 0) return false;
+    const bool full = cur.flags & kFull;
+    const bool poller = full && wave_id() < cur.nrows;
+    const uint64_t* row_slots = p.stat_slots + (int64_t)(cur.row0 + min(wave_id(), cur.nrows - 1)) * nc;
+    int64_t v0, vend;
+    span(cur, v0, vend);
+    // A: the first poll of the group's statistics, then the side loads of the current task
+    uint64_t pv[kPollKeep];
+    if (poller) poll_issue(row_slots, nc, pv);
+    RSide<DT, G, HAS_DRAFT, MASKED> sd;
+    if (full) resident_load_side<DT, G, HAS_DRAFT, MASKED>(p, cur, v0, vend, sd);
+    // B: the next task's statistics (its target loads were issued one iteration ago)
+    first_read(nxt, Y);
+    // C: the rest of the wait for the current group's statistics
+    float MX[G], NL[G];
+    if (full) {
+      if (poller) {
+        float mx, sum;
+        if (!poll_finish(row_slots, nc, cur.c1, &p.ctrl[1], pv, mx, sum) && lane_id() == 0)
+          atomic_store_relaxed(&p.ctrl[1], 1);
+        if (lane_id() == 0) {
+          s_MX[wave_id()] = mx;
+          s_L[wave_id()] = (float)(-log2((double)sum));
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        MX[g] = s_MX[g];
+        NL[g] = s_L[g];
+      }
+    }
+    // D: claim a new ticket; its round trip overlaps the scores
+    int tk = 0;
+    if (tid == 0) tk = atomic_add_relaxed(ticket, 1);
+    // E: scores of the current task, and its count
+    if (full) resident_scores<DT, G, HAS_DRAFT, MASKED>(p, cur, v0, vend, X, sd, MX, NL, s_key);
+    int cnt = 0;
+    if (tid == 0) cnt = atomic_add_relaxed(&p.req_cnt[cur.r], 1);
+    // F: decode the new ticket and check the previous task's count (the flag rides in the
+    // decode slot, which no wave rewrites before every wave has read it)
+    if (tid == 0) {
+      resident_decode(s_goff, meta, p.B, p.G, nc, total, tk, s_info[slot]);
+      s_info[slot][6] = pend_r >= 0 && pend_cnt == pend_target - 1 ? 1 : 0;
+    }
+    __syncthreads();
+    if (__builtin_amdgcn_readfirstlane(s_info[slot][6])) {
+      finalize_request(p, s_goff, pend_r, pend_greedy, pend_full, fsm);
+      __syncthreads();
+    }
+    pend_cnt = cnt;
+    pend_r = cur.r;
+    pend_target = (s_goff[cur.r + 1] - s_goff[cur.r]) * nc;  // every task of the request
+    pend_greedy = cur.flags & kGreedy;
+    pend_full = full;
+    cur = nxt;
+    nxt = resident_read(s_info[slot]);
+    slot = slot == 2 ? 0 : slot + 1;
+    int64_t n0, nend;
+    span(nxt, n0, nend);
+    resident_load_x<DT, G>(p, nxt, n0, nend, X);
+    return true;
+  };
+  for (;;) {
+    if (!iteration(xa, xb)) break;
+    if (!iteration(xb, xa)) break;
+  }
+  if (pend_r >= 0) {
+    if (tid == 0) s_last = pend_cnt == pend_target - 1;
+    __syncthreads();
+    if (s_last) finalize_request(p, s_goff, pend_r, pend_greedy, pend_full, fsm);
+  }
+
+  // The last workgroup out (every other one has made its final claim) returns the ticket and
+  // the exit counter to zero.
+  __syncthreads();
+  if (tid == 0) s_last = atomic_add_relaxed(&p.ctrl[2], 1) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (s_last) clear_masks(p);
   if (s_last && tid == 0) {
     atomic_store_relaxed(ticket, 0);
     atomic_store_relaxed(&p.ctrl[2], 0);
@@ -1875,6 +2383,19 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int
   return plan;
 }
 
+VerifyPlan verify_resident_plan(int target_dtype, int64_t vocab_size) {
+  VerifyPlan plan;
+  plan.ept = kRVecs * (target_dtype == MVSD_F32 ? 4 : 8);
+  plan.g = kGroup;
+  plan.sub = kVThreads * plan.ept;
+  const int64_t nc = (vocab_size + plan.sub - 1) / plan.sub;
+  const int64_t per = (vocab_size + nc - 1) / nc;
+  plan.chunk = (int)((per + 63) / 64 * 64);
+  plan.nc = (int)((vocab_size + plan.chunk - 1) / plan.chunk);
+  plan.nsub = plan.nc;
+  return plan;
+}
+
 template <int DT>
 const void* kernel_for(int mode, bool has_draft, bool masked) {
   constexpr int E = ept_of<DT>();
@@ -1884,6 +2405,13 @@ const void* kernel_for(int mode, bool has_draft, bool masked) {
                        : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false, true>);
     return has_draft ? reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, true, false>)
                      : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false, false>);
+  }
+  if (mode == kModeResident) {
+    if (masked)
+      return has_draft ? reinterpret_cast<const void*>(&verify_resident_kernel<DT, kGroup, true, true>)
+                       : reinterpret_cast<const void*>(&verify_resident_kernel<DT, kGroup, false, true>);
+    return has_draft ? reinterpret_cast<const void*>(&verify_resident_kernel<DT, kGroup, true, false>)
+                     : reinterpret_cast<const void*>(&verify_resident_kernel<DT, kGroup, false, false>);
   }
   if (masked)
     return has_draft ? reinterpret_cast<const void*>(&verify_fused_kernel<DT, E, kGroup, true, true>)
