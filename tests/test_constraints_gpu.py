@@ -82,7 +82,7 @@ def test_c4_masks_match_processed_path_and_oracle(device, B):
                           "c4 in-kernel masks")
 
 
-@pytest.mark.parametrize("mode", ["split", "fused", "resident"])
+@pytest.mark.parametrize("mode", ["split", "fused", "resident", "lds"])
 def test_c4_in_kernel_constraints_then_verify(device, monkeypatch, mode):
     """rejection_sample on the raw bf16 rows with the divide and the constraints in the
     kernels, against the oracle sampler on the same rows masked by the processed path (split
@@ -218,7 +218,7 @@ def test_division_selftest(device):
     assert int(failures.item()) == 0
 
 
-@pytest.mark.parametrize("mode", ["split", "fused", "resident"])
+@pytest.mark.parametrize("mode", ["split", "fused", "resident", "lds"])
 def test_masked_call_leaves_workspace_zero(device, monkeypatch, mode):
     """A masked call writes row masks into the workspace; the verify kernel zeroes them again
     on exit, so the whole workspace (bar the sticky flag) is zero after the call, and a later,

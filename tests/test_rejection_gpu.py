@@ -253,7 +253,7 @@ def test_synthetic_mode_parity(device):
     check_parity(w, out, ref, "synthetic")
 
 
-SINGLE_READ_MODES = ["fused", "resident"]
+SINGLE_READ_MODES = ["fused", "resident", "lds"]
 
 
 @pytest.mark.parametrize("mode", SINGLE_READ_MODES)

@@ -193,7 +193,8 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   // (B <= kMaxFusedRequests) and at most fused_max_chunks() sub-chunks per row.
   // MVSD_VERIFY_MODE=resident selects the register-resident kernel when its requirements
   // hold: 16-byte loads, B <= kMaxLdsRequests, and at least half as many resident workgroups
-  // as chunks per row (its progress argument).
+  // as chunks per row (its progress argument).  MVSD_VERIFY_MODE=lds selects the parked
+  // kernel when B <= lds_max_requests() and more workgroups are resident than chunks per row.
   const int two_phase = (!a->all_greedy && !a->recovered_token_ids) ? 1 : 0;
   // Sampling constraints apply only when some request samples (rejection_sampler.py:549-550).
   const bool masked = !a->all_greedy && (a->top_k || a->top_p);
@@ -229,6 +230,15 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
         cap = rcap;
       }
     }
+    if (B <= mvsd::lds_max_requests() && mode && strcmp(mode, "lds") == 0) {
+      const int lcap = verify_capacity(device, a->target_dtype, mvsd::kModeLds,
+                                       a->draft_probs != nullptr, masked);
+      const mvsd::VerifyPlan lplan = mvsd::verify_lds_plan(a->target_dtype, V);
+      if (lcap > 0 && lplan.nc <= size_plan.nsub && lplan.nc < lcap) {
+        kmode = mvsd::kModeLds;
+        cap = lcap;
+      }
+    }
     if (kmode == mvsd::kModeSplit)
       cap = verify_capacity(device, a->target_dtype, kmode, a->draft_probs != nullptr, masked);
     if (cap <= 0) return hip_status(hipErrorInvalidDevice);
@@ -241,6 +251,8 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
     plan = mvsd::verify_plan(a->target_dtype, V, groups > 0 ? groups : 1, two_phase ? 2 : 1, cap);
   else if (kmode == mvsd::kModeResident)
     plan = mvsd::verify_resident_plan(a->target_dtype, V);
+  else if (kmode == mvsd::kModeLds)
+    plan = mvsd::verify_lds_plan(a->target_dtype, V);
 
   char* ws = static_cast<char*>(a->workspace);
   mvsd::VerifyParams p;

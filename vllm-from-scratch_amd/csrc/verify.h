@@ -128,7 +128,10 @@ constexpr int kModeFused = 1;
 // The resident kernel: each task holds its target chunk in registers from the statistics to
 // the scores, so every input byte is read once.
 constexpr int kModeResident = 2;
-constexpr int kModes = 3;
+// The parked kernel: long tasks whose target chunk is parked in LDS between the statistics and
+// the scores, so every input byte is read once.
+constexpr int kModeLds = 3;
+constexpr int kModes = 4;
 
 // groups = 0 gives the workspace-sizing plan (nc = nsub).  phases is 2 when the batch needs
 // recovered scores (stats and score tasks per chunk), else 1; cap = resident workgroups.
@@ -137,6 +140,10 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int
 // Chunking of the resident kernel: the fewest chunks of at most its per-task column count,
 // balanced and aligned to 64 columns.
 VerifyPlan verify_resident_plan(int target_dtype, int64_t vocab_size);
+// Chunking of the parked kernel (chunks of its parked sub-chunk count) and the most requests
+// whose metadata fit its LDS.
+VerifyPlan verify_lds_plan(int target_dtype, int64_t vocab_size);
+int lds_max_requests();
 
 // masked: the variant that applies the row masks.
 const void* verify_kernel_ptr(int target_dtype, int mode, bool has_draft, bool masked);

@@ -724,10 +724,12 @@ __device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int n
 // entries masked by the row's sampling constraints add nothing to the sum; the maximum still
 // runs over every entry, which only moves the reference point of the exponentials (the
 // largest value of a row is never masked).
-template <int DT, int EPT, int G, bool MASKED, typename Hook>
+// With PARK, every thread also stores its raw target vectors of sub-chunk j (counted from v0)
+// at park[((j * G + g) * NV + i) * kVThreads + thread] in LDS, for the scores of the same task.
+template <int DT, int EPT, int G, bool MASKED, bool PARK = false, typename Hook>
 __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int row0, int nrows,
                                   int64_t v0, int64_t vend, float* s_red, float* s_M,
-                                  Hook&& after_loads) {
+                                  Hook&& after_loads, u32x4* park = nullptr) {
   using S = typename Elem<DT>::storage;
   const S* tb[G];
   target_bases<DT, G>(p, row0, nrows, tb);
@@ -740,6 +742,14 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
     s[g] = 0.f;
   }
   auto body = [&](const TargetBuf<DT, EPT, G>& buf, int64_t s0, auto) {
+    if constexpr (PARK) {
+      constexpr int NV = EPT / Elem<DT>::kVec;
+      const int j = (int)((s0 - v0) / (kVThreads * EPT));
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < NV; ++i) park[((j * G + g) * NV + i) * kVThreads + threadIdx.x] = buf.x[g][i];
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       if (g < nrows) {
@@ -793,10 +803,14 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
 // B-task: per row of the group, the chunk-local argmax of max(p - q, 0) * (1 / E).  The
 // group's stats were published by A-tasks holding lower tickets; the wait for them overlaps
 // with the first sub-chunk's loads.
-template <int DT, int EPT, int G, bool HAS_DRAFT, bool MASKED, typename Hook>
+// With PARKED the target comes from the LDS copy task_stats<..., PARK> made of the same
+// chunk (each thread reads back its own vectors), and after_loads runs once the wait for the
+// group's statistics is over instead of before it.
+template <int DT, int EPT, int G, bool HAS_DRAFT, bool MASKED, bool PARKED = false, typename Hook>
 __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1, int row0,
                                    int nrows, int64_t v0, int64_t vend, uint64_t* s_key,
-                                   float* s_M, float* s_L, Hook&& after_loads) {
+                                   float* s_M, float* s_L, Hook&& after_loads,
+                                   const u32x4* park = nullptr) {
   using S = typename Elem<DT>::storage;
   using Buf = ScoreBuf<DT, EPT, G>;
   const S* tb[G];
@@ -819,7 +833,9 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
     constexpr bool F = decltype(fast)::value;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      if constexpr (F)
+      if constexpr (PARKED)
+        ;
+      else if constexpr (F)
         load_raw<DT, EPT, MVSD_VERIFY_NT_SCORES>(tb[g], s0, buf.x[g]);
       else
         load_raw_checked<DT, EPT, MVSD_VERIFY_NT_SCORES>(tb[g], s0, vend, p.target_aligned,
@@ -832,7 +848,7 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
 
   float MX[G], NL[G];
   auto wait_stats = [&]() {
-    after_loads();
+    if constexpr (!PARKED) after_loads();
     if (wave_id() < nrows) {
       float mx, sum;
       if (!wave_row_stats(p.stat_slots + (int64_t)(row0 + wave_id()) * p.nc, p.nc, c1, &p.ctrl[1], mx, sum) &&
@@ -849,6 +865,7 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
       MX[g] = s_M[g];
       NL[g] = s_L[g];
     }
+    if constexpr (PARKED) after_loads();
   };
 
   // Scores are max(p - q, 0) / E >= 0 and ties keep the lowest index, so starting from
@@ -861,6 +878,15 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
     bi[g] = (int)v0;
   }
   auto body = [&](const Buf& buf, int64_t s0, auto fast) {
+    constexpr int NV = EPT / Elem<DT>::kVec;
+    u32x4 xp[PARKED ? G : 1][NV];
+    if constexpr (PARKED) {
+      const int j = (int)((s0 - v0) / (kVThreads * EPT));
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < NV; ++i) xp[g][i] = park[((j * G + g) * NV + i) * kVThreads + threadIdx.x];
+    }
     float inv[EPT];
 #pragma unroll
     for (int k = 0; k < EPT; ++k) inv[k] = recip_rn(raw_f32(buf.e, k));
@@ -870,7 +896,10 @@ __device__ inline void task_scores(const VerifyParams& p, int c, int r, float c1
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
           const int idx = elem_index<DT, EPT>(s0, k);
-          const float x = raw_elem<DT>(buf.x[g], k);
+          const u32x4* xg;
+          if constexpr (PARKED) xg = xp[g];
+          else xg = buf.x[g];
+          const float x = raw_elem<DT>(xg, k);
           float prob = __builtin_amdgcn_exp2f(fmaf(x - MX[g], c1, NL[g]));  // softmax
           if constexpr (MASKED) prob = row_masked(mk[g], x, idx) ? 0.f : prob;
           float w;
@@ -2331,6 +2360,117 @@ __global__ __launch_bounds__(kVThreads) MVSD_RESIDENT_ATTRS void verify_resident
   }
 }
 
+// ------------------------------------------------------------------ parked kernel ----
+// Single-read kernel with long streaming tasks (MVSD_VERIFY_MODE=lds).  A task is one (row
+// group, chunk of kLdsSubs sub-chunks) pair holding both phases:
+//   1. the group's target chunk streams through the split kernel's two-deep sub-chunk
+//      pipeline into per-row statistics, and every thread parks its raw target vectors in
+//      LDS; the statistics are published;
+//   2. the chunk's draft and noise stream through the same pipeline; behind the first
+//      sub-chunk's loads the workgroup waits for the group's statistics, then scores the
+//      parked target against them.
+// Each thread reads back only the vectors it parked, so the parking needs no barrier.
+// Greedy tasks and tasks of requests with supplied recovered ids have phase 1 only.
+//
+// Progress.  The next ticket is claimed once the task's wait is over (tasks without a wait
+// claim it behind their first loads) and decoded at the end of the task, so a workgroup never
+// waits while it holds an unpublished ticket.  Take the lowest group g* anybody waits for:
+// every workgroup holding an unpublished ticket of g* is in its phase 1, which has no wait,
+// and publishes; if some ticket of g* is unclaimed, the workgroups not waiting for g* (those
+// in other groups' tasks below g*, or between tasks) go on claiming, and a workgroup waiting
+// for g* holds one ticket, so the claims of g* stop only if fewer workgroups are resident than
+// g* has chunks (nc); the host keeps nc below the resident workgroups.  The waits are bounded
+// all the same (kSpinLimit, flag ctrl[1]).
+#ifndef MVSD_LDS_SUBS
+#define MVSD_LDS_SUBS 4
+#endif
+constexpr int kLdsSubs = MVSD_LDS_SUBS;  // sub-chunks per task, all parked in LDS
+constexpr int kLdsRequests = 1024;       // requests whose metadata fit beside the parked target
+
+template <int DT, int EPT, int G, bool HAS_DRAFT, bool MASKED>
+__global__ __launch_bounds__(kVThreads) void verify_lds_kernel(VerifyParams p) {
+  constexpr int NV = EPT / Elem<DT>::kVec;
+  __shared__ float s_red[G * kVWaves];
+  __shared__ uint64_t s_key[G * kVWaves];
+  __shared__ float s_M[G];
+  __shared__ float s_L[G];
+  __shared__ int s_info[2][8];
+  __shared__ int s_last;
+  __shared__ FinalizeSmem fsm;
+  __shared__ int s_goff[kLdsRequests + 1];
+  __shared__ int s_rbegin[kLdsRequests], s_rkf[kLdsRequests];
+  __shared__ float s_rc1[kLdsRequests];
+  __shared__ u32x4 s_park[kLdsSubs * G * NV * kVThreads];
+
+  const int tid = threadIdx.x;
+  int* ticket = &p.qticket[0];
+  // the first ticket is claimed before the tables are built, so its round trip overlaps them
+  int tfirst = 0;
+  if (tid == 0) tfirst = atomic_add_relaxed(ticket, 1);
+  const RequestMeta meta{s_rbegin, s_rkf, s_rc1};
+  build_lds_tables(p, s_goff, meta);
+  const int nc = p.nc;
+  const int total = s_goff[p.B] * nc;
+  if (tid == 0) resident_decode(s_goff, meta, p.B, p.G, nc, total, tfirst, s_info[0]);
+  __syncthreads();
+
+  // Deferred request-completion count: the counter's result is examined after the next task,
+  // so its round trip is never waited for on the task path.
+  int pend_cnt = 0, pend_r = -1, pend_target = 0;
+  bool pend_greedy = false, pend_full = false;
+  auto settle = [&]() {
+    if (pend_r >= 0) {
+      if (tid == 0) s_last = pend_cnt == pend_target - 1;
+      __syncthreads();
+      if (s_last) finalize_request(p, s_goff, pend_r, pend_greedy, pend_full, fsm);
+      __syncthreads();
+      pend_r = -1;
+    }
+  };
+
+  for (int par = 0;; par ^= 1) {
+    const RTask k = resident_read(s_info[par]);
+    if (k.t < 0) break;
+    int tn = 0;
+    auto claim = [&]() {
+      if (tid == 0) tn = atomic_add_relaxed(ticket, 1);
+    };
+    const bool greedy = k.flags & kGreedy;
+    const bool full = k.flags & kFull;
+    const int64_t v0 = (int64_t)k.c * p.chunk;
+    const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
+    if (greedy) {
+      task_argmax<DT, EPT, G, MASKED>(p, k.c, k.row0, k.nrows, v0, vend, s_key, claim);
+    } else if (!full) {
+      task_stats<DT, EPT, G, MASKED>(p, k.c, k.c1, k.row0, k.nrows, v0, vend, s_red, s_M, claim);
+    } else {
+      task_stats<DT, EPT, G, MASKED, true>(p, k.c, k.c1, k.row0, k.nrows, v0, vend, s_red, s_M,
+                                           [] {}, s_park);
+      task_scores<DT, EPT, G, HAS_DRAFT, MASKED, true>(p, k.c, k.r, k.c1, k.row0, k.nrows, v0,
+                                                       vend, s_key, s_M, s_L, claim, s_park);
+    }
+    settle();
+    if (tid == 0) pend_cnt = atomic_add_relaxed(&p.req_cnt[k.r], 1);
+    pend_r = k.r;
+    pend_target = (s_goff[k.r + 1] - s_goff[k.r]) * nc;  // every task of the request
+    pend_greedy = greedy;
+    pend_full = full;
+    if (tid == 0) resident_decode(s_goff, meta, p.B, p.G, nc, total, tn, s_info[par ^ 1]);
+    __syncthreads();
+  }
+  settle();
+
+  // The last workgroup out (every other one has made its final claim) returns the ticket and
+  // the exit counter to zero.
+  if (tid == 0) s_last = atomic_add_relaxed(&p.ctrl[2], 1) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (s_last) clear_masks(p);
+  if (s_last && tid == 0) {
+    atomic_store_relaxed(ticket, 0);
+    atomic_store_relaxed(&p.ctrl[2], 0);
+  }
+}
+
 // ------------------------------------------------------------------ workspace init ---
 __global__ __launch_bounds__(256) void zero_fill_kernel(uint64_t* p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
@@ -2383,6 +2523,19 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t groups, int
   return plan;
 }
 
+VerifyPlan verify_lds_plan(int target_dtype, int64_t vocab_size) {
+  VerifyPlan plan;
+  plan.ept = target_dtype == MVSD_F32 ? ept_of<MVSD_F32>() : ept_of<MVSD_BF16>();
+  plan.g = kGroup;
+  plan.sub = kVThreads * plan.ept;
+  plan.chunk = kLdsSubs * plan.sub;
+  plan.nc = (int)((vocab_size + plan.chunk - 1) / plan.chunk);
+  plan.nsub = plan.nc;
+  return plan;
+}
+
+int lds_max_requests() { return kLdsRequests; }
+
 VerifyPlan verify_resident_plan(int target_dtype, int64_t vocab_size) {
   VerifyPlan plan;
   plan.ept = kRVecs * (target_dtype == MVSD_F32 ? 4 : 8);
@@ -2405,6 +2558,13 @@ const void* kernel_for(int mode, bool has_draft, bool masked) {
                        : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false, true>);
     return has_draft ? reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, true, false>)
                      : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false, false>);
+  }
+  if (mode == kModeLds) {
+    if (masked)
+      return has_draft ? reinterpret_cast<const void*>(&verify_lds_kernel<DT, E, kGroup, true, true>)
+                       : reinterpret_cast<const void*>(&verify_lds_kernel<DT, E, kGroup, false, true>);
+    return has_draft ? reinterpret_cast<const void*>(&verify_lds_kernel<DT, E, kGroup, true, false>)
+                     : reinterpret_cast<const void*>(&verify_lds_kernel<DT, E, kGroup, false, false>);
   }
   if (mode == kModeResident) {
     if (masked)
