@@ -1048,8 +1048,32 @@ __device__ inline void fetch_task(const VerifyParams& p, const TaskDecode& td, i
 // consecutive requests once (the group counts wait in goff for the scan).  Requests without
 // drafts get their output row here (bonus, then -1), from workgroup r mod grid; every other
 // row is written by its finalisation.
+// Exclusive scan of one value per thread over the kVThreads-thread block: shuffle scans within
+// the waves, then one barrier for the wave totals.  Returns this thread's exclusive prefix;
+// total receives the block's sum.
+__device__ inline int block_exclusive_scan(int v, int& total) {
+  __shared__ int s_wave[kVWaves];
+  const int lane = lane_id(), w = wave_id();
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int y = __shfl_up(x, d, kWave);
+    x += lane >= d ? y : 0;
+  }
+  if (lane == kWave - 1) s_wave[w] = x;
+  __syncthreads();
+  int before = 0, sum = 0;
+#pragma unroll
+  for (int i = 0; i < kVWaves; ++i) {
+    const int t = s_wave[i];
+    before += i < w ? t : 0;
+    sum += t;
+  }
+  total = sum;
+  return before + x - v;
+}
+
 __device__ inline void build_lds_tables(const VerifyParams& p, int* goff, const RequestMeta& m) {
-  __shared__ int s_scan[kVThreads];
   const int tid = threadIdx.x;
   const int per = (p.B + kVThreads - 1) / kVThreads;
   const int r0 = tid * per, r1 = min(p.B, r0 + per);
@@ -1065,15 +1089,8 @@ __device__ inline void build_lds_tables(const VerifyParams& p, int* goff, const 
     m.kflags[r] = k | ((greedy ? kGreedy : 0) | (!greedy && !p.recovered ? kFull : 0)) << 16;
     m.c1[r] = exp2_scale(req_temperature(p, r));
   }
-  s_scan[tid] = run;
-  __syncthreads();
-  for (int off = 1; off < kVThreads; off <<= 1) {
-    const int add = tid >= off ? s_scan[tid - off] : 0;
-    __syncthreads();
-    s_scan[tid] += add;
-    __syncthreads();
-  }
-  int acc = s_scan[tid] - run;
+  int total;
+  int acc = block_exclusive_scan(run, total);
   for (int r = r0; r < r1; ++r) {
     const int ng = goff[r];
     goff[r] = acc;
@@ -1083,7 +1100,7 @@ __device__ inline void build_lds_tables(const VerifyParams& p, int* goff, const 
       for (int c = 0; c <= p.max_spec_len; ++c) out[c] = c == 0 ? p.bonus[r] : -1;
     }
   }
-  if (tid == kVThreads - 1) goff[p.B] = s_scan[kVThreads - 1];
+  if (tid == 0) goff[p.B] = total;
   __syncthreads();
 }
 
