@@ -230,6 +230,33 @@ int mvsd_ngram_propose(int32_t* drafts, int32_t* num_valid, int32_t* token_ids,
                        int64_t max_model_len, mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
+/* apply_logits_processors — penalties and min_tokens of the verify rows, in place.        */
+/* Replaces: RejectionSampler.apply_logits_processors / apply_penalties /                  */
+/*           _combine_outputs_with_spec_tokens, minivllm/sample/rejection_sampler.py:338-406, */
+/*           with apply_all_penalties, minivllm/sample/ops/penalties.py:51-72, and          */
+/*           Sampler.apply_min_tokens_for_spec_decode, minivllm/sample/sampler.py:192-228.   */
+/* logits: fp32 verify rows (num_tokens of them, request-major) at logits + j * stride.    */
+/* Row j of request r (rows cu[r-1] .. cu[r]-1, cu without a leading 0) has the history    */
+/* "committed output + spec_tokens of its request before row j".  Penalties (ent_off NULL:  */
+/* none): ent_tok[ent_off[r] .. ent_off[r+1]) lists request r's distinct prompt, output and */
+/* draft tokens, ent_info the committed output count | in_prompt << 31; for each listed    */
+/* token t with count c (committed + earlier drafts equal to t):                           */
+/*   if in_prompt or c > 0: x *= x > 0 ? 1 / repetition[r] : repetition[r];               */
+/*   x -= frequency[r] * c;  x -= presence[r] * (c > 0)   (fp32, in this order).           */
+/* presence / frequency / repetition [B] fp32, NULL = 0 / 0 / 1.  Then min_tokens (n_mask   */
+/* NULL: none): the first n_mask[r] rows of request r get stop_tok[stop_off[r] ..          */
+/* stop_off[r+1]) set to -inf.  Tokens outside [0, vocab_size) are skipped.                */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_apply_logits_processors(float* logits, int64_t stride, int64_t num_tokens,
+                                 int64_t vocab_size, int64_t batch_size,
+                                 const int32_t* cu_num_draft_tokens, const int32_t* spec_tokens,
+                                 const int32_t* ent_off, const int32_t* ent_tok,
+                                 const int32_t* ent_info, const float* presence,
+                                 const float* frequency, const float* repetition,
+                                 const int32_t* n_mask, const int32_t* stop_off,
+                                 const int32_t* stop_tok, mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
 /* selftest — on-device check of an arithmetic assumption of the kernels.  No counterpart   */
 /* in the reference.  test 0: the FMA-corrected hardware reciprocal used for 1/E equals     */
 /* IEEE fp32 division for every b in [2^-126, 2^126).  test 1: the corrected division x/T  */

@@ -12,6 +12,7 @@
 #include "rows.h"
 #include "selftest.h"
 #include "verify.h"
+#include "processors.h"
 
 namespace {
 
@@ -354,6 +355,41 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
     if (tasks > 0x7fffffff - 4 * (int64_t)cap) return MVSD_E_RANGE;
   }
   return hip_status(mvsd::launch_verify(p, a->target_dtype, kmode, grid, (hipStream_t)stream));
+}
+
+int mvsd_apply_logits_processors(float* logits, int64_t stride, int64_t num_tokens,
+                                 int64_t vocab_size, int64_t batch_size,
+                                 const int32_t* cu_num_draft_tokens, const int32_t* spec_tokens,
+                                 const int32_t* ent_off, const int32_t* ent_tok,
+                                 const int32_t* ent_info, const float* presence,
+                                 const float* frequency, const float* repetition,
+                                 const int32_t* n_mask, const int32_t* stop_off,
+                                 const int32_t* stop_tok, mvsd_stream_t stream) {
+  if (num_tokens < 0 || batch_size < 0 || vocab_size <= 0) return MVSD_E_INVALID;
+  if (num_tokens == 0 || batch_size == 0 || (!ent_off && !n_mask)) return MVSD_OK;
+  if (num_tokens > 0x7fffffff || batch_size > 0x7fffffff || vocab_size > 0x7fffffff)
+    return MVSD_E_RANGE;
+  if (!logits || stride < vocab_size || !cu_num_draft_tokens) return MVSD_E_INVALID;
+  if (ent_off && (!ent_tok || !ent_info || !spec_tokens)) return MVSD_E_INVALID;
+  if (n_mask && (!stop_off || !stop_tok)) return MVSD_E_INVALID;
+  mvsd::ProcessorParams p;
+  p.logits = logits;
+  p.stride = stride;
+  p.P = (int)num_tokens;
+  p.V = (int)vocab_size;
+  p.B = (int)batch_size;
+  p.cu = cu_num_draft_tokens;
+  p.spec = spec_tokens;
+  p.ent_off = ent_off;
+  p.ent_tok = ent_tok;
+  p.ent_info = ent_info;
+  p.presence = presence;
+  p.frequency = frequency;
+  p.repetition = repetition;
+  p.n_mask = n_mask;
+  p.stop_off = stop_off;
+  p.stop_tok = stop_tok;
+  return hip_status(mvsd::launch_logits_processors(p, (hipStream_t)stream));
 }
 
 int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream) {

@@ -89,6 +89,10 @@ SIGNATURES = {
     "mvsd_sample_recovered_tokens": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
                                              c_void_p, c_int64, c_void_p, c_int64, c_int64,
                                              c_int64, c_int64, c_int64, c_void_p]),
+    "mvsd_apply_logits_processors": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                             c_void_p, c_void_p]),
     "mvsd_ngram_propose": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
                                    c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int,
                                    c_int64, c_int32, c_int32, c_int32, c_int, c_int64,

@@ -36,6 +36,7 @@ from __future__ import annotations
 from dataclasses import replace
 from typing import TYPE_CHECKING
 
+import numpy as np
 import torch
 
 from .. import _native as nat
@@ -139,11 +140,73 @@ class RejectionSampler:
 
     def apply_logits_processors(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata,
                                 metadata: "SpecDecodeMetadata") -> torch.Tensor:
-        """Penalties and min_tokens over the hypothetical draft-prefix history (:338-356)."""
-        if not sampling_metadata.no_penalties or _has_active_min_tokens(sampling_metadata):
-            raise NotImplementedError(
-                "penalties and min_tokens on verify rows are not provided by this build")
+        """Penalties, then min_tokens, on the fp32 verify rows in place (:338-356).
+
+        Verify row j of request i sees the hypothetical history "committed output + drafts
+        [:j]" (:387-406); rows whose history is still shorter than min_tokens get their stop
+        tokens masked (the caller's ``Sampler.apply_min_tokens_for_spec_decode``,
+        sampler.py:192-228, done here in the same launch).  One ``mvsd_apply_logits_processors``
+        launch; the histories are summarised on the host per request (distinct tokens,
+        committed counts, prompt flags) and the kernel adds the draft-prefix counts per row.
+        """
+        num_draft = [int(k) for k in metadata.num_draft_tokens]
+        has_penalties = not sampling_metadata.no_penalties
+        masks = _min_tokens_rows(sampling_metadata, num_draft)
+        if not has_penalties and masks is None:
+            return logits
+        specs = sampling_metadata.spec_token_ids
+        if not specs:
+            specs = [[] for _ in num_draft]
+        entries = None
+        if has_penalties:
+            entries = _penalty_entries(sampling_metadata.prompt_token_ids,
+                                       sampling_metadata.output_token_ids, specs)
+        _launch_logits_processors(
+            logits, metadata.cu_num_draft_tokens, num_draft,
+            [list(spec)[:k] + [-1] * (k - len(spec)) for spec, k in zip(specs, num_draft)],
+            entries, sampling_metadata if has_penalties else None, masks)
         return logits
+
+    @staticmethod
+    def apply_penalties(logits: torch.Tensor, sampling_metadata: SamplingMetadata,
+                        metadata: "SpecDecodeMetadata",
+                        output_token_ids: list[list[int]]) -> torch.Tensor:
+        """Penalties of the verify rows with explicit per-row histories (:358-385):
+        ``output_token_ids[j]`` is row j's output history, and the prompt is that of row j's
+        request.  In place; returns ``logits``."""
+        if sampling_metadata.no_penalties:
+            return logits
+        num_rows = logits.shape[0]
+        num_draft = [int(k) for k in metadata.num_draft_tokens]
+        prompts = [prompt for prompt, count in zip(sampling_metadata.prompt_token_ids, num_draft)
+                   for _ in range(count)]
+        cu = metadata.cu_num_draft_tokens
+        per_row = replace(
+            sampling_metadata,
+            presence_penalties=_expand_opt(sampling_metadata.presence_penalties, cu, num_rows),
+            frequency_penalties=_expand_opt(sampling_metadata.frequency_penalties, cu, num_rows),
+            repetition_penalties=_expand_opt(sampling_metadata.repetition_penalties, cu,
+                                             num_rows))
+        # every row is a request of its own: one row, no drafts
+        rows_cu = torch.arange(1, num_rows + 1, dtype=torch.int32, device=logits.device)
+        entries = _penalty_entries(prompts, output_token_ids, [[] for _ in range(num_rows)])
+        _launch_logits_processors(logits, rows_cu, [1] * num_rows, [[-1]] * num_rows, entries,
+                                  per_row, None)
+        return logits
+
+    @staticmethod
+    def _combine_outputs_with_spec_tokens(
+            output_token_ids: list[list[int]],
+            spec_token_ids: list[list[int]] | None = None) -> list[list[int]]:
+        """Per-row histories "committed + drafts[:j]", one per draft position; requests
+        without drafts give no rows (:387-406)."""
+        if spec_token_ids is None:
+            return output_token_ids
+        result = []
+        for out, spec in zip(output_token_ids, spec_token_ids):
+            for j in range(len(spec)):
+                result.append([*out, *spec[:j]])
+        return result
 
     @staticmethod
     def parse_output(output_token_ids: torch.Tensor, vocab_size: int, discard_req_indices=(),
@@ -156,6 +219,103 @@ class RejectionSampler:
         if len(discard_req_indices) > 0:
             valid[list(discard_req_indices)] = False
         return [row[valid[i]].tolist() for i, row in enumerate(out)], None
+
+
+def _penalty_entries(prompts, outputs, specs):
+    """Per request: the distinct tokens of prompt, committed output and drafts, each with
+    its committed output count and prompt flag, as (ent_off [B+1], ent_tok, ent_info) int32
+    arrays with ent_info = count | in_prompt << 31."""
+    offs = [0]
+    toks: list[np.ndarray] = []
+    infos: list[np.ndarray] = []
+    for i, spec in enumerate(specs):
+        prompt = np.asarray(prompts[i] if i < len(prompts) else [], dtype=np.int64)
+        out = np.asarray(outputs[i] if i < len(outputs) else [], dtype=np.int64)
+        union = np.unique(np.concatenate([prompt, out, np.asarray(spec, dtype=np.int64)]))
+        out_vals, out_counts = np.unique(out, return_counts=True)
+        counts = np.zeros(union.shape[0], dtype=np.int64)
+        counts[np.searchsorted(union, out_vals)] = out_counts
+        in_prompt = np.isin(union, prompt)
+        toks.append(union)
+        infos.append(counts | (in_prompt.astype(np.int64) << 31))
+        offs.append(offs[-1] + union.shape[0])
+    tok = np.concatenate(toks) if toks else np.zeros(0, np.int64)
+    info = np.concatenate(infos) if infos else np.zeros(0, np.int64)
+    return (np.asarray(offs, dtype=np.int32), tok.astype(np.int32),
+            info.astype(np.uint32).view(np.int32))
+
+
+def _min_tokens_rows(sm: SamplingMetadata, num_draft: list[int]):
+    """(n_mask [B], stop_off [B+1], stop_tok) for min_tokens (sampler.py:204-228), or None
+    when no row is masked: the first clamp(min_tokens - len(output), 0, K_i) rows of request i
+    mask its stop tokens."""
+    if not sm.min_tokens:
+        return None
+    n_mask = np.zeros(len(num_draft), dtype=np.int32)
+    stop_off = [0]
+    stop_tok: list[int] = []
+    for i, k in enumerate(num_draft):
+        stop_ids = list(sm.stop_token_ids[i]) if i < len(sm.stop_token_ids) else []
+        min_tokens = sm.min_tokens[i] if i < len(sm.min_tokens) else 0
+        if stop_ids:
+            produced = len(sm.output_token_ids[i]) if i < len(sm.output_token_ids) else 0
+            n_mask[i] = min(max(min_tokens - produced, 0), k)
+            stop_tok.extend(stop_ids)
+        stop_off.append(len(stop_tok))
+    if not n_mask.any():
+        return None
+    return n_mask, np.asarray(stop_off, dtype=np.int32), np.asarray(stop_tok, dtype=np.int32)
+
+
+def _expand_opt(values: torch.Tensor | None, cu: torch.Tensor, num_rows: int):
+    return None if values is None else expand_batch_to_tokens(values, cu, num_rows)
+
+
+def _launch_logits_processors(logits, cu, num_draft, specs, entries, penalties, masks):
+    """One mvsd_apply_logits_processors launch on fp32 rows ``logits`` (request-major)."""
+    assert logits.ndim == 2 and logits.dtype == torch.float32, "fp32 [P, V] logits expected"
+    nat.require_device_tensor(logits, "logits")
+    if logits.stride(1) != 1:
+        raise ValueError("logits processors need rows with unit stride")
+    num_rows, V = logits.shape
+    if sum(num_draft) != num_rows:
+        raise ValueError(f"{num_rows} verify rows but {sum(num_draft)} draft tokens")
+    device = logits.device
+    keep = []
+
+    def dev(array, dtype=torch.int32):
+        t = torch.as_tensor(np.ascontiguousarray(array)).to(device=device, dtype=dtype)
+        keep.append(t)
+        return t.data_ptr()
+
+    def dev_opt(values):
+        if values is None:
+            return None
+        t = values.to(device=device, dtype=torch.float32).contiguous()
+        keep.append(t)
+        return t.data_ptr()
+
+    if entries is not None and entries[1].size == 0:
+        entries = None  # no history token anywhere: the penalties are no-ops
+    if entries is None and masks is None:
+        return
+    cu_t = _as(cu, torch.int32, device)
+    spec = np.asarray([t for row in specs for t in row], dtype=np.int32)
+    ent_off = ent_tok = ent_info = None
+    presence = frequency = repetition = None
+    if entries is not None:
+        ent_off, ent_tok, ent_info = (dev(a) for a in entries)
+        presence = dev_opt(penalties.presence_penalties)
+        frequency = dev_opt(penalties.frequency_penalties)
+        repetition = dev_opt(penalties.repetition_penalties)
+    n_mask = stop_off = stop_tok = None
+    if masks is not None:
+        n_mask, stop_off, stop_tok = (dev(a) for a in masks)
+    nat.check(nat.lib().mvsd_apply_logits_processors(
+        logits.data_ptr(), logits.stride(0), num_rows, V, len(num_draft), cu_t.data_ptr(),
+        dev(spec) if spec.size else None, ent_off, ent_tok, ent_info, presence, frequency,
+        repetition, n_mask, stop_off, stop_tok, nat.stream_of(device)),
+        "mvsd_apply_logits_processors")
 
 
 def _has_active_min_tokens(sm: SamplingMetadata) -> bool:
