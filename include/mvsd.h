@@ -257,6 +257,29 @@ int mvsd_apply_logits_processors(float* logits, int64_t stride, int64_t num_toke
                                  const int32_t* stop_tok, mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
+/* spec_logprobs — logprobs of every output position of a verification step.              */
+/* Replaces: RejectionSampler._get_logprobs_tensors, minivllm/sample/rejection_sampler.py: */
+/*           229-300, with Sampler.compute_logprobs / gather_logprobs /                    */
+/*           batched_count_greater_than, minivllm/sample/sampler.py:313-349.               */
+/* Position (r, j), j < width, reads compact row start_r + j (clamped to num_tokens +      */
+/* batch_size - 1), where the compact rows are each request's verify rows then its bonus   */
+/* row and start_r = cu_num_sampled_tokens[r-1] (0 for r = 0; no leading 0 in the array).  */
+/* Verify row v is target + t * target_stride with t = target_rows[v] (or v if NULL); the   */
+/* bonus row of request q is bonus + q * bonus_stride; both fp32.  Token =                 */
+/* sampled_token_ids[r * sampled_stride + j], -1 read as 0.  With lp(x) the fp32            */
+/* log-softmax (x - max) - log(sum exp(x - max)) of the row (logits_mode != 0: lp(x) = x): */
+/*   ids[n, 0] = token, lps[n, 0] = lp(x_token); ids / lps[n, 1 .. k] = the k largest lp    */
+/*   by (value desc, index asc); ranks[n] = #{i : lp(x_i) >= lp(x_token)};                  */
+/* n = r * width + j; ids / lps are [batch_size * width, k + 1].  0 <= k <= 32, k <= V.     */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_spec_logprobs(int32_t* ids, float* lps, int32_t* ranks, const float* target,
+                       int64_t target_stride, const int32_t* target_rows, const float* bonus,
+                       int64_t bonus_stride, const int32_t* cu_num_sampled_tokens,
+                       const int32_t* sampled_token_ids, int64_t sampled_stride,
+                       int64_t batch_size, int64_t num_tokens, int64_t vocab_size,
+                       int64_t width, int64_t k, int logits_mode, mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
 /* selftest — on-device check of an arithmetic assumption of the kernels.  No counterpart   */
 /* in the reference.  test 0: the FMA-corrected hardware reciprocal used for 1/E equals     */
 /* IEEE fp32 division for every b in [2^-126, 2^126).  test 1: the corrected division x/T  */

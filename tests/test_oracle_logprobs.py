@@ -1,0 +1,67 @@
+"""The speculative-logprobs oracle (oracle/logprobs.py) against the reference's known answers
+for the row indexing, and against closed forms of log-softmax, top-k and rank."""
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from mvsd.testing.spec_metadata import make_metadata
+from oracle import logprobs as olp
+
+ROOT = Path(__file__).resolve().parents[1]
+KATS = json.loads((ROOT / "tests" / "golden" / "reference_kats.json").read_text())
+
+
+def hand_log_softmax(row):
+    """float64 log-softmax written out (the reference tests' hand_log_softmax)."""
+    top = max(row)
+    total = sum(math.exp(v - top) for v in row if v != -math.inf)
+    return [v - top - math.log(total) for v in row]
+
+
+def kat_rows(case):
+    if "log_of_rows" in case:
+        return torch.tensor(case["log_of_rows"], dtype=torch.float32).log()
+    return torch.tensor(case["rows"], dtype=torch.float32)
+
+
+def oracle_for(case):
+    meta = make_metadata(case["drafts"])
+    logits = kat_rows(case)
+    return olp.get_logprobs_tensors(
+        case["k"], meta.cu_num_sampled_tokens, meta.target_logits_indices,
+        meta.bonus_logits_indices, logits[meta.target_logits_indices],
+        logits[meta.bonus_logits_indices], torch.tensor(case["sampled"], dtype=torch.int32))
+
+
+@pytest.mark.parametrize("case", [c for c in KATS["spec_logprobs"] if "expect_logprob_of" in c],
+                         ids=lambda c: c["name"])
+def test_oracle_row_indexing_kats(case):
+    ids, lps, _ = oracle_for(case)
+    logits = kat_rows(case)
+    if "expect_token_column" in case:
+        assert ids[:, 0].tolist() == case["expect_token_column"]
+    for e in case["expect_logprob_of"]:
+        want = hand_log_softmax(logits[e["row"]].tolist())[e["token"]]
+        assert abs(lps[e["slot"], 0].item() - want) <= case["tolerance"]
+
+
+def test_closed_forms():
+    rows = torch.tensor([[1.0, 3.0, 3.0, -2.0, 0.5]], dtype=torch.float32)
+    lp = olp.compute_logprobs(rows)
+    assert abs(float(lp.exp().sum()) - 1.0) < 1e-6
+    ids, lps, ranks = olp.gather_logprobs(lp, 3, torch.tensor([2]))
+    # sampled token first; top-3 by value then index: the tie 3.0 / 3.0 keeps index order
+    assert ids.tolist() == [[2, 1, 2, 0]]
+    assert ranks.tolist() == [2]                      # ties count as >=: rank 2 for token 2
+    _, _, ranks = olp.gather_logprobs(lp, 0, torch.tensor([3]))
+    assert ranks.tolist() == [5]                      # the smallest entry is last
+    want = hand_log_softmax(rows[0].tolist())
+    assert np.allclose(lps[0].numpy(), [want[2], want[1], want[2], want[0]], atol=1e-6)
+    # logits mode reports the values themselves
+    ids, lps, ranks = olp.gather_logprobs(rows, 2, torch.tensor([0]))
+    assert lps.tolist() == [[1.0, 3.0, 3.0]] and ranks.tolist() == [3]

@@ -12,6 +12,7 @@
 #include "rows.h"
 #include "selftest.h"
 #include "verify.h"
+#include "logprobs.h"
 #include "processors.h"
 
 namespace {
@@ -390,6 +391,43 @@ int mvsd_apply_logits_processors(float* logits, int64_t stride, int64_t num_toke
   p.stop_off = stop_off;
   p.stop_tok = stop_tok;
   return hip_status(mvsd::launch_logits_processors(p, (hipStream_t)stream));
+}
+
+int mvsd_spec_logprobs(int32_t* ids, float* lps, int32_t* ranks, const float* target,
+                       int64_t target_stride, const int32_t* target_rows, const float* bonus,
+                       int64_t bonus_stride, const int32_t* cu_num_sampled_tokens,
+                       const int32_t* sampled_token_ids, int64_t sampled_stride,
+                       int64_t batch_size, int64_t num_tokens, int64_t vocab_size,
+                       int64_t width, int64_t k, int logits_mode, mvsd_stream_t stream) {
+  if (batch_size < 0 || num_tokens < 0 || vocab_size <= 0 || width < 0 || k < 0)
+    return MVSD_E_INVALID;
+  if (batch_size == 0 || width == 0) return MVSD_OK;
+  if (k > mvsd::logprobs_max_k() || k > vocab_size) return MVSD_E_RANGE;
+  if (batch_size * width > 0x7fffffff || num_tokens > 0x7fffffff || vocab_size > 0x7fffffff)
+    return MVSD_E_RANGE;
+  if (!ids || !lps || !ranks || !bonus || !cu_num_sampled_tokens || !sampled_token_ids)
+    return MVSD_E_INVALID;
+  if (num_tokens > 0 && (!target || target_stride < vocab_size)) return MVSD_E_INVALID;
+  if (bonus_stride < vocab_size || sampled_stride < width) return MVSD_E_INVALID;
+  mvsd::LogprobParams p;
+  p.target = target;
+  p.tstride = target_stride;
+  p.target_rows = target_rows;
+  p.bonus = bonus;
+  p.bstride = bonus_stride;
+  p.cu_sampled = cu_num_sampled_tokens;
+  p.tokens = sampled_token_ids;
+  p.tok_stride = sampled_stride;
+  p.B = (int)batch_size;
+  p.P = (int)num_tokens;
+  p.V = (int)vocab_size;
+  p.W = (int)width;
+  p.k = (int)k;
+  p.logits_mode = logits_mode ? 1 : 0;
+  p.ids = ids;
+  p.lps = lps;
+  p.ranks = ranks;
+  return hip_status(mvsd::launch_spec_logprobs(p, (hipStream_t)stream));
 }
 
 int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream) {

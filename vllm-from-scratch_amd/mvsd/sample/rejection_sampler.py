@@ -95,8 +95,13 @@ class RejectionSampler:
                 f"sampling metadata has {len(sampling_metadata.prompt_token_ids)} rows but the "
                 f"spec metadata has {len(metadata.num_draft_tokens)} requests: they must match "
                 "request for request, in the same order")
-        if sampling_metadata.max_num_logprobs is not None:
-            raise NotImplementedError("speculative logprobs are not provided by this build")
+        max_num_logprobs = sampling_metadata.max_num_logprobs
+        if max_num_logprobs == -1:
+            # the reference refuses full-vocabulary logprobs on the speculative path too
+            # (:257-267): its top-k cannot take -1
+            raise NotImplementedError(
+                "speculative decoding with logprobs=-1 (the whole vocabulary) is not supported; "
+                "request logprobs=k with k >= 1")
 
         # 1) bonus tokens from the bonus rows with the regular sampler (:169-181)
         bonus_logits = logits[metadata.bonus_logits_indices]
@@ -114,7 +119,10 @@ class RejectionSampler:
                             # a replaced recovered-token seam receives materialised
                             # probabilities, which must carry the constraints
                             or (constrained
-                                and sample_recovered_tokens is not _SAMPLE_RECOVERED_TOKENS))
+                                and sample_recovered_tokens is not _SAMPLE_RECOVERED_TOKENS)
+                            # processed logprobs report the processed rows
+                            or (max_num_logprobs is not None
+                                and self.is_processed_logprobs_mode))
         if not needs_processing:
             # 2+3 fused: gather, fp32 upcast, temperature divide and top-k / top-p happen in
             # the kernels (the constraints become per-row thresholds on the raw rows)
@@ -125,6 +133,7 @@ class RejectionSampler:
                 synthetic_conditional_rates=self.synthetic_conditional_rates,
                 target_rows=metadata.target_logits_indices, apply_temperature=True,
                 apply_top_k_top_p=constrained)
+            target_logits = None
         else:
             target_logits = logits[metadata.target_logits_indices].to(torch.float32)
             target_logits = self.apply_logits_processors(target_logits, sampling_metadata,
@@ -136,7 +145,74 @@ class RejectionSampler:
                 metadata.cu_num_draft_tokens, draft_probs, target_logits, bonus_token_ids,
                 sampling_metadata, synthetic_mode=self.synthetic_mode,
                 synthetic_conditional_rates=self.synthetic_conditional_rates)
-        return SamplerOutput(sampled_token_ids=output_token_ids, logprobs_tensors=None)
+
+        # 4) logprobs of every output position (:212-223); raw modes read the raw verify rows
+        logprobs_tensors = None
+        if max_num_logprobs is not None:
+            bonus_rows = bonus_out.logprobs_tensors.logprobs
+            if self.is_processed_logprobs_mode:
+                logprobs_tensors = self._get_logprobs_tensors(
+                    max_num_logprobs, metadata, logits, target_logits, bonus_rows,
+                    output_token_ids)
+            else:
+                logprobs_tensors = self._get_logprobs_tensors(
+                    max_num_logprobs, metadata, logits, None, bonus_rows, output_token_ids)
+        return SamplerOutput(sampled_token_ids=output_token_ids,
+                             logprobs_tensors=logprobs_tensors)
+
+    def _get_logprobs_tensors(self, max_num_logprobs: int, metadata: "SpecDecodeMetadata",
+                              logits: torch.Tensor, target_logits: torch.Tensor | None,
+                              bonus_logits: torch.Tensor,
+                              sampled_token_ids: torch.Tensor):
+        """Logprobs of every output position ``[B * (max_spec_len + 1)]`` (:229-300).
+
+        Position j of request i reads compact row ``start_i + j`` (clamped): verify row j
+        while j < K_i, the bonus row at j = K_i, so accepted, recovered and bonus tokens each
+        read their own row and padding positions read rows that parse_output drops with the
+        same valid mask.  Verify rows come from ``target_logits`` ([P, V], the processed rows
+        in the processed modes) or, when it is None, from ``logits`` at
+        ``metadata.target_logits_indices``; the bonus rows from ``bonus_logits`` [B, V].  The
+        values are the log-softmax of each row, or the rows themselves in the ``*_logits``
+        modes.  One ``mvsd_spec_logprobs`` launch.
+        """
+        from ..outputs import LogprobsTensors
+
+        if max_num_logprobs == -1:
+            raise NotImplementedError(
+                "speculative decoding with logprobs=-1 (the whole vocabulary) is not supported")
+        device = sampled_token_ids.device
+        nat.require_device_tensor(sampled_token_ids, "sampled_token_ids")
+        B, W = sampled_token_ids.shape
+        V = int(bonus_logits.shape[-1])
+        num_tokens = int(metadata.draft_token_ids.shape[0])
+        if not 0 <= max_num_logprobs <= min(LOGPROBS_MAX_K, V):
+            raise ValueError(f"logprobs={max_num_logprobs} outside [0, {min(LOGPROBS_MAX_K, V)}]")
+        keep = []
+        rows = None
+        if target_logits is None:
+            target_logits, rows = logits, _as(metadata.target_logits_indices, torch.int32, device)
+        if target_logits.dtype != torch.float32 or target_logits.stride(-1) != 1:
+            target_logits = (target_logits if rows is None else target_logits[rows.long()]).float()
+            target_logits = target_logits.contiguous()
+            rows = None
+        bonus = bonus_logits.to(torch.float32)
+        if bonus.stride(-1) != 1:
+            bonus = bonus.contiguous()
+        tokens = _as(sampled_token_ids, torch.int32, device)
+        cu = _as(metadata.cu_num_sampled_tokens, torch.int32, device)
+        keep += [target_logits, bonus, tokens, cu]
+        n_out = max_num_logprobs + 1
+        ids = torch.empty((B * W, n_out), dtype=torch.int32, device=device)
+        lps = torch.empty((B * W, n_out), dtype=torch.float32, device=device)
+        ranks = torch.empty((B * W,), dtype=torch.int32, device=device)
+        nat.check(nat.lib().mvsd_spec_logprobs(
+            ids.data_ptr(), lps.data_ptr(), ranks.data_ptr(),
+            target_logits.data_ptr() if num_tokens else None, target_logits.stride(0),
+            None if rows is None else rows.data_ptr(), bonus.data_ptr(), bonus.stride(0),
+            cu.data_ptr(), tokens.data_ptr(), tokens.stride(0), B, num_tokens, V, W,
+            max_num_logprobs, 1 if self.is_logits_logprobs_mode else 0, nat.stream_of(device)),
+            "mvsd_spec_logprobs")
+        return LogprobsTensors(ids, lps, ranks)
 
     def apply_logits_processors(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata,
                                 metadata: "SpecDecodeMetadata") -> torch.Tensor:
@@ -211,14 +287,20 @@ class RejectionSampler:
     @staticmethod
     def parse_output(output_token_ids: torch.Tensor, vocab_size: int, discard_req_indices=(),
                      logprobs_tensors=None):
-        """``[B, max_spec_len + 1]`` -> ``list[list[int]]``; the path's only D2H (:304-334)."""
-        if logprobs_tensors is not None:
-            raise NotImplementedError("speculative logprobs are not provided by this build")
+        """``[B, max_spec_len + 1]`` -> ``list[list[int]]``; the path's only D2H (:304-334).
+
+        Logprobs are filtered with the same valid mask, so rejected positions disappear from
+        tokens and logprobs together; ``cu_num_generated_tokens`` gives each request's first
+        row (before ``discard_req_indices`` is applied, as in the reference)."""
         out = output_token_ids.cpu().numpy()
         valid = (out != PLACEHOLDER_TOKEN_ID) & (out < vocab_size)
+        output_logprobs = None
+        if logprobs_tensors is not None:
+            cu_num_tokens = [0] + valid.sum(axis=1).cumsum().tolist()
+            output_logprobs = logprobs_tensors.filter(valid.flatten()).tolists(cu_num_tokens)
         if len(discard_req_indices) > 0:
             valid[list(discard_req_indices)] = False
-        return [row[valid[i]].tolist() for i, row in enumerate(out)], None
+        return [row[valid[i]].tolist() for i, row in enumerate(out)], output_logprobs
 
 
 def _penalty_entries(prompts, outputs, specs):
@@ -657,6 +739,9 @@ _SAMPLE_RECOVERED_TOKENS = sample_recovered_tokens
 
 
 # --------------------------------------------------------------------------- helpers
+
+# Largest logprobs=k of the speculative path (the kernel's per-thread candidate lists).
+LOGPROBS_MAX_K = 32
 
 # One zero-initialised verification workspace per (device, stream).  The kernel leaves it
 # zeroed after every call (include/mvsd.h), so it is reused without clearing; it only grows.
