@@ -164,3 +164,28 @@ def test_full_vocabulary_logprobs_are_refused(device):
                           top_p=None, max_num_logprobs=-1, prompt_token_ids=[[]])
     with pytest.raises(NotImplementedError):
         rs.RejectionSampler(BonusSampler())(meta, None, logits, sm)
+
+
+@pytest.mark.parametrize("V", [1000, 151936])
+def test_masked_rows_match_oracle(device, V):
+    """Rows whose entries are mostly -inf (processed rows after top-k / top-p / min_p): the
+    masked entries add nothing to the log-sum, whichever lane holds them."""
+    rng = np.random.default_rng(V)
+    drafts = [[1, 2, 3], [], [4, 5]]
+    meta = make_metadata(drafts, device=device)
+    B, W = len(drafts), meta.max_spec_len + 1
+    n_rows = meta.target_logits_indices.numel() + B
+    logits = torch.from_numpy(rng.normal(0, 2, (n_rows, V)).astype(np.float32))
+    keep = torch.from_numpy(rng.random((n_rows, V)) < 0.05)
+    keep[:, 3] = True
+    logits = torch.where(keep, logits, torch.full_like(logits, -math.inf)).to(device)
+    sampled = torch.from_numpy(rng.integers(0, 4, (B, W)).astype(np.int32)).to(device)
+    target = logits[meta.target_logits_indices]
+    bonus = logits[meta.bonus_logits_indices]
+    sampler = rs.RejectionSampler(BonusSampler("processed_logprobs"))
+    got = sampler._get_logprobs_tensors(5, meta, logits, target, bonus, sampled)
+    want = olp.get_logprobs_tensors(5, meta.cu_num_sampled_tokens, meta.target_logits_indices,
+                                    meta.bonus_logits_indices, target.cpu(), bonus.cpu(),
+                                    sampled.cpu())
+    assert not torch.isnan(got.logprobs).any()
+    _check(got, want, f"masked V={V}")

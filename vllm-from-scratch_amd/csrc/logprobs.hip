@@ -68,7 +68,7 @@ __global__ __launch_bounds__(kLpThreads) void spec_logprobs_kernel(LogprobParams
         s = s * expf(m - v);
         m = v;
       }
-      s += expf(v - m);
+      if (v != -INFINITY) s += expf(v - m);  // masked entries add nothing (and no NaN)
     }
     const float wm = wave_max(m);
     const float ws = wave_sum(m == -INFINITY ? 0.f : s * expf(m - wm));
