@@ -280,6 +280,20 @@ int mvsd_spec_logprobs(int32_t* ids, float* lps, int32_t* ranks, const float* ta
                        int64_t width, int64_t k, int logits_mode, mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
+/* sampler_rows — row operations of the regular sampler on fp32 rows x + r * stride.       */
+/* Replaces, in minivllm/sample/sampler.py: greedy_sample (:295-298, op 0: ids[r] = argmax */
+/* of row r, NaN first, lowest index on ties), apply_min_p (:280-293, op 1: with p the      */
+/* softmax of row r, entries with p < max(p) * aux[r] become -inf in place; aux[r] <= 0     */
+/* leaves the row), compute_logprobs (:313-315, op 3: out row r = (x - max) - log(sum      */
+/* exp(x - max))); and random_sample, minivllm/sample/ops/topk_topp_sampler.py:82-90        */
+/* (op 2: ids[r] = argmax of softmax(row r) / aux row r, the exponential race with the     */
+/* noise rows at aux + r * aux_stride).                                                     */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_sampler_rows(int op, int32_t* ids, float* out, int64_t out_stride, float* x,
+                      int64_t stride, const float* aux, int64_t aux_stride, int64_t num_rows,
+                      int64_t vocab_size, mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
 /* selftest — on-device check of an arithmetic assumption of the kernels.  No counterpart   */
 /* in the reference.  test 0: the FMA-corrected hardware reciprocal used for 1/E equals     */
 /* IEEE fp32 division for every b in [2^-126, 2^126).  test 1: the corrected division x/T  */

@@ -10,6 +10,7 @@
 
 #include "mvsd_device.h"
 #include "rows.h"
+#include "sampler.h"
 #include "selftest.h"
 #include "verify.h"
 #include "logprobs.h"
@@ -428,6 +429,22 @@ int mvsd_spec_logprobs(int32_t* ids, float* lps, int32_t* ranks, const float* ta
   p.lps = lps;
   p.ranks = ranks;
   return hip_status(mvsd::launch_spec_logprobs(p, (hipStream_t)stream));
+}
+
+int mvsd_sampler_rows(int op, int32_t* ids, float* out, int64_t out_stride, float* x,
+                      int64_t stride, const float* aux, int64_t aux_stride, int64_t num_rows,
+                      int64_t vocab_size, mvsd_stream_t stream) {
+  if (num_rows < 0 || vocab_size <= 0 || op < 0 || op > 3) return MVSD_E_INVALID;
+  if (num_rows == 0) return MVSD_OK;
+  if (num_rows > 0x7fffffff || vocab_size > 0x7fffffff) return MVSD_E_RANGE;
+  if (!x || stride < vocab_size) return MVSD_E_INVALID;
+  if ((op == mvsd::kSamplerArgmax || op == mvsd::kSamplerRace) && !ids) return MVSD_E_INVALID;
+  if (op == mvsd::kSamplerMinP && !aux) return MVSD_E_INVALID;
+  if (op == mvsd::kSamplerRace && (!aux || aux_stride < vocab_size)) return MVSD_E_INVALID;
+  if (op == mvsd::kSamplerLogSoftmax && (!out || out_stride < vocab_size)) return MVSD_E_INVALID;
+  return hip_status(mvsd::launch_sampler_rows(op, ids, out, out_stride, x, stride, aux,
+                                              aux_stride, num_rows, vocab_size,
+                                              (hipStream_t)stream));
 }
 
 int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream) {

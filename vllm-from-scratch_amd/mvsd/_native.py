@@ -96,6 +96,8 @@ SIGNATURES = {
     "mvsd_spec_logprobs": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
                                    c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                                    c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "mvsd_sampler_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
+                                  c_void_p, c_int64, c_int64, c_int64, c_void_p]),
     "mvsd_ngram_propose": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
                                    c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int,
                                    c_int64, c_int32, c_int32, c_int32, c_int, c_int64,

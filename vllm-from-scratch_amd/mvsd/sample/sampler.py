@@ -1,0 +1,274 @@
+"""The regular sampler on MI355X (drop-in for minivllm/sample/sampler.py ``Sampler``).
+
+The rejection sampler takes its bonus tokens from a sampler object (rejection_sampler.py:
+169-181); this is one with the reference's names, call protocol and order of operations
+(sampler.py:73-120, :243-349):
+
+    logits -> fp32
+    -> penalties (bonus rows: history = committed output + all drafts) -> min_tokens
+    -> greedy rows: argmax (no temperature)
+    -> random rows: / temperature -> min_p -> top-k / top-p -> exponential race
+    -> rows with temperature < eps take the greedy result
+    -> logprobs of the raw (before any processing) or processed rows on request
+
+Every row operation is a HIP kernel (``mvsd_apply_logits_processors``,
+``mvsd_apply_top_k_top_p``, ``mvsd_sampler_rows``, ``mvsd_spec_logprobs``); the temperature
+divide is a tensor divide, as in the reference.  The exponential noise is drawn by
+``generate_sampler_noise`` in the reference's order (the whole block from the global RNG when
+some row has no generator, then each seeded row from its generator), so a given RNG state
+gives the same noise; the function is a seam that tests may replace.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .. import _native as nat
+from ..outputs import LogprobsTensors, SamplerOutput
+from .metadata import SAMPLING_EPS, SamplingMetadata
+from .ops.topk_topp_sampler import apply_top_k_top_p
+
+_ARGMAX, _MIN_P, _RACE, _LOG_SOFTMAX = 0, 1, 2, 3
+
+
+def generate_sampler_noise(shape, generators: dict[int, torch.Generator],
+                           device: torch.device) -> torch.Tensor:
+    """Exp(1) noise of random_sample (ops/topk_topp_sampler.py:82-90)."""
+    noise = torch.empty(shape, dtype=torch.float32, device=device)
+    if len(generators) != shape[0]:
+        noise.exponential_()
+    for row, generator in generators.items():
+        noise[row].exponential_(generator=generator)
+    return noise
+
+
+def _rows(op, x: torch.Tensor, *, ids=None, out=None, aux=None):
+    nat.require_device_tensor(x, "logits")
+    assert x.ndim == 2 and x.dtype == torch.float32 and x.stride(1) == 1
+    n, V = x.shape
+    nat.check(nat.lib().mvsd_sampler_rows(
+        op, nat.ptr(ids), nat.ptr(out), 0 if out is None else out.stride(0), x.data_ptr(),
+        x.stride(0), nat.ptr(aux), 0 if aux is None or aux.ndim < 2 else aux.stride(0), n, V,
+        nat.stream_of(x.device)), "mvsd_sampler_rows")
+
+
+def random_sample(probs_logits: torch.Tensor, generators: dict[int, torch.Generator]):
+    """argmax of softmax(row) / E per row (the exponential race, ops/topk_topp_sampler.py:82-90,
+    with the softmax of the processed logits folded in)."""
+    x = probs_logits.contiguous()
+    noise = generate_sampler_noise(tuple(x.shape), generators, x.device)
+    noise = noise.to(device=x.device, dtype=torch.float32).contiguous()
+    ids = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)
+    _rows(_RACE, x, ids=ids, aux=noise)
+    return ids.to(torch.int64)
+
+
+class TopKTopPSampler:
+    """Temperature-scaled logits -> one token per row, with the processed logits or logprobs of
+    the ``processed_*`` modes (ops/topk_topp_sampler.py:93-115)."""
+
+    def __init__(self, logprobs_mode: str = "raw_logprobs") -> None:
+        self.logprobs_mode = logprobs_mode
+
+    def __call__(self, logits, generators, k, p):
+        logits = apply_top_k_top_p(logits, k, p)
+        logits_to_return = None
+        if self.logprobs_mode == "processed_logits":
+            logits_to_return = logits
+        elif self.logprobs_mode == "processed_logprobs":
+            logits_to_return = Sampler.compute_logprobs(logits)
+        return random_sample(logits, generators), logits_to_return
+
+
+class Sampler:
+    def __init__(self, logprobs_mode: str = "raw_logprobs") -> None:
+        self.logprobs_mode = logprobs_mode
+        self.topk_topp_sampler = TopKTopPSampler(logprobs_mode)
+
+    def forward(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata,
+                predict_bonus_token: bool = False,
+                logprobs_mode_override: str | None = None) -> SamplerOutput:
+        logprobs_mode = logprobs_mode_override or self.logprobs_mode
+        assert not (sampling_metadata.all_greedy and sampling_metadata.all_random)
+        num_logprobs = sampling_metadata.max_num_logprobs
+        raw_logprobs = None
+        if num_logprobs is not None:
+            if logprobs_mode == "raw_logprobs":
+                raw_logprobs = self.compute_logprobs(logits.to(torch.float32))
+            elif logprobs_mode == "raw_logits":
+                raw_logprobs = (logits.clone() if logits.dtype == torch.float32
+                                else logits.to(torch.float32))
+        logits = logits.to(torch.float32).contiguous()
+        logits = self.apply_logits_processors(logits, sampling_metadata, predict_bonus_token)
+        sampled, processed = self.sample(logits, sampling_metadata)
+        if processed is not None:
+            raw_logprobs = processed
+        sampled = sampled.long()
+        if num_logprobs is None:
+            tensors = None
+        elif num_logprobs == -1:
+            tensors = LogprobsTensors(torch.empty(0), raw_logprobs, torch.empty(0))
+        else:
+            tensors = self.gather_logprobs(raw_logprobs, num_logprobs, sampled)
+        return SamplerOutput(sampled_token_ids=sampled.to(torch.int32).unsqueeze(dim=1),
+                             logprobs_tensors=tensors)
+
+    # -------- logits processors --------
+
+    def apply_logits_processors(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata,
+                                predict_bonus_token: bool = False) -> torch.Tensor:
+        """Penalties, then min_tokens, in place (sampler.py:122-141); bonus rows
+        (``predict_bonus_token``) count every draft in the penalty history."""
+        output_token_ids = sampling_metadata.output_token_ids
+        if predict_bonus_token and not sampling_metadata.no_penalties:
+            output_token_ids = self._combine_outputs_with_spec_tokens(
+                output_token_ids, sampling_metadata.spec_token_ids)
+        logits = self.apply_penalties(logits, sampling_metadata, output_token_ids)
+        return self.apply_min_tokens(logits, sampling_metadata)
+
+    def apply_penalties(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata,
+                        output_token_ids: list[list[int]] | None = None) -> torch.Tensor:
+        from .rejection_sampler import _launch_logits_processors, _penalty_entries
+
+        if sampling_metadata.no_penalties:
+            return logits
+        if output_token_ids is None:
+            output_token_ids = sampling_metadata.output_token_ids
+        n = logits.shape[0]
+        cu = torch.arange(1, n + 1, dtype=torch.int32, device=logits.device)
+        entries = _penalty_entries(sampling_metadata.prompt_token_ids, output_token_ids,
+                                   [[] for _ in range(n)])
+        _launch_logits_processors(logits, cu, [1] * n, [[-1]] * n, entries, sampling_metadata,
+                                  None)
+        return logits
+
+    @staticmethod
+    def _combine_outputs_with_spec_tokens(output_token_ids, spec_token_ids=None):
+        """Bonus-row histories: committed output + every draft, one row per request
+        (sampler.py:159-175)."""
+        if spec_token_ids is None:
+            return output_token_ids
+        return [[*out, *spec] if spec else out
+                for out, spec in zip(output_token_ids, spec_token_ids)]
+
+    def apply_min_tokens(self, logits: torch.Tensor,
+                         sampling_metadata: SamplingMetadata) -> torch.Tensor:
+        """Stop tokens of rows whose committed output is shorter than min_tokens -> -inf
+        (sampler.py:177-190)."""
+        from .rejection_sampler import _launch_logits_processors
+
+        n = logits.shape[0]
+        n_mask = np.zeros(n, dtype=np.int32)
+        stop_off, stop_tok = [0], []
+        for row, (min_tokens, stop_ids) in enumerate(zip(sampling_metadata.min_tokens,
+                                                          sampling_metadata.stop_token_ids)):
+            if row < n and stop_ids and len(sampling_metadata.output_token_ids[row]) < min_tokens:
+                n_mask[row] = 1
+                stop_tok.extend(stop_ids)
+            if row < n:
+                stop_off.append(len(stop_tok))
+        if not n_mask.any():
+            return logits
+        stop_off += [len(stop_tok)] * (n + 1 - len(stop_off))
+        cu = torch.arange(1, n + 1, dtype=torch.int32, device=logits.device)
+        _launch_logits_processors(logits, cu, [1] * n, [[-1]] * n, None, None,
+                                  (n_mask, np.asarray(stop_off, np.int32),
+                                   np.asarray(stop_tok, np.int32)))
+        return logits
+
+    def apply_min_tokens_for_spec_decode(self, logits, sampling_metadata, num_draft_tokens):
+        """min_tokens on verify rows (sampler.py:192-228): the first clamp(min_tokens -
+        len(output), 0, K_i) rows of each request mask its stop tokens."""
+        from .rejection_sampler import _launch_logits_processors, _min_tokens_rows
+
+        num_draft = [int(k) for k in num_draft_tokens]
+        masks = _min_tokens_rows(sampling_metadata, num_draft)
+        if masks is None:
+            return logits
+        cu = torch.as_tensor(np.cumsum(num_draft), dtype=torch.int32, device=logits.device)
+        _launch_logits_processors(logits, cu, num_draft, [[-1] * k for k in num_draft], None,
+                                  None, masks)
+        return logits
+
+    # -------- sampling --------
+
+    def sample(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata,
+               logprobs_mode: str | None = None):
+        """(tokens, processed logits / logprobs of the processed_* modes) (sampler.py:243-278)."""
+        mode = logprobs_mode or self.logprobs_mode
+        if sampling_metadata.all_random:
+            greedy_sampled = None
+        else:
+            greedy_sampled = self.greedy_sample(logits)
+            if sampling_metadata.all_greedy:
+                processed = None
+                if sampling_metadata.max_num_logprobs is not None:
+                    if mode == "processed_logits":
+                        processed = logits
+                    elif mode == "processed_logprobs":
+                        processed = self.compute_logprobs(logits)
+                return greedy_sampled, processed
+        temperature = sampling_metadata.temperature
+        if temperature is None:
+            raise ValueError("random rows in the batch but no temperature tensor")
+        safe = torch.where(temperature < SAMPLING_EPS, torch.ones_like(temperature), temperature)
+        logits = logits.div_(safe.unsqueeze(dim=1))
+        logits = self.apply_min_p(logits, sampling_metadata.min_p)
+        random_sampled, processed = self.topk_topp_sampler(
+            logits, sampling_metadata.generators, sampling_metadata.top_k,
+            sampling_metadata.top_p)
+        if greedy_sampled is None:
+            return random_sampled, processed
+        return torch.where(temperature < SAMPLING_EPS, greedy_sampled, random_sampled), processed
+
+    @staticmethod
+    def apply_min_p(logits: torch.Tensor, min_p: torch.Tensor | None) -> torch.Tensor:
+        """Entries whose probability is below max(p) * min_p -> -inf, in place
+        (sampler.py:280-293)."""
+        if min_p is None:
+            return logits
+        _rows(_MIN_P, logits, aux=min_p.to(device=logits.device, dtype=torch.float32).contiguous())
+        return logits
+
+    @staticmethod
+    def greedy_sample(logits: torch.Tensor) -> torch.Tensor:
+        x = logits.contiguous()
+        ids = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)
+        _rows(_ARGMAX, x, ids=ids)
+        return ids.to(torch.int64)
+
+    # -------- logprobs --------
+
+    @staticmethod
+    def compute_logprobs(logits: torch.Tensor) -> torch.Tensor:
+        x = logits.to(torch.float32).contiguous()
+        out = torch.empty_like(x)
+        _rows(_LOG_SOFTMAX, x, out=out)
+        return out
+
+    @staticmethod
+    def batched_count_greater_than(x: torch.Tensor, values: torch.Tensor) -> torch.Tensor:
+        """#{x >= value} per row (sampler.py:318-327): the rank of a token."""
+        return (x >= values).sum(-1)
+
+    @staticmethod
+    def gather_logprobs(logprobs: torch.Tensor, num_logprobs: int,
+                        token_ids: torch.Tensor) -> LogprobsTensors:
+        """Sampled token first, then the top ``num_logprobs`` (value, then index), and the
+        sampled token's rank (sampler.py:330-349); one ``mvsd_spec_logprobs`` launch with each
+        row its own position."""
+        assert token_ids.dtype == torch.int64
+        x = logprobs.to(torch.float32).contiguous()
+        n, V = x.shape
+        device = x.device
+        ids = torch.empty((n, num_logprobs + 1), dtype=torch.int32, device=device)
+        lps = torch.empty((n, num_logprobs + 1), dtype=torch.float32, device=device)
+        ranks = torch.empty((n,), dtype=torch.int32, device=device)
+        cu = torch.arange(1, n + 1, dtype=torch.int32, device=device)
+        tokens = token_ids.to(device=device, dtype=torch.int32).reshape(n, 1).contiguous()
+        nat.check(nat.lib().mvsd_spec_logprobs(
+            ids.data_ptr(), lps.data_ptr(), ranks.data_ptr(), None, V, None, x.data_ptr(),
+            x.stride(0), cu.data_ptr(), tokens.data_ptr(), 1, n, 0, V, 1, num_logprobs, 1,
+            nat.stream_of(device)), "mvsd_spec_logprobs")
+        return LogprobsTensors(ids, lps, ranks)

@@ -64,3 +64,35 @@ def make_metadata(draft_token_ids: list[list[int]],
         bonus_logits_indices=dev(bonus_logits_indices),
         logits_indices=dev(logits_indices),
     )
+
+
+def sampling_metadata(temperatures, drafts, *, device="cpu", max_num_logprobs=None,
+                      logprobs_mode="raw_logprobs", output_token_ids=None,
+                      prompt_token_ids=None, top_k=None, top_p=None, min_p=None,
+                      no_penalties=True, presence_penalties=None, frequency_penalties=None,
+                      repetition_penalties=None, min_tokens=None, stop_token_ids=None,
+                      generators=None):
+    """A row-aligned SamplingMetadata from plain lists (the keyword set of the reference's
+    test builder, tests/step68/spec68_helpers.py:22-51): temperatures below 1e-5 are greedy;
+    missing histories, min_tokens and stop lists default to empty."""
+    from ..sample.metadata import SAMPLING_EPS, SamplingMetadata
+
+    def tensor(values, dtype=torch.float32):
+        return None if values is None else torch.tensor(values, dtype=dtype, device=device)
+
+    n = len(temperatures)
+    all_greedy = all(t < SAMPLING_EPS for t in temperatures)
+    return SamplingMetadata(
+        temperature=None if all_greedy else tensor(temperatures),
+        all_greedy=all_greedy, all_random=all(t >= SAMPLING_EPS for t in temperatures),
+        top_k=tensor(top_k, torch.int64), top_p=tensor(top_p), min_p=tensor(min_p),
+        generators=dict(generators or {}), no_penalties=no_penalties,
+        prompt_token_ids=prompt_token_ids or [[] for _ in range(n)],
+        output_token_ids=output_token_ids or [[] for _ in range(n)],
+        min_tokens=min_tokens or [0] * n,
+        stop_token_ids=stop_token_ids or [[] for _ in range(n)],
+        spec_token_ids=[list(d) for d in drafts],
+        presence_penalties=tensor(presence_penalties),
+        frequency_penalties=tensor(frequency_penalties),
+        repetition_penalties=tensor(repetition_penalties),
+        max_num_logprobs=max_num_logprobs, logprobs_mode=logprobs_mode)
