@@ -201,6 +201,24 @@ int mvsd_apply_top_k_top_p(float* logits, int64_t logits_stride, const int64_t* 
                            mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
+/* ngram_valid_sampled — the valid sampled tokens of one step, per request.               */
+/* Replaces: NgramProposerGPU.update_token_ids_ngram                                     */
+/*           (minivllm/spec_decode/ngram_proposer_gpu.py:247-290).                        */
+/*                                                                                        */
+/* sampled [num_reqs, width] int32 (row stride sampled_stride); discard [num_reqs] uint8  */
+/* (NULL = keep all).  valid_ids [num_reqs, width] = sampled, or -1 for discarded rows.   */
+/* counts[i] = #{j : valid_ids[i, j] != -1 and valid_ids[i, j] < vocab_size}.             */
+/* next_token_ids[i] = valid_ids[i, counts[i] - 1] when counts[i] > 0, else               */
+/* token_ids[i, max(num_tokens[i] - 1, 0)] (clamped to the row).                          */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_ngram_valid_sampled(int32_t* next_token_ids, int32_t* counts, int32_t* valid_ids,
+                             int64_t valid_stride, const int32_t* sampled,
+                             int64_t sampled_stride, int64_t width, const uint8_t* discard,
+                             const int32_t* token_ids, int64_t row_stride,
+                             const int32_t* num_tokens, int64_t vocab_size, int64_t num_reqs,
+                             mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
 /* ngram_propose — prompt-lookup drafts for a batch of int32 token histories.            */
 /* Replaces: NgramGPUKernel._find_first_and_extract_all_n_parallel + forward             */
 /*           (minivllm/spec_decode/ngram_proposer_gpu.py:56-148) with the in-place       */

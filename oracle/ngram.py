@@ -100,3 +100,25 @@ def find_python(tokens, min_n, max_n, k) -> tuple[int, int]:
             if t[s:s + n] == t[L - n:]:
                 return s, n
     return -1, 0
+
+
+def valid_sampled_tokens(sampled, discard, token_ids, num_tokens, vocab_size):
+    """NgramProposerGPU.update_token_ids_ngram (minivllm/spec_decode/ngram_proposer_gpu.py:
+    247-290) in numpy: (next_token_ids, counts, valid_ids).  Discarded rows become -1; the
+    count is #{v != -1 and v < vocab_size}; the next token is valid_ids[i, count - 1] when the
+    count is positive, else token_ids[i, max(num_tokens[i] - 1, 0)].  Pinned by the
+    reference's known answer (tests/step60/test_ngram_gpu_state.py:157-179) and by the
+    per-row definition in tests/test_oracle_ngram.py."""
+    sampled = np.asarray(sampled, dtype=np.int64)
+    valid = sampled.copy()
+    valid[np.asarray(discard, dtype=bool)] = -1
+    ok = (valid != -1) & (valid < vocab_size)
+    counts = ok.sum(axis=1)
+    last = np.clip(counts - 1, 0, None)
+    selected = valid[np.arange(valid.shape[0]), last] if valid.shape[1] else \
+        np.zeros(valid.shape[0], np.int64)
+    tokens = np.asarray(token_ids, dtype=np.int64)
+    back = np.clip(np.asarray(num_tokens, dtype=np.int64) - 1, 0, None)
+    backup = tokens[np.arange(tokens.shape[0]), back]
+    nxt = np.where(counts > 0, selected, backup)
+    return nxt.astype(np.int32), counts.astype(np.int32), valid.astype(np.int32)

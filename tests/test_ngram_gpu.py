@@ -121,6 +121,40 @@ def test_update_token_ids_and_masked_scatter(device):
     assert tokens[1, :7].tolist() == [4, 5, 6, 5, 0, 0, 0]
 
 
+@pytest.mark.parametrize("num_reqs,width", [(1, 1), (37, 5), (1024, 8)])
+def test_valid_sampled_tokens_match_oracle(device, num_reqs, width):
+    """update_token_ids_ngram (one mvsd_ngram_valid_sampled launch) equals oracle/ngram.py's
+    restatement: -1 and ids >= vocab anywhere in a row, discarded rows, empty histories, and
+    sampled rows given as a list of ragged lists."""
+    rng = np.random.default_rng(num_reqs * 10 + width)
+    vocab = 50
+    histories = [list(rng.integers(0, vocab, int(rng.integers(0, 12)))) for _ in range(num_reqs)]
+    batch = FakeInputBatch(histories, 16, vocab_size=vocab)
+    tokens, lens = state(histories, 16, device)
+    sampled = rng.integers(-1, vocab + 5, (num_reqs, width)).astype(np.int32)
+    discard = rng.random(num_reqs) < 0.25
+    prop = NgramProposerGPU(Cfg(k=2), device)
+    nxt, counts, valid = prop.update_token_ids_ngram(
+        torch.from_numpy(sampled).to(device), batch, tokens, lens,
+        torch.from_numpy(discard).to(device))
+    want = ong.valid_sampled_tokens(sampled, discard, tokens.cpu().numpy(), lens.cpu().numpy(),
+                                      vocab)
+    assert nxt.cpu().tolist() == want[0].tolist()
+    assert counts.cpu().tolist() == want[1].tolist()
+    assert valid.cpu().tolist() == want[2].tolist()
+    # ragged lists: padded with -1 to the longest row
+    ragged = [list(rng.integers(0, vocab, int(rng.integers(0, width + 1)))) for _ in
+              range(num_reqs)]
+    nxt, counts, valid = prop.update_token_ids_ngram(ragged, batch, tokens, lens,
+                                                     torch.from_numpy(discard).to(device))
+    w = max(max(len(r) for r in ragged), 1)
+    padded = np.array([r + [-1] * (w - len(r)) for r in ragged], dtype=np.int32)
+    want = ong.valid_sampled_tokens(padded, discard, tokens.cpu().numpy(), lens.cpu().numpy(),
+                                      vocab)
+    assert nxt.cpu().tolist() == want[0].tolist()
+    assert counts.cpu().tolist() == want[1].tolist()
+
+
 def test_history_follows_request_ids_across_reorder(device):
     """tests/step60/test_ngram_gpu_state.py:182-225"""
     prop = NgramProposerGPU(Cfg(k=2, min_n=1, max_n=1), device)

@@ -92,3 +92,29 @@ def test_kmp_equals_brute_force_large_random():
         for r in range(R):
             assert d1[r, :c1[r]].tolist() == ngram.find_brute_cpu(tokens[r, :lens[r]], lo, hi,
                                                                   10 ** 9, 5)
+
+
+def test_valid_sampled_tokens_reference_kat():
+    """tests/step60/test_ngram_gpu_state.py:157-179: row 0 discarded, 99 >= vocab 10 does not
+    count, the discarded row falls back to its history's last token."""
+    nxt, counts, valid = ngram.valid_sampled_tokens([[7, 8], [5, 99]], [True, False],
+                                                    [[1, 2, 3, 0], [4, 5, 6, 0]], [3, 3], 10)
+    assert counts.tolist() == [0, 1]
+    assert valid.tolist() == [[-1, -1], [5, 99]]
+    assert nxt.tolist() == [3, 5]
+
+
+def test_valid_sampled_tokens_by_definition():
+    """Row by row with plain loops: the count skips -1 and ids >= vocab wherever they sit, and
+    the next token is the entry at column count - 1 (not the last valid entry)."""
+    rng = np.random.default_rng(8)
+    sampled = rng.integers(-1, 14, (40, 5))
+    discard = rng.random(40) < 0.2
+    tokens = rng.integers(0, 10, (40, 9))
+    lens = rng.integers(0, 10, 40)
+    nxt, counts, valid = ngram.valid_sampled_tokens(sampled, discard, tokens, lens, 10)
+    for i in range(40):
+        row = [-1] * 5 if discard[i] else list(sampled[i])
+        c = sum(1 for v in row if v != -1 and v < 10)
+        assert valid[i].tolist() == row and counts[i] == c
+        assert nxt[i] == (row[c - 1] if c else tokens[i, max(lens[i] - 1, 0)])

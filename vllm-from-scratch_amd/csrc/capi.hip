@@ -545,6 +545,23 @@ int mvsd_sample_recovered_tokens(int32_t* recovered_token_ids, const int32_t* cu
                                            (hipStream_t)stream));
 }
 
+int mvsd_ngram_valid_sampled(int32_t* next_token_ids, int32_t* counts, int32_t* valid_ids,
+                             int64_t valid_stride, const int32_t* sampled,
+                             int64_t sampled_stride, int64_t width, const uint8_t* discard,
+                             const int32_t* token_ids, int64_t row_stride,
+                             const int32_t* num_tokens, int64_t vocab_size, int64_t num_reqs,
+                             mvsd_stream_t stream) {
+  if (num_reqs < 0 || width < 0 || vocab_size < 0) return MVSD_E_INVALID;
+  if (num_reqs == 0) return MVSD_OK;
+  if (!next_token_ids || !counts || !valid_ids || !token_ids || !num_tokens) return MVSD_E_INVALID;
+  if (width > 0 && !sampled) return MVSD_E_INVALID;
+  if (valid_stride < width || sampled_stride < width || row_stride < 1) return MVSD_E_INVALID;
+  if (vocab_size > 0x7fffffff || num_reqs > 0x7fffffff) return MVSD_E_RANGE;
+  return hip_status(mvsd::launch_ngram_valid_sampled(
+      next_token_ids, counts, valid_ids, valid_stride, sampled, sampled_stride, width, discard,
+      token_ids, row_stride, num_tokens, (int32_t)vocab_size, num_reqs, (hipStream_t)stream));
+}
+
 int mvsd_ngram_propose(int32_t* drafts, int32_t* num_valid, int32_t* token_ids,
                        int64_t row_stride, int64_t max_seq_len, const int32_t* num_tokens,
                        const int32_t* new_tokens, int64_t new_tokens_stride,

@@ -125,4 +125,52 @@ hipError_t launch_ngram(const NgramParams& p, int64_t num_reqs, hipStream_t stre
   return hipGetLastError();
 }
 
+// Valid sampled tokens of one step, one thread per request
+// (minivllm/spec_decode/ngram_proposer_gpu.py:247-290): a discarded request's row becomes -1;
+// the count is the number of entries that are not -1 and below the vocabulary size; the next
+// token is entry count - 1 of the row when the count is positive, else the history's token at
+// max(num_tokens - 1, 0).
+__global__ __launch_bounds__(256) void ngram_valid_sampled_kernel(
+    int32_t* next_token_ids, int32_t* counts, int32_t* valid_ids, int64_t valid_stride,
+    const int32_t* sampled, int64_t sampled_stride, int64_t width, const uint8_t* discard,
+    const int32_t* token_ids, int64_t row_stride, const int32_t* num_tokens, int32_t vocab_size,
+    int64_t num_reqs) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= num_reqs) return;
+  const bool drop = discard && discard[r];
+  const int32_t* src = sampled + r * sampled_stride;
+  int32_t* dst = valid_ids + r * valid_stride;
+  int count = 0;
+  for (int64_t j = 0; j < width; ++j) {
+    const int32_t v = drop ? -1 : src[j];
+    dst[j] = v;
+    count += (v != -1 && v < vocab_size) ? 1 : 0;
+  }
+  int32_t next;
+  if (count > 0) {
+    next = src[count - 1];  // count > 0 means the row was kept
+  } else {
+    // lengths beyond the row are clamped to its last column (the reference would raise)
+    const int64_t n = num_tokens[r];
+    next = token_ids[r * row_stride + (n > 1 ? (n - 1 < row_stride ? n - 1 : row_stride - 1) : 0)];
+  }
+  counts[r] = count;
+  next_token_ids[r] = next;
+}
+
+hipError_t launch_ngram_valid_sampled(int32_t* next_token_ids, int32_t* counts,
+                                      int32_t* valid_ids, int64_t valid_stride,
+                                      const int32_t* sampled, int64_t sampled_stride,
+                                      int64_t width, const uint8_t* discard,
+                                      const int32_t* token_ids, int64_t row_stride,
+                                      const int32_t* num_tokens, int32_t vocab_size,
+                                      int64_t num_reqs, hipStream_t stream) {
+  if (num_reqs == 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((num_reqs + 255) / 256);
+  hipLaunchKernelGGL(ngram_valid_sampled_kernel, dim3(blocks), dim3(256), 0, stream,
+                     next_token_ids, counts, valid_ids, valid_stride, sampled, sampled_stride,
+                     width, discard, token_ids, row_stride, num_tokens, vocab_size, num_reqs);
+  return hipGetLastError();
+}
+
 }  // namespace mvsd

@@ -43,4 +43,12 @@ struct NgramParams {
 
 hipError_t launch_ngram(const NgramParams& p, int64_t num_reqs, hipStream_t stream);
 
+hipError_t launch_ngram_valid_sampled(int32_t* next_token_ids, int32_t* counts,
+                                      int32_t* valid_ids, int64_t valid_stride,
+                                      const int32_t* sampled, int64_t sampled_stride,
+                                      int64_t width, const uint8_t* discard,
+                                      const int32_t* token_ids, int64_t row_stride,
+                                      const int32_t* num_tokens, int32_t vocab_size,
+                                      int64_t num_reqs, hipStream_t stream);
+
 }  // namespace mvsd

@@ -102,6 +102,9 @@ SIGNATURES = {
                                    c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int,
                                    c_int64, c_int32, c_int32, c_int32, c_int, c_int64,
                                    c_void_p]),
+    "mvsd_ngram_valid_sampled": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
+                                         c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                         c_void_p, c_int64, c_int64, c_void_p]),
 }
 
 _lib = None

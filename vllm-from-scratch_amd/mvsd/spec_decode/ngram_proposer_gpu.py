@@ -126,25 +126,31 @@ class NgramProposerGPU:
                                token_ids_gpu: torch.Tensor, num_tokens_no_spec: torch.Tensor,
                                discard_request_mask: torch.Tensor,
                                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        """Valid sampled tokens of this step (:247-290): discarded rows become -1, ids
-        >= vocab do not count, and the fallback next token is the history's last one."""
+        """Valid sampled tokens of this step (:247-290) in one ``mvsd_ngram_valid_sampled``
+        launch: discarded rows become -1, ids >= vocab do not count, and a row without valid
+        tokens takes the history's last token as its next token."""
         num_reqs = gpu_input_batch.num_reqs
         if isinstance(sampled_token_ids, list):
             width = max(max((len(s) for s in sampled_token_ids), default=0), 1)
             padded = [list(s) + [-1] * (width - len(s)) for s in sampled_token_ids]
             sampled_token_ids = torch.tensor(padded, dtype=torch.int32, device=self.device)
-        backup_idx = (num_tokens_no_spec[:num_reqs] - 1).clamp_(min=0)
-        backup_next = torch.gather(token_ids_gpu[:num_reqs], 1,
-                                   backup_idx.long().unsqueeze(1)).squeeze(1)
-        valid_ids = sampled_token_ids.clone()
-        valid_ids.masked_fill_(discard_request_mask[:num_reqs].unsqueeze(1), -1)
-        valid = (valid_ids != -1) & (valid_ids < gpu_input_batch.vocab_size)
-        counts = valid.sum(dim=1).to(torch.int32)
-        last = counts - 1
-        has = last >= 0
-        last.clamp_(min=0)
-        selected = torch.gather(valid_ids, 1, last.long().unsqueeze(1)).squeeze(1)
-        next_token_ids = torch.where(has, selected, backup_next)
+        sampled = sampled_token_ids[:num_reqs]
+        if sampled.dtype != torch.int32 or sampled.stride(-1) != 1:
+            sampled = sampled.to(torch.int32).contiguous()
+        nat.require_device_tensor(sampled, "sampled_token_ids")
+        tokens = token_ids_gpu if token_ids_gpu.stride(-1) == 1 else token_ids_gpu.contiguous()
+        lens = num_tokens_no_spec.to(torch.int32).contiguous()
+        discard = discard_request_mask[:num_reqs].to(torch.uint8).contiguous()
+        width = sampled.shape[1]
+        valid_ids = torch.empty((num_reqs, width), dtype=torch.int32, device=sampled.device)
+        counts = torch.empty((num_reqs,), dtype=torch.int32, device=sampled.device)
+        next_token_ids = torch.empty((num_reqs,), dtype=torch.int32, device=sampled.device)
+        nat.check(nat.lib().mvsd_ngram_valid_sampled(
+            next_token_ids.data_ptr(), counts.data_ptr(), valid_ids.data_ptr(),
+            valid_ids.stride(0), sampled.data_ptr(), sampled.stride(0), width,
+            discard.data_ptr(), tokens.data_ptr(), tokens.stride(0), lens.data_ptr(),
+            int(gpu_input_batch.vocab_size), num_reqs, nat.stream_of(sampled.device)),
+            "mvsd_ngram_valid_sampled")
         return next_token_ids, counts, valid_ids
 
     def load_model(self, *args, **kwargs):
