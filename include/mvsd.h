@@ -321,6 +321,38 @@ int mvsd_sampler_rows(int op, int32_t* ids, float* out, int64_t out_stride, floa
 /* ------------------------------------------------------------------------------------ */
 int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream);
 
+/* ------------------------------------------------------------------------------------ */
+/* v2_rejection_sample — the V2 model runner's verification, non-block path.              */
+/* Replaces: rejection_sample (minivllm/worker/gpu/spec_decode/rejection_sampler_utils.py: */
+/*           935-1201) with use_block_verification=False: _compute_local_logits_stats_     */
+/*           kernel (:206-316), _rejection_kernel (:497-706), _resample_kernel (:709-866), */
+/*           _insert_resampled_kernel (:869-932), and the counter draws of                  */
+/*           minivllm/worker/gpu/sample/gumbel.py:72-131 (Philox4x32-10, as Triton's        */
+/*           tl.randint4x / tl.rand).                                                       */
+/* target_logits [num_logits, V] (F32/BF16/F16, already temperature-scaled, as the         */
+/* reference assumes); draft_logits [states, K, V] pre-temperature or NULL; draft_sampled  */
+/* [num_logits] int32 (entry j+1 is the draft at row j); cu_num_logits [num_reqs + 1]      */
+/* int32 with a leading 0; pos [num_logits] int64; idx_mapping [num_reqs] and              */
+/* expanded_idx_mapping / expanded_local_pos [num_logits] int32; temperature [states] f32; */
+/* seed [states] int64; synthetic_conditional_rates [K] f32 or NULL.  Writes sampled       */
+/* [num_reqs, >= K+1] int64 (entries at or past num_sampled[r] are left as they were) and  */
+/* num_sampled [num_reqs] int32.  workspace: mvsd_v2_workspace_bytes() bytes, 256-byte    */
+/* aligned, caller-owned, no initial contents needed.  Draft ids >= V count as invalid     */
+/* (the reference does not check them); a request whose cu_num_logits span is empty, out  */
+/* of range or longer than K+1 gets num_sampled 0.                                          */
+/* ------------------------------------------------------------------------------------ */
+int64_t mvsd_v2_workspace_bytes(int64_t num_logits, int64_t num_reqs, int64_t vocab_size);
+
+int mvsd_v2_rejection_sample(
+    int64_t* sampled, int64_t sampled_stride, int32_t* num_sampled, const void* target_logits,
+    int target_dtype, int64_t target_stride, int64_t num_logits, const void* draft_logits,
+    int draft_dtype, int64_t draft_stride0, int64_t draft_stride1, const int32_t* draft_sampled,
+    const int32_t* cu_num_logits, const int64_t* pos, const int32_t* idx_mapping,
+    const int32_t* expanded_idx_mapping, const int32_t* expanded_local_pos,
+    const float* temperature, const int64_t* seed, int64_t num_req_states, int64_t num_reqs,
+    int64_t vocab_size, int32_t num_speculative_steps, const float* synthetic_conditional_rates,
+    int use_fp64, void* workspace, int64_t workspace_bytes, mvsd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

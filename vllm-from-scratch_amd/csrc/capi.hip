@@ -116,6 +116,11 @@ WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
 
 }  // namespace
 
+namespace mvsd {
+// Status of a HIP call for the entry points defined in other sources (MVSD_OK on success).
+int record_hip_error(hipError_t err) { return hip_status(err); }
+}  // namespace mvsd
+
 extern "C" {
 
 int mvsd_version(void) { return (0 << 16) | (1 << 8) | 0; }

@@ -1,0 +1,562 @@
+// V2 speculative-decoding verification (the V2 model runner's rejection sampler) for gfx950.
+//
+// Replaces rejection_sample (minivllm/worker/gpu/spec_decode/rejection_sampler_utils.py:935-1201),
+// non-block path, with four launches on the caller's stream:
+//   1. v2_stats_kernel     one workgroup per (verify row, 4096-column chunk): greedy rows keep
+//                          the chunk's (max, first argmax); random rows keep (max, sum exp) of
+//                          the target row and of the temperature-scaled draft row (:206-316);
+//   2. v2_chain_kernel     one wavefront per request walks its draft chain (:497-706): the
+//                          chunk partials are combined across lanes, the acceptance uniform
+//                          is drawn from the request's counter stream at the row's position;
+//   3. v2_resample_kernel  one workgroup per (request, chunk) scores the rejected (or bonus)
+//                          row: residual log-probabilities log(p - q) (or the target row, or
+//                          the target row without the rejected draft) plus Gumbel noise drawn
+//                          per vocabulary index (:709-866, gumbel.py:95-131);
+//   4. v2_insert_kernel    one wavefront per request takes the first chunk maximum and writes
+//                          the resampled token and the sampled count (:869-932).
+// The counter stream is Philox4x32 with ten rounds keyed by the 64-bit seed and counted by
+// the 64-bit position (or the 32-bit vocabulary index), the generator behind Triton's
+// tl.randint4x / tl.rand that gumbel.py:72-91 uses (Salmon et al., SC 2011).
+//
+// HBM traffic per call: every verify row of the target once (and the draft row of random
+// requests once) in pass 1, one target row (and one draft row) per request in pass 3; the
+// partials are a few hundred bytes per row.
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "mvsd_device.h"
+
+namespace mvsd {
+
+int record_hip_error(hipError_t err);  // capi.hip: keeps err for mvsd_last_hip_error()
+
+namespace {
+
+constexpr int kV2Chunk = 4096;                 // columns per workgroup in passes 1 and 3
+constexpr int kV2PerThread = kV2Chunk / kThreads;  // 16
+
+// ------------------------------------------------------------------ counter RNG -------
+
+struct U32x4 {
+  uint32_t x, y, z, w;
+};
+
+__device__ inline U32x4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                      uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t h0 = __umulhi(0xCD9E8D57u, c2), l0 = 0xCD9E8D57u * c2;
+    const uint32_t h2 = __umulhi(0xD2511F53u, c0), l2 = 0xD2511F53u * c0;
+    c0 = h0 ^ c1 ^ k0;
+    c2 = h2 ^ c3 ^ k1;
+    c1 = l0;
+    c3 = l2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return {c0, c1, c2, c3};
+}
+
+// tl.randint4x(seed, offset) with a 64-bit offset: counter (lo, hi, 0, 0), key (seed lo, hi).
+__device__ inline U32x4 randint4x64(int64_t seed, int64_t offset) {
+  return philox4x32_10((uint32_t)offset, (uint32_t)((uint64_t)offset >> 32), 0u, 0u,
+                       (uint32_t)seed, (uint32_t)((uint64_t)seed >> 32));
+}
+
+// tl.randint4x(seed32, offset32) with a 32-bit seed and a 32-bit offset.
+__device__ inline U32x4 randint4x32(uint32_t seed, int32_t offset) {
+  return philox4x32_10((uint32_t)offset, 0u, 0u, 0u, seed, 0u);
+}
+
+// uint_to_uniform_float for 32 bits, clamped away from zero (tl_rand32, includes_zero=False).
+__device__ inline float uniform_f32(uint32_t bits) {
+  int32_t i = (int32_t)bits;
+  i = i < 0 ? -i - 1 : i;
+  const float u = (float)i * 4.6566127342e-10f;
+  return fmaxf(u, 4.6566127342e-10f);
+}
+
+// tl_rand64(includes_zero=False): (hi << 32 | lo) * 2^-64, clamped to the smallest normal.
+__device__ inline double uniform_f64(uint32_t lo, uint32_t hi) {
+  const uint64_t r = ((uint64_t)hi << 32) | lo;
+  const double u = (double)r * 5.421010862427522170037e-20;
+  return fmax(u, 2.2250738585072014e-308);
+}
+
+// ------------------------------------------------------------------ arguments ---------
+
+struct V2Params {
+  int64_t* sampled;
+  int64_t sampled_stride;
+  int32_t* num_sampled;
+  const void* target;
+  int64_t target_stride;
+  const void* draft;  // [states, K, V] or null
+  int64_t draft_stride0, draft_stride1;
+  const int32_t* draft_sampled;
+  const int32_t* cu_num_logits;
+  const int64_t* pos;
+  const int32_t* idx_mapping;
+  const int32_t* exp_idx_mapping;
+  const int32_t* exp_local_pos;
+  const float* temperature;
+  const int64_t* seed;
+  const float* rates;  // synthetic conditional rates [K] or null
+  int64_t num_logits;
+  int32_t num_reqs, num_states, vocab, K, nchunks;
+  int use_fp64;
+  bool target_aligned, draft_aligned;
+  // workspace
+  float *tmax, *tsum, *dmax, *dsum;
+  int32_t* targ;
+  int32_t* acc;  // accepted length per request, -1 for a malformed request
+  float *tlse, *dlse;
+  double* rval;
+  int32_t* ridx;
+};
+
+__device__ inline int clamp_state(int s, int n) { return s < 0 ? 0 : (s >= n ? n - 1 : s); }
+
+// Load this thread's 16 columns of a chunk as fp32; columns at or past `limit` read -inf.
+template <int DT>
+__device__ inline void load_chunk(const void* base, int64_t row_off, int c0, int limit,
+                                  bool aligned, float (&x)[kV2PerThread]) {
+  using S = typename Elem<DT>::storage;
+  constexpr int VEC = Elem<DT>::kVec;
+  const S* p = reinterpret_cast<const S*>(base) + row_off;
+#pragma unroll
+  for (int j = 0; j < kV2PerThread / VEC; ++j) {
+    const int col = c0 + (j * kThreads + (int)threadIdx.x) * VEC;
+    float v[VEC];
+    load_vec<DT>(p, col, limit, aligned, -INFINITY, v);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) x[j * VEC + e] = v[e];
+  }
+}
+
+__device__ inline int chunk_col(int c0, int k, int VEC) {
+  const int j = k / VEC, e = k % VEC;
+  return c0 + (j * kThreads + (int)threadIdx.x) * VEC + e;
+}
+
+// (max, sum exp(x - max)) of the block's values; sum is 0 when the max is -inf.
+__device__ inline void block_max_sumexp(float (&x)[kV2PerThread], float* s_max, float* s_sum,
+                                        float& m, float& s) {
+  float mv[1] = {-INFINITY};
+#pragma unroll
+  for (int k = 0; k < kV2PerThread; ++k) mv[0] = fmaxf(mv[0], x[k]);
+  block_max<1>(mv, s_max);
+  m = mv[0];
+  float sv[1] = {0.f};
+  if (m > -INFINITY) {
+#pragma unroll
+    for (int k = 0; k < kV2PerThread; ++k) sv[0] += expf(x[k] - m);
+  }
+  block_sum<1>(sv, s_sum);
+  s = m > -INFINITY ? sv[0] : 0.f;
+}
+
+// Best (value, index) over the block: larger value, then lower index.  Doubles so the fp64
+// Gumbel scores reduce with the same code.
+__device__ inline void block_best(double& v, int& i, double* s_v, int* s_i) {
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) {
+    const double ov = __shfl_xor(v, off);
+    const int oi = __shfl_xor(i, off);
+    const bool take = (ov > v) | ((ov == v) & (oi < i));
+    v = take ? ov : v;
+    i = take ? oi : i;
+  }
+  if (lane_id() == 0) {
+    s_v[wave_id()] = v;
+    s_i[wave_id()] = i;
+  }
+  __syncthreads();
+  v = s_v[0];
+  i = s_i[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    const bool take = (s_v[w] > v) | ((s_v[w] == v) & (s_i[w] < i));
+    v = take ? s_v[w] : v;
+    i = take ? s_i[w] : i;
+  }
+}
+
+// ------------------------------------------------------------------ pass 1 ------------
+
+template <int TDT, int DDT, bool HAS_DRAFT>
+__global__ __launch_bounds__(kThreads) void v2_stats_kernel(V2Params p) {
+  __shared__ float s_a[kWaves], s_b[kWaves];
+  __shared__ double s_v[kWaves];
+  __shared__ int s_i[kWaves];
+  const int64_t row = blockIdx.x;
+  const int c = blockIdx.y;
+  const int step = p.exp_local_pos[row];
+  if (step < 0 || step >= p.K) return;
+  const int st = clamp_state(p.exp_idx_mapping[row], p.num_states);
+  const float temp = p.temperature[st];
+  const int c0 = c * kV2Chunk;
+  const int64_t slot = row * p.nchunks + c;
+  float x[kV2PerThread];
+  load_chunk<TDT>(p.target, row * p.target_stride, c0, p.vocab, p.target_aligned, x);
+  if (temp == 0.f) {
+    double bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int k = 0; k < kV2PerThread; ++k) {
+      const int col = chunk_col(c0, k, Elem<TDT>::kVec);
+      const bool take = col < p.vocab && (((double)x[k] > bv) | (((double)x[k] == bv) & (col < bi)));
+      bv = take ? (double)x[k] : bv;
+      bi = take ? col : bi;
+    }
+    block_best(bv, bi, s_v, s_i);
+    if (threadIdx.x == 0) {
+      p.tmax[slot] = (float)bv;
+      p.targ[slot] = bi == 0x7fffffff ? c0 : bi;
+    }
+    return;
+  }
+  float m, s;
+  block_max_sumexp(x, s_a, s_b, m, s);
+  if (threadIdx.x == 0) {
+    p.tmax[slot] = m;
+    p.tsum[slot] = s;
+  }
+  if constexpr (HAS_DRAFT) {
+    __syncthreads();
+    load_chunk<DDT>(p.draft, (int64_t)st * p.draft_stride0 + (int64_t)step * p.draft_stride1, c0,
+                    p.vocab, p.draft_aligned, x);
+#pragma unroll
+    for (int k = 0; k < kV2PerThread; ++k) x[k] = x[k] / temp;
+    block_max_sumexp(x, s_a, s_b, m, s);
+    if (threadIdx.x == 0) {
+      p.dmax[slot] = m;
+      p.dsum[slot] = s;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ pass 2 ------------
+
+// Log-sum-exp of a row from its chunk partials (every lane of the wave gets it).
+__device__ inline float wave_lse(const float* maxes, const float* sums, int64_t base, int n) {
+  float gm = -INFINITY;
+  for (int c = lane_id(); c < n; c += kWave) gm = fmaxf(gm, maxes[base + c]);
+  gm = wave_max(gm);
+  float s = 0.f;
+  for (int c = lane_id(); c < n; c += kWave) s += sums[base + c] * expf(maxes[base + c] - gm);
+  s = wave_sum(s);
+  return gm + logf(s);
+}
+
+template <int TDT, int DDT, bool HAS_DRAFT>
+__global__ __launch_bounds__(kThreads) void v2_chain_kernel(V2Params p) {
+  const int r = blockIdx.x * kWaves + wave_id();
+  if (r >= p.num_reqs) return;
+  const int64_t start = p.cu_num_logits[r], end = p.cu_num_logits[r + 1];
+  if (start < 0 || end > p.num_logits || end <= start || end - start - 1 > p.K) {
+    if (lane_id() == 0) p.acc[r] = -1;
+    return;
+  }
+  const int nd = (int)(end - start - 1);
+  const int st = clamp_state(p.idx_mapping[r], p.num_states);
+  const int64_t seed = p.seed[st];
+  const float temp = p.temperature[st];
+  const bool greedy = temp == 0.f;
+  using TS = typename Elem<TDT>::storage;
+  using DS = typename Elem<DDT>::storage;
+  const TS* tgt = reinterpret_cast<const TS*>(p.target);
+  int acc = 0;
+  bool verifying = true;
+  float t_lse = 0.f, d_lse = 0.f;
+  int64_t* out = p.sampled + (int64_t)r * p.sampled_stride;
+  for (int i = 0; i < nd; ++i) {
+    const int64_t li = start + i;
+    int d = p.draft_sampled[li + 1];
+    const bool valid = d >= 0 && d < p.vocab;
+    d = valid ? d : 0;
+    if (!greedy) verifying = verifying && valid;
+    if (!verifying) continue;
+    const float u = uniform_f32(randint4x64(seed, p.pos[li]).x);
+    const int64_t base = li * p.nchunks;
+    if (greedy) {
+      float bv = -INFINITY;
+      int bc = 0x7fffffff;
+      for (int c = lane_id(); c < p.nchunks; c += kWave) {
+        float v = p.tmax[base + c];
+        v = v != v ? -INFINITY : v;
+        argmax_update(bv, bc, v, c, true);
+      }
+      wave_argmax(bv, bc);
+      const int am = p.targ[base + (bc == 0x7fffffff ? 0 : bc)];
+      bool ok = p.rates ? (u < p.rates[i]) : (am == d);
+      ok = ok && valid;
+      verifying = ok;
+      acc += ok;
+      if (lane_id() == 0) out[i] = ok ? d : am;
+    } else {
+      t_lse = wave_lse(p.tmax, p.tsum, base, p.nchunks);
+      const float tlp = Elem<TDT>::cvt(tgt[li * p.target_stride + d]) - t_lse;
+      float dlp = 0.f;
+      d_lse = 0.f;
+      if constexpr (HAS_DRAFT) {
+        const DS* drf = reinterpret_cast<const DS*>(p.draft);
+        d_lse = wave_lse(p.dmax, p.dsum, base, p.nchunks);
+        const float dv =
+            Elem<DDT>::cvt(drf[(int64_t)st * p.draft_stride0 + (int64_t)i * p.draft_stride1 + d]);
+        dlp = dv / temp - d_lse;
+      }
+      const bool ok = p.rates ? (u < p.rates[i]) : (tlp > logf(u) + dlp);
+      verifying = ok;
+      acc += ok;
+      if (lane_id() == 0) out[i] = d;
+    }
+  }
+  if (lane_id() == 0) {
+    p.acc[r] = acc;
+    p.tlse[r] = t_lse;
+    p.dlse[r] = d_lse;
+  }
+}
+
+// ------------------------------------------------------------------ pass 3 ------------
+
+template <int TDT, int DDT, bool HAS_DRAFT>
+__global__ __launch_bounds__(kThreads) void v2_resample_kernel(V2Params p) {
+  __shared__ double s_v[kWaves];
+  __shared__ int s_i[kWaves];
+  const int r = blockIdx.x;
+  const int c = blockIdx.y;
+  const int acc = p.acc[r];
+  if (acc < 0) return;
+  const int64_t start = p.cu_num_logits[r], end = p.cu_num_logits[r + 1];
+  const int64_t ri = start + acc;
+  const bool is_bonus = ri == end - 1;
+  const int st = clamp_state(p.exp_idx_mapping[ri], p.num_states);
+  const float temp = p.temperature[st];
+  if (temp == 0.f && !is_bonus) return;
+  const int rej = is_bonus ? 0 : p.draft_sampled[ri + 1];
+  const bool rej_valid = rej >= 0 && rej < p.vocab;
+  const int c0 = c * kV2Chunk;
+  float x[kV2PerThread];
+  load_chunk<TDT>(p.target, ri * p.target_stride, c0, p.vocab, p.target_aligned, x);
+  constexpr int TV = Elem<TDT>::kVec;
+  if (!is_bonus && rej_valid) {
+    if constexpr (HAS_DRAFT) {
+      float q[kV2PerThread];
+      load_chunk<DDT>(p.draft, (int64_t)st * p.draft_stride0 + (int64_t)acc * p.draft_stride1, c0,
+                      p.vocab, p.draft_aligned, q);
+      const float tl = p.tlse[r], dlz = p.dlse[r];
+#pragma unroll
+      for (int k = 0; k < kV2PerThread; ++k) {
+        const float tlp = x[k] - tl;
+        const float dlp = q[k] / temp - dlz;
+        const float ratio = expf(dlp - tlp);
+        x[k] = ratio < 1.f ? tlp + log1pf(-ratio) : -INFINITY;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kV2PerThread; ++k)
+        x[k] = chunk_col(c0, k, TV) == rej ? -INFINITY : x[k];
+    }
+  }
+  double bv = -INFINITY;
+  int bi = 0x7fffffff;
+  uint32_t gseed = 0;
+  if (temp != 0.f) gseed = randint4x64(p.seed[st], p.pos[ri]).x;
+#pragma unroll
+  for (int k = 0; k < kV2PerThread; ++k) {
+    const int col = chunk_col(c0, k, TV);
+    if (col >= p.vocab) continue;
+    double sc;
+    if (temp == 0.f) {
+      sc = (double)x[k];
+    } else if (p.use_fp64) {
+      const U32x4 rn = randint4x32(gseed, col);
+      sc = (double)x[k] + (-log(-log(uniform_f64(rn.x, rn.y))));
+    } else {
+      const float uu = uniform_f32(randint4x32(gseed, col).x);
+      sc = (double)(x[k] + (-logf(-log1pf(-uu))));
+    }
+    const bool take = (sc > bv) | ((sc == bv) & (col < bi));
+    bv = take ? sc : bv;
+    bi = take ? col : bi;
+  }
+  block_best(bv, bi, s_v, s_i);
+  if (threadIdx.x == 0) {
+    const int64_t slot = (int64_t)r * p.nchunks + c;
+    p.rval[slot] = bv;
+    p.ridx[slot] = bi == 0x7fffffff ? c0 : bi;
+  }
+}
+
+// ------------------------------------------------------------------ pass 4 ------------
+
+__global__ __launch_bounds__(kThreads) void v2_insert_kernel(V2Params p) {
+  const int r = blockIdx.x * kWaves + wave_id();
+  if (r >= p.num_reqs) return;
+  const int acc = p.acc[r];
+  if (acc < 0) {
+    if (lane_id() == 0) p.num_sampled[r] = 0;
+    return;
+  }
+  const int64_t start = p.cu_num_logits[r], end = p.cu_num_logits[r + 1];
+  const int64_t ri = start + acc;
+  const bool is_bonus = ri == end - 1;
+  const int st = clamp_state(p.exp_idx_mapping[ri], p.num_states);
+  if (lane_id() == 0) p.num_sampled[r] = acc + 1;
+  if (p.temperature[st] == 0.f && !is_bonus) return;
+  const int64_t base = (int64_t)r * p.nchunks;
+  double bv = -INFINITY;
+  int bc = 0x7fffffff;
+  for (int c = lane_id(); c < p.nchunks; c += kWave) {
+    double v = p.rval[base + c];
+    v = v != v ? -INFINITY : v;
+    const bool take = (v > bv) | ((v == bv) & (c < bc));
+    bv = take ? v : bv;
+    bc = take ? c : bc;
+  }
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) {
+    const double ov = __shfl_xor(bv, off);
+    const int oc = __shfl_xor(bc, off);
+    const bool take = (ov > bv) | ((ov == bv) & (oc < bc));
+    bv = take ? ov : bv;
+    bc = take ? oc : bc;
+  }
+  if (lane_id() == 0) p.sampled[(int64_t)r * p.sampled_stride + acc] = p.ridx[base + (bc == 0x7fffffff ? 0 : bc)];
+}
+
+template <int TDT, int DDT, bool HAS_DRAFT>
+hipError_t launch_all(const V2Params& p, hipStream_t stream) {
+  if (p.num_logits > 0 && p.K > 0) {
+    hipLaunchKernelGGL((v2_stats_kernel<TDT, DDT, HAS_DRAFT>),
+                       dim3((unsigned)p.num_logits, p.nchunks), dim3(kThreads), 0, stream, p);
+  }
+  const unsigned wg = (unsigned)((p.num_reqs + kWaves - 1) / kWaves);
+  hipLaunchKernelGGL((v2_chain_kernel<TDT, DDT, HAS_DRAFT>), dim3(wg), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((v2_resample_kernel<TDT, DDT, HAS_DRAFT>),
+                     dim3((unsigned)p.num_reqs, p.nchunks), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL(v2_insert_kernel, dim3(wg), dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int TDT>
+hipError_t dispatch_draft(const V2Params& p, int draft_dtype, hipStream_t stream) {
+  if (!p.draft) return launch_all<TDT, MVSD_F32, false>(p, stream);
+  switch (draft_dtype) {
+    case MVSD_F32: return launch_all<TDT, MVSD_F32, true>(p, stream);
+    case MVSD_BF16: return launch_all<TDT, MVSD_BF16, true>(p, stream);
+    case MVSD_F16: return launch_all<TDT, MVSD_F16, true>(p, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+inline int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
+
+}  // namespace
+}  // namespace mvsd
+
+extern "C" {
+
+int64_t mvsd_v2_workspace_bytes(int64_t num_logits, int64_t num_reqs, int64_t vocab_size) {
+  if (num_logits < 0 || num_reqs < 0 || vocab_size <= 0) return -1;
+  const int64_t nch = (vocab_size + mvsd::kV2Chunk - 1) / mvsd::kV2Chunk;
+  const int64_t rows = num_logits * nch, reqs = num_reqs * nch;
+  return 5 * mvsd::align256(rows * 4) + 3 * mvsd::align256(num_reqs * 4) +
+         mvsd::align256(reqs * 8) + mvsd::align256(reqs * 4);
+}
+
+int mvsd_v2_rejection_sample(
+    int64_t* sampled, int64_t sampled_stride, int32_t* num_sampled, const void* target_logits,
+    int target_dtype, int64_t target_stride, int64_t num_logits, const void* draft_logits,
+    int draft_dtype, int64_t draft_stride0, int64_t draft_stride1, const int32_t* draft_sampled,
+    const int32_t* cu_num_logits, const int64_t* pos, const int32_t* idx_mapping,
+    const int32_t* expanded_idx_mapping, const int32_t* expanded_local_pos,
+    const float* temperature, const int64_t* seed, int64_t num_req_states, int64_t num_reqs,
+    int64_t vocab_size, int32_t num_speculative_steps, const float* synthetic_conditional_rates,
+    int use_fp64, void* workspace, int64_t workspace_bytes, mvsd_stream_t stream) {
+  using namespace mvsd;
+  if (num_reqs < 0 || num_logits < 0 || num_speculative_steps < 0) return MVSD_E_INVALID;
+  if (num_reqs == 0) return MVSD_OK;
+  if (!sampled || !num_sampled || !target_logits || !draft_sampled || !cu_num_logits || !pos ||
+      !idx_mapping || !expanded_idx_mapping || !expanded_local_pos || !temperature || !seed ||
+      !workspace)
+    return MVSD_E_INVALID;
+  if (vocab_size <= 0 || num_req_states <= 0 || sampled_stride < num_speculative_steps + 1 ||
+      target_stride < vocab_size)
+    return MVSD_E_INVALID;
+  if (target_dtype != MVSD_F32 && target_dtype != MVSD_BF16 && target_dtype != MVSD_F16)
+    return MVSD_E_INVALID;
+  if (draft_logits && draft_dtype != MVSD_F32 && draft_dtype != MVSD_BF16 && draft_dtype != MVSD_F16)
+    return MVSD_E_INVALID;
+  if (draft_logits && (draft_stride1 < vocab_size || draft_stride0 < draft_stride1 * num_speculative_steps))
+    return MVSD_E_INVALID;
+  if (vocab_size > 0x7fffffff - kV2Chunk || num_reqs > 0x7fffffff || num_req_states > 0x7fffffff ||
+      num_logits > 0x7fffffff || num_speculative_steps > 128)
+    return MVSD_E_RANGE;
+  const int64_t need = mvsd_v2_workspace_bytes(num_logits, num_reqs, vocab_size);
+  if (workspace_bytes < need || ((uintptr_t)workspace & 255) != 0) return MVSD_E_WORKSPACE;
+  const int nch = (int)((vocab_size + kV2Chunk - 1) / kV2Chunk);
+  if (nch > 65535 || (int64_t)nch * num_reqs > 0x7fffffff) return MVSD_E_RANGE;
+
+  V2Params p{};
+  p.sampled = sampled;
+  p.sampled_stride = sampled_stride;
+  p.num_sampled = num_sampled;
+  p.target = target_logits;
+  p.target_stride = target_stride;
+  p.draft = draft_logits;
+  p.draft_stride0 = draft_stride0;
+  p.draft_stride1 = draft_stride1;
+  p.draft_sampled = draft_sampled;
+  p.cu_num_logits = cu_num_logits;
+  p.pos = pos;
+  p.idx_mapping = idx_mapping;
+  p.exp_idx_mapping = expanded_idx_mapping;
+  p.exp_local_pos = expanded_local_pos;
+  p.temperature = temperature;
+  p.seed = seed;
+  p.rates = synthetic_conditional_rates;
+  p.num_logits = num_logits;
+  p.num_reqs = (int32_t)num_reqs;
+  p.num_states = (int32_t)num_req_states;
+  p.vocab = (int32_t)vocab_size;
+  p.K = num_speculative_steps;
+  p.nchunks = nch;
+  p.use_fp64 = use_fp64 != 0;
+  const int tsz = target_dtype == MVSD_F32 ? 4 : 2;
+  const int dsz = draft_dtype == MVSD_F32 ? 4 : 2;
+  p.target_aligned = ((uintptr_t)target_logits % 16 == 0) && ((target_stride * tsz) % 16 == 0);
+  p.draft_aligned = draft_logits && ((uintptr_t)draft_logits % 16 == 0) &&
+                    ((draft_stride0 * dsz) % 16 == 0) && ((draft_stride1 * dsz) % 16 == 0);
+  char* w = static_cast<char*>(workspace);
+  const int64_t rows = num_logits * nch, reqs = num_reqs * (int64_t)nch;
+  auto take = [&](int64_t bytes) {
+    char* q = w;
+    w += align256(bytes);
+    return q;
+  };
+  p.tmax = reinterpret_cast<float*>(take(rows * 4));
+  p.tsum = reinterpret_cast<float*>(take(rows * 4));
+  p.dmax = reinterpret_cast<float*>(take(rows * 4));
+  p.dsum = reinterpret_cast<float*>(take(rows * 4));
+  p.targ = reinterpret_cast<int32_t*>(take(rows * 4));
+  p.acc = reinterpret_cast<int32_t*>(take(num_reqs * 4));
+  p.tlse = reinterpret_cast<float*>(take(num_reqs * 4));
+  p.dlse = reinterpret_cast<float*>(take(num_reqs * 4));
+  p.rval = reinterpret_cast<double*>(take(reqs * 8));
+  p.ridx = reinterpret_cast<int32_t*>(take(reqs * 4));
+
+  hipError_t err = hipErrorInvalidValue;
+  switch (target_dtype) {
+    case MVSD_F32: err = dispatch_draft<MVSD_F32>(p, draft_dtype, (hipStream_t)stream); break;
+    case MVSD_BF16: err = dispatch_draft<MVSD_BF16>(p, draft_dtype, (hipStream_t)stream); break;
+    case MVSD_F16: err = dispatch_draft<MVSD_F16>(p, draft_dtype, (hipStream_t)stream); break;
+  }
+  return record_hip_error(err);
+}
+
+}  // extern "C"

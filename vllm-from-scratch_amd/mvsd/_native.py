@@ -102,6 +102,12 @@ SIGNATURES = {
                                    c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int,
                                    c_int64, c_int32, c_int32, c_int32, c_int, c_int64,
                                    c_void_p]),
+    "mvsd_v2_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
+    "mvsd_v2_rejection_sample": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int, c_int64,
+                                         c_int64, c_void_p, c_int, c_int64, c_int64, c_void_p,
+                                         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                         c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int32,
+                                         c_void_p, c_int, c_void_p, c_int64, c_void_p]),
     "mvsd_ngram_valid_sampled": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
                                          c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                          c_void_p, c_int64, c_int64, c_void_p]),
