@@ -1,6 +1,6 @@
 """Benchmark of the speculative-decoding verification path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config h|c1|c2|c3|c4|c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config h|c1|c2|c3|c4|c5|v2]
 
 A step is one ``rejection_sample`` call (the persistent verify kernel; with top-k / top-p the
 constraints kernel before it) over the whole batch, inputs already resident in HBM; the
@@ -42,7 +42,7 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="h", choices=["h", "c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="h", choices=["h", "c1", "c2", "c3", "c4", "c5", "v2"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="minimum CPU time of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -218,6 +218,99 @@ def bench_ngram(args, device):
     print(json.dumps(line))
 
 
+def bench_v2(args, device):
+    """The V2 runner's verification (mvsd.worker.gpu.spec_decode.rejection_sample) on the
+    headline shape: B=256, k=4, V=151936 fp32, all random at T=0.8, draft logits
+    [B, k, V] pre-temperature, target = draft + N(0, 0.5^2) (already scaled), drafts sampled
+    from softmax(draft / T), 1280 target rows (each request's 4 verify rows and its bonus
+    row).  Algorithmic bytes = verify rows of target and draft once + the bonus rows that are
+    resampled + the index arrays and outputs."""
+    from mvsd.worker.gpu.spec_decode import rejection_sample
+    from oracle import v2_rejection as ov2
+
+    B, K, V, T = 256, 4, 151936, 0.8
+    g = torch.Generator(device=device).manual_seed(2002)
+    draft = torch.randn(B, K, V, generator=g, device=device) * 2.0
+    rows = B * (K + 1)
+    target = torch.empty(rows, V, device=device)
+    tv = target.view(B, K + 1, V)
+    tv[:, :K] = draft + 0.5 * torch.randn(B, K, V, generator=g, device=device)
+    tv[:, K] = torch.randn(B, V, generator=g, device=device) * 2.0
+    probs = torch.softmax(draft.view(B * K, V) / T, -1)
+    ids = torch.multinomial(probs, 1, generator=g).view(B, K).to(torch.int32)
+    del probs
+    ds = torch.zeros(B, K + 1, dtype=torch.int32, device=device)
+    ds[:, 1:] = ids
+    ar = torch.arange(B, dtype=torch.int32, device=device)
+    case = dict(target_logits=target, draft_logits=draft, draft_sampled=ds.view(-1),
+                cu_num_logits=torch.arange(0, rows + 1, K + 1, dtype=torch.int32, device=device),
+                pos=torch.arange(rows, dtype=torch.int64, device=device) + 4096,
+                idx_mapping=ar, expanded_idx_mapping=ar.repeat_interleave(K + 1),
+                expanded_local_pos=torch.arange(K + 1, dtype=torch.int32,
+                                                device=device).repeat(B),
+                temperature=torch.full((B,), T, device=device),
+                seed=torch.randint(0, 2**62, (B,), generator=g, device=device),
+                num_speculative_steps=K)
+    torch.cuda.synchronize()
+
+    def step():
+        return rejection_sample(**case)
+
+    ms, launch_ms, wall_ms, (s, n) = time_steps(step, args.steps, args.warmup)
+    n_host = n.cpu().numpy()
+    n_bonus = int((n_host == K + 1).sum())
+    P = B * K
+    nbytes = 2 * P * V * 4 + n_bonus * V * 4 + rows * (4 + 8 + 4 + 4) + B * (4 + 4 + 4 + 8) \
+        + B * (K + 1) * 8 + B * 4
+    hist = np.bincount(n_host - 1, minlength=K + 1).tolist()
+    gbs = nbytes / (ms / 1e3) / 1e9
+    kernel_gbs = nbytes / (launch_ms / 1e3) / 1e9
+    line = {"metric": "V2 rejection-sampler HBM GB/s (% of peak) + verified tok/s, B=256 k=4 V=152k",
+            "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (seeded torch generator on device; no checkpoint)",
+            "config": {"workload": "v2 B=256 k=4 V=151936 fp32 random T=0.8, draft logits",
+                       "batch_size": B, "num_logits": rows, "vocab_size": V,
+                       "algorithmic_bytes": nbytes},
+            "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+            "verified_tok_per_s": round(float(n_host.sum()) / (ms / 1e3), 1),
+            "accept_length_hist": hist, "wall_ms_per_step": round(wall_ms, 5),
+            "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+                         "traffic": None,
+                         "kernel": "v2_stats + v2_chain + v2_resample + v2_insert per call",
+                         "kernel_ms": round(launch_ms, 5)},
+            "cpu_baseline": None}
+    if not args.no_cpu_baseline:
+        sub = 16  # requests in the CPU sample
+        host = {k: (v.cpu().numpy() if isinstance(v, torch.Tensor) else v)
+                for k, v in case.items()}
+        r_rows = sub * (K + 1)
+        host["target_logits"] = host["target_logits"][:r_rows]
+        for k in ("draft_sampled", "pos", "expanded_idx_mapping", "expanded_local_pos"):
+            host[k] = host[k][:r_rows]
+        host["cu_num_logits"] = host["cu_num_logits"][:sub + 1]
+        host["idx_mapping"] = host["idx_mapping"][:sub]
+        t0 = time.perf_counter()
+        runs = 0
+        while True:
+            es, en = ov2.rejection_sample(**host)
+            runs += 1
+            if time.perf_counter() - t0 >= min(args.cpu_seconds, 10.0):
+                break
+        cpu_s = (time.perf_counter() - t0) / runs
+        ok = bool((en == n_host[:sub]).all())
+        sub_bytes = nbytes * sub / B
+        line["cpu_baseline"] = {"value": round(sub_bytes / cpu_s / 1e9, 4), "unit": "GB/s",
+                                "cores": 1, "kind": "port",
+                                "sample": f"first {sub} of {B} requests through "
+                                f"oracle/v2_rejection.py (numpy), {runs} runs; "
+                                f"num_sampled equal to the GPU's: {ok}",
+                                "seconds": round(cpu_s * runs, 2)}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -227,6 +320,9 @@ def main():
     device = torch.device("cuda", 0)
     if args.config == "c3":
         bench_ngram(args, device)
+        return
+    if args.config == "v2":
+        bench_v2(args, device)
         return
     from mvsd.sample.rejection_sampler import RejectionSampler
     from mvsd.testing import configs

@@ -47,8 +47,10 @@ __device__ inline U32x4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uin
                                       uint32_t k0, uint32_t k1) {
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
-    const uint32_t h0 = __umulhi(0xCD9E8D57u, c2), l0 = 0xCD9E8D57u * c2;
-    const uint32_t h2 = __umulhi(0xD2511F53u, c0), l2 = 0xD2511F53u * c0;
+    // One 32x32->64 multiply per product (v_mad_u64_u32) instead of separate lo and hi.
+    const uint64_t p0 = (uint64_t)0xCD9E8D57u * c2, p2 = (uint64_t)0xD2511F53u * c0;
+    const uint32_t h0 = (uint32_t)(p0 >> 32), l0 = (uint32_t)p0;
+    const uint32_t h2 = (uint32_t)(p2 >> 32), l2 = (uint32_t)p2;
     c0 = h0 ^ c1 ^ k0;
     c2 = h2 ^ c3 ^ k1;
     c1 = l0;
