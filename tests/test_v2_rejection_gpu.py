@@ -118,3 +118,41 @@ def test_no_host_synchronisation():
     finally:
         torch.cuda.set_sync_debug_mode(0)
     torch.cuda.synchronize()
+
+
+def test_int64_index_tensors():
+    """The dtypes the reference's V2 test passes (tests/step73/test_v2_rejection_diff.py:96-98):
+    int64 idx_mapping, expanded_idx_mapping, cu_num_logits and draft_sampled.  Every converted
+    index array must stay allocated until the launch, or two of them share one block."""
+    temps = [0.8, 1.0, 0.0, 1.3, 0.5, 0.9, 1.1, 0.7]
+    case = make_case([4, 4, 4, 2, 4, 3, 4, 4], temps, 4, V, seed=31, states=12)
+    for key in ("idx_mapping", "expanded_idx_mapping", "cu_num_logits", "draft_sampled",
+                "expanded_local_pos"):
+        case[key] = case[key].to(torch.int64)
+    _compare(case, "int64 index tensors")
+
+
+@pytest.mark.parametrize("name", ["draft_sampled", "cu_num_logits", "pos", "idx_mapping",
+                                  "expanded_idx_mapping", "expanded_local_pos", "temperature",
+                                  "seed", "draft_logits", "synthetic_conditional_rates"])
+def test_host_argument_is_refused_before_launch(name):
+    """A host tensor for any argument raises before anything is enqueued (the kernels would
+    otherwise dereference a host address)."""
+    from mvsd.worker.gpu.spec_decode import rejection_sample
+    case = make_case([2, 2], [0.8, 0.0], 2, 1024, seed=3)
+    dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
+    kw = {}
+    if name == "synthetic_conditional_rates":
+        kw[name] = torch.tensor([0.9, 0.5])  # host
+    else:
+        dev[name] = case[name]  # host copy
+    with pytest.raises(NotImplementedError, match="device tensors"):
+        rejection_sample(**dev, **kw)
+
+
+def test_short_synthetic_rates_are_refused():
+    from mvsd.worker.gpu.spec_decode import rejection_sample
+    case = make_case([3, 3], [0.8, 0.0], 3, 1024, seed=3)
+    dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
+    with pytest.raises(ValueError, match="synthetic_conditional_rates"):
+        rejection_sample(**dev, synthetic_conditional_rates=torch.tensor([0.9, 0.5]).cuda())

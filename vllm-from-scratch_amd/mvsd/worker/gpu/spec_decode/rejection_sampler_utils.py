@@ -31,8 +31,22 @@ from ...._native import (F32, check, dtype_code, lib, ptr, require_device_tensor
 _FLOAT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
-def _as(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    return t if t.dtype == dtype and t.is_contiguous() else t.to(dtype).contiguous()
+def _on_device(t: torch.Tensor, name: str, device: torch.device) -> None:
+    """Refuse a tensor the kernels cannot address: host memory, or another device."""
+    require_device_tensor(t, name)
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device} but target_logits is on {device}")
+
+
+def _as(t: torch.Tensor, dtype: torch.dtype, keep: list) -> torch.Tensor:
+    """``t`` as a contiguous ``dtype`` tensor; a converted copy is appended to ``keep`` so that
+    it stays allocated until the launch has been enqueued (a temporary freed before the
+    launch could hand its memory to the next conversion on the same stream)."""
+    if t.dtype == dtype and t.is_contiguous():
+        return t
+    out = t.to(dtype).contiguous()
+    keep.append(out)
+    return out
 
 
 def rejection_sample(
@@ -64,12 +78,23 @@ def rejection_sample(
     if target_logits.dtype not in _FLOAT_DTYPES:
         raise TypeError(f"target_logits dtype {target_logits.dtype} is not supported")
     device = target_logits.device
+    # Every tensor the kernels read or write must live on the target's device: a host tensor
+    # would hand the kernels a host address (the reference's Triton kernels refuse them too).
+    named = [("draft_sampled", draft_sampled), ("cu_num_logits", cu_num_logits), ("pos", pos),
+             ("idx_mapping", idx_mapping), ("expanded_idx_mapping", expanded_idx_mapping),
+             ("expanded_local_pos", expanded_local_pos), ("temperature", temperature),
+             ("seed", seed)]
+    if draft_logits is not None:
+        named.append(("draft_logits", draft_logits))
+    if synthetic_conditional_rates is not None:
+        named.append(("synthetic_conditional_rates", synthetic_conditional_rates))
+    for name, t in named:
+        _on_device(t, name, device)
     num_reqs = cu_num_logits.shape[0] - 1
     num_logits, vocab_size = target_logits.shape
     d_stride0 = d_stride1 = 0
     d_code = F32
     if draft_logits is not None:
-        require_device_tensor(draft_logits, "draft_logits")
         if draft_logits.dtype not in _FLOAT_DTYPES:
             raise TypeError(f"draft_logits dtype {draft_logits.dtype} is not supported")
         d_stride0, d_stride1 = draft_logits.stride(0), draft_logits.stride(1)
@@ -81,6 +106,36 @@ def rejection_sample(
     num_sampled = sampled.new_empty(num_reqs, dtype=torch.int32)
     if num_reqs == 0:
         return sampled, num_sampled
+    keep: list[torch.Tensor] = []
+    rates = None
+    if synthetic_conditional_rates is not None:
+        rates = _as(synthetic_conditional_rates, torch.float32, keep)
+        if rates.numel() < K:
+            raise ValueError(f"synthetic_conditional_rates has {rates.numel()} entries but "
+                             f"num_speculative_steps is {K}")
+    temp = _as(temperature, torch.float32, keep)
+    seeds = _as(seed, torch.int64, keep)
+    num_states = min(temp.numel(), seeds.numel())
+    if draft_logits is not None:
+        num_states = min(num_states, draft_logits.shape[0])
+    sampled_i32 = _as(draft_sampled, torch.int32, keep)
+    cu = _as(cu_num_logits, torch.int32, keep)
+    pos64 = _as(pos, torch.int64, keep)
+    idx = _as(idx_mapping, torch.int32, keep)
+    eidx = _as(expanded_idx_mapping, torch.int32, keep)
+    elpos = _as(expanded_local_pos, torch.int32, keep)
+    ws_bytes = lib().mvsd_v2_workspace_bytes(num_logits, num_reqs, vocab_size)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    check(lib().mvsd_v2_rejection_sample(
+        sampled.data_ptr(), sampled.stride(0), num_sampled.data_ptr(),
+        target_logits.data_ptr(), dtype_code(target_logits.dtype), target_logits.stride(0),
+        num_logits, ptr(draft_logits), d_code, d_stride0, d_stride1, sampled_i32.data_ptr(),
+        cu.data_ptr(), pos64.data_ptr(), idx.data_ptr(), eidx.data_ptr(), elpos.data_ptr(),
+        temp.data_ptr(), seeds.data_ptr(), num_states, num_reqs, vocab_size, K, ptr(rates),
+        int(bool(use_fp64)), workspace.data_ptr(), workspace.numel(), stream_of(device)),
+        "mvsd_v2_rejection_sample")
+    del keep  # the launch is enqueued; stream-ordered frees are safe from here on
+    return sampled, num_sampled
     rates = None
     if synthetic_conditional_rates is not None:
         rates = _as(synthetic_conditional_rates, torch.float32)
