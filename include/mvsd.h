@@ -70,7 +70,8 @@ int mvsd_expand_batch_to_tokens(void* out, const void* x, int dtype,
                                 mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
-/* rejection_sample — fused verification of a whole batch in one persistent launch.      */
+/* rejection_sample — fused verification of a whole batch, one persistent launch per 4096  */
+/* requests.                                                                              */
 /* Replaces: rejection_sample (minivllm/sample/rejection_sampler.py:414-534) together    */
 /* with what it launches: target softmax (:502), target argmax (:485),                   */
 /* rejection_greedy_sample_kernel (:678-740), sample_recovered_tokens + its kernel       */
@@ -138,16 +139,28 @@ typedef struct mvsd_rejection_args {
 } mvsd_rejection_args;
 
 /* Workspace contract: zero-filled before its first use (mvsd_rejection_workspace_init, or
- * any zeroed allocation); every call leaves it zero-filled again except for the int at
- * byte offset 4, a sticky flag that becomes non-zero if a wait inside the kernel ever hit
- * its spin bound (results of that call are then unreliable).  One workspace must not be used by two
- * calls that can run concurrently (different streams).  Sizes: the query below is monotone
- * in every argument, so a workspace sized for the largest batch serves smaller ones. */
+ * any zeroed allocation); every call leaves it zero-filled again, also after a failed call.
+ * One workspace must not be used by two calls that can run concurrently (different streams).
+ * Sizes: the query below is monotone in every argument, so a workspace sized for the largest
+ * batch serves smaller ones.
+ *
+ * Failure: the kernel's cross-workgroup waits are bounded (about 0.3 s of polling, see
+ * mvsd_set_wait_limit).  When a wait gives up, every output entry of the requests whose
+ * inputs were incomplete is set to MVSD_POISON (INT32_MIN, never a token id), and the
+ * workspace is still returned to zero, so the next call is unaffected.  The caller detects
+ * the failure on its existing device-to-host copy of the output (the reference's
+ * parse_output, rejection_sampler.py:320); the Python layer raises RuntimeError there. */
+#define MVSD_POISON ((int32_t)0x80000000)
 int64_t mvsd_rejection_workspace_bytes(int64_t batch_size, int64_t num_tokens,
                                        int64_t vocab_size, int target_dtype,
                                        int64_t max_spec_len);
 /* Zero-fill a workspace on `stream` with a kernel (no hipMemsetAsync). */
 int mvsd_rejection_workspace_init(void* workspace, int64_t workspace_bytes, mvsd_stream_t stream);
+/* Polls after which a wait inside mvsd_rejection_sample gives up, for calls made from now on
+ * (process-wide; polls < 0 restores the default, 0 makes every wait give up at once so that
+ * tests can exercise the failure path while every kernel still exits normally).  Returns the
+ * previous limit.  No counterpart in the reference. */
+int mvsd_set_wait_limit(int polls);
 int mvsd_rejection_sample(const mvsd_rejection_args* args, mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */

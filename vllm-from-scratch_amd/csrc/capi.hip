@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "mvsd_device.h"
@@ -45,26 +46,26 @@ int elem_size(int dtype) {
 
 constexpr int kMaxDevices = 64;
 
-// Resident-workgroup capacity of a verify kernel per device, dtype and kernel kind
-// (CUs x occupancy).
-int verify_capacity(int device, int dtype, int mode, bool has_draft, bool masked) {
+// Polls before a verify-kernel wait gives up (mvsd_set_wait_limit).
+std::atomic<int> g_wait_limit{mvsd::kSpinLimitDefault};
+
+// Resident-workgroup capacity of the verify kernel variant per device (CUs x occupancy).
+int verify_capacity(int device, int dtype, bool has_draft, bool masked) {
   static std::mutex mu;
-  static int cache[kMaxDevices][3][mvsd::kModes][4];
-  if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2 || mode < 0 ||
-      mode >= mvsd::kModes)
-    return 0;
+  static int cache[kMaxDevices][3][4];
+  if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2) return 0;
   std::lock_guard<std::mutex> lock(mu);
-  int& slot = cache[device][dtype][mode][(masked ? 2 : 0) + (has_draft ? 1 : 0)];
+  int& slot = cache[device][dtype][(masked ? 2 : 0) + (has_draft ? 1 : 0)];
   if (slot > 0) return slot;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     return 0;
-  const void* fn = mvsd::verify_kernel_ptr(dtype, mode, has_draft, masked);
+  const void* fn = mvsd::verify_kernel_ptr(dtype, has_draft, masked);
   if (!fn) return 0;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, mvsd::kVThreads, 0) != hipSuccess)
     return 0;
-  // The persistent kernels rely on every launched workgroup being resident, so the runtime's
+  // The persistent kernel relies on every launched workgroup being resident, so the runtime's
   // figure is capped by an LDS estimate with a coarse (2 KiB) allocation granularity.
   hipFuncAttributes attr;
   int lds_cu = 0;
@@ -84,34 +85,36 @@ int verify_capacity(int device, int dtype, int mode, bool has_draft, bool masked
 
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
-// Workspace layout.  ctrl = {ticket, sticky spin-limit flag (byte offset 4), exit counter}.
+// Workspace layout of the verify kernel for launches of at most Bl requests over P verify
+// rows with at most nc chunks per row.  ctrl = {ticket, wait-failure flag, exit counter}.
 struct WorkspaceLayout {
-  int64_t ctrl, grp_off, grp_desc, req_cnt, queues, qgi, masks, stat_slots, arg_slots, total;
+  int64_t ctrl, req_cnt, score_cnt, decision, masks, stat_slots, score_slots, total;
 };
 
-WorkspaceLayout verify_layout(int64_t B, int64_t P, int64_t nc) {
+WorkspaceLayout verify_layout(int64_t Bl, int64_t P, int64_t nc) {
   WorkspaceLayout l;
   int64_t off = 0;
+  const int64_t b = Bl > 0 ? Bl : 1, rows = P > 0 ? P : 1;
   l.ctrl = off;
   off = align_up(off + 3 * 4, 256);
-  l.grp_off = off;
-  off = align_up(off + (B + 1) * 4, 256);
-  l.grp_desc = off;
-  off = align_up(off + (P > 0 ? P : 1) * 16, 256);
   l.req_cnt = off;
-  off = align_up(off + (B > 0 ? B : 1) * 4, 256);
-  l.queues = off;  // qticket, qcount, qoff: kMaxQueues ints each
-  off = align_up(off + 3 * mvsd::kMaxQueues * 4, 256);
-  l.qgi = off;
-  off = align_up(off + (P > 0 ? P : 1) * 4, 256);
+  off = align_up(off + b * 4, 256);
+  l.score_cnt = off;
+  off = align_up(off + b * 4, 256);
+  l.decision = off;
+  off = align_up(off + b * 4, 256);
   l.masks = off;  // row masks of the sampling constraints (zeroed again by the verify kernel)
-  off = align_up(off + (P > 0 ? P : 1) * 16, 256);
+  off = align_up(off + rows * 16, 256);
   l.stat_slots = off;
-  off = align_up(off + P * nc * 8, 256);
-  l.arg_slots = off;
-  off = align_up(off + P * nc * 8, 256);
+  off = align_up(off + rows * nc * 8, 256);
+  l.score_slots = off;
+  off = align_up(off + b * nc * 8, 256);
   l.total = off;
   return l;
+}
+
+int64_t launch_requests(int64_t B) {
+  return B < mvsd::kMaxLaunchRequests ? B : mvsd::kMaxLaunchRequests;
 }
 
 }  // namespace
@@ -156,8 +159,14 @@ int64_t mvsd_rejection_workspace_bytes(int64_t batch_size, int64_t num_tokens, i
                                        int target_dtype, int64_t max_spec_len) {
   (void)max_spec_len;
   if (batch_size < 0 || num_tokens < 0 || vocab_size <= 0) return -1;
-  const mvsd::VerifyPlan plan = mvsd::verify_plan(target_dtype, vocab_size, 0, 1, 0);
-  return verify_layout(batch_size, num_tokens, plan.nsub).total;
+  const mvsd::VerifyPlan plan = mvsd::verify_plan(target_dtype, vocab_size, 0, 0);
+  return verify_layout(launch_requests(batch_size), num_tokens, plan.nc_max).total;
+}
+
+int mvsd_set_wait_limit(int polls) {
+  const int prev = g_wait_limit.load();
+  g_wait_limit.store(polls < 0 ? mvsd::kSpinLimitDefault : polls);
+  return prev;
 }
 
 int mvsd_rejection_workspace_init(void* workspace, int64_t workspace_bytes, mvsd_stream_t stream) {
@@ -188,79 +197,22 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   const bool need_noise = !a->all_greedy && !a->recovered_token_ids;
   if (P > 0 && need_noise && (!a->exp_noise || a->noise_stride < V)) return MVSD_E_INVALID;
 
-  // Slot arrays are sized for the most chunks any plan can use (nsub), so the layout does not
-  // depend on the device.
-  const mvsd::VerifyPlan size_plan = mvsd::verify_plan(a->target_dtype, V, 0, 1, 0);
-  const WorkspaceLayout lay = verify_layout(B, P, size_plan.nsub);
+  // Slot arrays are sized for the most chunks any plan can use, so the layout does not depend
+  // on the device.
+  const mvsd::VerifyPlan size_plan = mvsd::verify_plan(a->target_dtype, V, 0, 0);
+  const WorkspaceLayout lay = verify_layout(launch_requests(B), P, size_plan.nc_max);
   if (!a->workspace || a->workspace_bytes < lay.total) return MVSD_E_WORKSPACE;
   if ((uintptr_t)a->workspace % 256 != 0) return MVSD_E_ALIGN;
 
-  // Kernel choice: the split kernel (stats tasks, then score tasks that re-read the target
-  // chunk) by default.  MVSD_VERIFY_MODE=fused selects the single-read kernel when its
-  // requirements hold: 16-byte loads (below), the request metadata in LDS
-  // (B <= kMaxFusedRequests) and at most fused_max_chunks() sub-chunks per row.
-  // MVSD_VERIFY_MODE=resident selects the register-resident kernel when its requirements
-  // hold: 16-byte loads, B <= kMaxLdsRequests, and at least half as many resident workgroups
-  // as chunks per row (its progress argument).  MVSD_VERIFY_MODE=lds selects the parked
-  // kernel when B <= lds_max_requests() and more workgroups are resident than chunks per row.
-  const int two_phase = (!a->all_greedy && !a->recovered_token_ids) ? 1 : 0;
+  // Random requests with in-kernel recovered ids get score units (one per request).
+  const bool scores = !a->all_greedy && !a->recovered_token_ids;
   // Sampling constraints apply only when some request samples (rejection_sampler.py:549-550).
   const bool masked = !a->all_greedy && (a->top_k || a->top_p);
-  int cap = 0;
-  int kmode = mvsd::kModeSplit;
-  if (P > 0) {
-    int device = 0;
-    hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess) return hip_status(err);
-    // The fused kernel issues unconditional 16-byte loads: rows must be 16-byte aligned and
-    // V a multiple of the vector width.
-    const int esz = elem_size(a->target_dtype);
-    const bool vec_ok = aligned16(a->target_logits, a->target_stride * esz) &&
-                        aligned16(a->exp_noise, a->noise_stride * 4) &&
-                        (!a->draft_probs || aligned16(a->draft_probs, a->draft_stride * 4)) &&
-                        V % (16 / esz) == 0;
-    const char* mode = getenv("MVSD_VERIFY_MODE");
-    if (vec_ok && B <= mvsd::kMaxFusedRequests && size_plan.nsub <= mvsd::fused_max_chunks() &&
-        mode && strcmp(mode, "fused") == 0) {
-      const int fcap = verify_capacity(device, a->target_dtype, mvsd::kModeFused,
-                                       a->draft_probs != nullptr, masked);
-      if (fcap > 0) {
-        kmode = mvsd::kModeFused;
-        cap = fcap;
-      }
-    }
-    if (vec_ok && B <= mvsd::kMaxLdsRequests && mode && strcmp(mode, "resident") == 0) {
-      const int rcap = verify_capacity(device, a->target_dtype, mvsd::kModeResident,
-                                       a->draft_probs != nullptr, masked);
-      const mvsd::VerifyPlan rplan = mvsd::verify_resident_plan(a->target_dtype, V);
-      if (rcap > 0 && rplan.nc <= size_plan.nsub && rplan.nc <= 2 * rcap) {
-        kmode = mvsd::kModeResident;
-        cap = rcap;
-      }
-    }
-    if (B <= mvsd::lds_max_requests() && mode && strcmp(mode, "lds") == 0) {
-      const int lcap = verify_capacity(device, a->target_dtype, mvsd::kModeLds,
-                                       a->draft_probs != nullptr, masked);
-      const mvsd::VerifyPlan lplan = mvsd::verify_lds_plan(a->target_dtype, V);
-      if (lcap > 0 && lplan.nc <= size_plan.nsub && lplan.nc < lcap) {
-        kmode = mvsd::kModeLds;
-        cap = lcap;
-      }
-    }
-    if (kmode == mvsd::kModeSplit)
-      cap = verify_capacity(device, a->target_dtype, kmode, a->draft_probs != nullptr, masked);
-    if (cap <= 0) return hip_status(hipErrorInvalidDevice);
-  }
-  // Upper bound on groups: min(P, B * ceil(max_spec_len / G)).
-  int64_t groups = B * ((a->max_spec_len + size_plan.g - 1) / size_plan.g);
-  if (groups > P) groups = P;
-  mvsd::VerifyPlan plan = size_plan;
-  if (kmode == mvsd::kModeSplit)
-    plan = mvsd::verify_plan(a->target_dtype, V, groups > 0 ? groups : 1, two_phase ? 2 : 1, cap);
-  else if (kmode == mvsd::kModeResident)
-    plan = mvsd::verify_resident_plan(a->target_dtype, V);
-  else if (kmode == mvsd::kModeLds)
-    plan = mvsd::verify_lds_plan(a->target_dtype, V);
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_status(err);
+  const int cap = verify_capacity(device, a->target_dtype, a->draft_probs != nullptr, masked);
+  if (cap <= 0) return hip_status(hipErrorInvalidDevice);
 
   char* ws = static_cast<char*>(a->workspace);
   mvsd::VerifyParams p;
@@ -289,79 +241,62 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   p.P = (int)P;
   p.V = (int)V;
   p.max_spec_len = (int)a->max_spec_len;
-  p.chunk = plan.chunk;
-  p.nc = plan.nc;
-  p.split = 0;
-  p.arg_stride = plan.nc;
-  p.G = plan.g;
+  p.G = size_plan.g;
+  p.spin_limit = g_wait_limit.load();
   const int esz = elem_size(a->target_dtype);
   p.target_aligned = aligned16(a->target_logits, a->target_stride * esz);
   p.draft_aligned = a->draft_probs ? aligned16(a->draft_probs, a->draft_stride * 4) : false;
   p.noise_aligned = a->exp_noise ? aligned16(a->exp_noise, a->noise_stride * 4) : false;
   p.ctrl = reinterpret_cast<int*>(ws + lay.ctrl);
-  p.grp_off = reinterpret_cast<int*>(ws + lay.grp_off);
-  p.grp_desc = reinterpret_cast<int4*>(ws + lay.grp_desc);
   p.req_cnt = reinterpret_cast<int*>(ws + lay.req_cnt);
-  p.qticket = reinterpret_cast<int*>(ws + lay.queues);
-  p.qcount = p.qticket + mvsd::kMaxQueues;
-  p.qoff = p.qcount + mvsd::kMaxQueues;
-  p.qgi = reinterpret_cast<int*>(ws + lay.qgi);
-  // Work queues (MVSD_VERIFY_QUEUES, 1..16; one per XCD gives each queue one L2).  One queue
-  // measured fastest at the headline: the re-read is served by the Infinity Cache anyway.
-  int nq = 1;
-  if (const char* env = getenv("MVSD_VERIFY_QUEUES")) nq = atoi(env);
-  p.nq = nq < 1 ? 1 : (nq > mvsd::kMaxQueues ? mvsd::kMaxQueues : nq);
-  // Without the init kernel (group offsets built in each workgroup's LDS) when one queue
-  // serves the batch and its requests fit (MVSD_VERIFY_LDS_GROUPS=0 keeps the init kernel).
-  p.lds_groups = kmode == mvsd::kModeSplit && p.nq == 1 && B <= mvsd::kMaxLdsRequests && P > 0;
-  if (const char* env = getenv("MVSD_VERIFY_LDS_GROUPS")) p.lds_groups = p.lds_groups && atoi(env) != 0;
-  if (kmode != mvsd::kModeSplit) {
-    p.nq = 1;  // one ticket; the group offsets always in LDS
-    p.lds_groups = 1;
-  }
+  p.score_cnt = reinterpret_cast<int*>(ws + lay.score_cnt);
+  p.decision = reinterpret_cast<int*>(ws + lay.decision);
   p.top_k = masked ? a->top_k : nullptr;
   p.top_p = masked ? a->top_p : nullptr;
   p.masks = masked ? reinterpret_cast<float4*>(ws + lay.masks) : nullptr;
   p.stat_slots = reinterpret_cast<uint64_t*>(ws + lay.stat_slots);
-  p.arg_slots = reinterpret_cast<uint64_t*>(ws + lay.arg_slots);
+  p.score_slots = reinterpret_cast<uint64_t*>(ws + lay.score_slots);
 
-  int grid = 0;
-  if (P > 0) {
-    int64_t tasks;
-    if (kmode != mvsd::kModeSplit) {
-      tasks = groups * plan.nc;
-      grid = (int)(tasks < cap ? tasks : cap);
-    } else {
-      // Each queue is served by grid / nq workgroups.  A group's score chunks are claimed
-      // `lag` groups after its stats chunks: enough for that queue's workgroups (each holding
-      // a current and a prefetched ticket) to have finished the stats, and as few as possible
-      // so that the score tasks re-read the target chunk while it is still cached (L2 or the
-      // Infinity Cache).
-      p.two_phase = two_phase;
-      grid = cap / p.nq * p.nq;
-      if (grid < p.nq) grid = p.nq;
-      const int per_queue = grid / p.nq;
-      int lag = (2 * per_queue + 2 * plan.nc - 1) / (2 * plan.nc) + 1;
-      if (const char* env = getenv("MVSD_VERIFY_LAG")) lag = atoi(env);
-      p.lag = lag < 1 ? 1 : (lag > 4096 ? 4096 : lag);
-      const int64_t step = p.two_phase ? 2 * plan.nc : plan.nc;
-      // Epilogue split (one queue): the score tasks of the last `lag` groups use the empty
-      // stats slots of their steps as a second half-chunk task each (MVSD_VERIFY_SPLIT=0
-      // turns it off).  MVSD_VERIFY_QUARTER=n runs the score tasks of the last n groups in
-      // quarter chunks instead (off by default: no gain measured on MI355X, the end of the
-      // launch is set by the last requests' finalisation rather than by the task length).
-      p.split = p.two_phase && p.nq == 1 && 2 * plan.nc <= size_plan.nsub ? 1 : 0;
-      if (const char* env = getenv("MVSD_VERIFY_SPLIT")) p.split = p.split && atoi(env) != 0;
-      int quarter = 0;
-      if (const char* env = getenv("MVSD_VERIFY_QUARTER")) quarter = atoi(env);
-      p.quarter = p.split && 4 * plan.nc <= size_plan.nsub ? (quarter < 0 ? 0 : (quarter > p.lag ? p.lag : quarter)) : 0;
-      if (p.split) p.arg_stride = (p.quarter > 0 ? 4 : 2) * plan.nc;
-      tasks = (groups + (p.two_phase ? p.lag * p.nq : 0) + p.quarter) * step;
-    }
-    // every workgroup may claim up to three tickets past the last task
-    if (tasks > 0x7fffffff - 4 * (int64_t)cap) return MVSD_E_RANGE;
+  // The row masks of the whole batch, then one verify launch per kMaxLaunchRequests requests
+  // (their tables live in LDS); the launches share the workspace, which each leaves zeroed.
+  if (masked) {
+    err = mvsd::launch_constraints(p, a->target_dtype, (hipStream_t)stream);
+    if (err != hipSuccess) return hip_status(err);
   }
-  return hip_status(mvsd::launch_verify(p, a->target_dtype, kmode, grid, (hipStream_t)stream));
+  const int groups_per_req = (int)((a->max_spec_len + size_plan.g - 1) / size_plan.g);
+  for (int64_t r0 = 0; r0 < B; r0 += mvsd::kMaxLaunchRequests) {
+    const int64_t Bl = launch_requests(B - r0);
+    mvsd::VerifyParams q = p;
+    q.B = (int)Bl;
+    q.out = p.out + r0 * p.out_stride;
+    q.bonus = p.bonus + r0;
+    q.cu = p.cu + r0;
+    q.cu_prev = r0 > 0 ? p.cu + r0 - 1 : nullptr;
+    if (p.temperature) q.temperature = p.temperature + r0;
+    if (p.noise) q.noise = p.noise + r0 * p.noise_stride;
+    if (p.top_k) q.top_k = p.top_k + r0;
+    if (p.top_p) q.top_p = p.top_p + r0;
+    // Units: at most one stats unit per group and one score unit per random request.
+    int64_t groups = Bl * groups_per_req;
+    if (groups > P) groups = P;
+    const int64_t units = groups + (scores ? Bl : 0);
+    const mvsd::VerifyPlan plan = mvsd::verify_plan(a->target_dtype, V, units, cap);
+    q.chunk = plan.chunk;
+    q.nc = plan.nc;
+    int64_t grid = units * plan.nc;
+    if (grid > cap) grid = cap;
+    if (grid < 1) grid = 1;
+    // A request's score unit comes `lag` stats units after its last one: with two tickets per
+    // resident workgroup in hand, that is enough for its stats tasks to have finished (and its
+    // decision to be published), and short enough for the rejected row to be re-read from the
+    // Infinity Cache.
+    q.lag = (int)((grid + plan.nc - 1) / plan.nc) + 2;
+    // every workgroup may claim two tickets past the last task
+    if (units * plan.nc > 0x7fffffff - 4 * grid) return MVSD_E_RANGE;
+    err = mvsd::launch_verify(q, a->target_dtype, (int)grid, (hipStream_t)stream);
+    if (err != hipSuccess) return hip_status(err);
+  }
+  return MVSD_OK;
 }
 
 int mvsd_apply_logits_processors(float* logits, int64_t stride, int64_t num_tokens,

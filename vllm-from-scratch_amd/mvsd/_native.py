@@ -19,6 +19,9 @@ from .build import LIB_PATH
 # dtype codes (include/mvsd.h)
 F32, BF16, F16, F64, I32, I64, U8 = range(7)
 
+# Output entry of a verification whose bounded waits gave up (MVSD_POISON in include/mvsd.h).
+POISON = -(2 ** 31)
+
 _TORCH_CODES = {
     torch.float32: F32,
     torch.bfloat16: BF16,
@@ -79,6 +82,7 @@ SIGNATURES = {
                                             c_double, c_double, c_void_p]),
     "mvsd_rejection_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int, c_int64]),
     "mvsd_rejection_workspace_init": (c_int, [c_void_p, c_int64, c_void_p]),
+    "mvsd_set_wait_limit": (c_int, [c_int]),
     "mvsd_rejection_sample": (c_int, [ctypes.POINTER(RejectionArgs), c_void_p]),
     "mvsd_apply_top_k_top_p": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                                        c_void_p]),

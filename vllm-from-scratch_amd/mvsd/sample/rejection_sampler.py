@@ -9,13 +9,17 @@ Same public names, signatures, dtypes and error behaviour as the reference modul
     apply_sampling_constraints / expand_batch_to_tokens / generate_uniform_probs /
     sample_recovered_tokens, PLACEHOLDER_TOKEN_ID, GREEDY_TEMPERATURE, MAX_SPEC_LEN
 
-The arithmetic is one persistent HIP launch (``mvsd_rejection_sample`` in include/mvsd.h,
-after a one-block init launch): target softmax statistics, greedy argmax, exponential-race
-recovered tokens, acceptance chain and bonus emission, reading each draft / noise element once
-and each target element once per phase (statistics, then scores; the single-read variant is
-selected with MVSD_VERIFY_MODE=fused).  ``RejectionSampler.forward`` also folds the gather of
-verify rows and the temperature divide into that launch when no logits processor or
-top-k/top-p needs the processed logits.
+The arithmetic is one persistent HIP launch (``mvsd_rejection_sample`` in include/mvsd.h):
+target softmax statistics or greedy argmax over every verify row, the acceptance chain of
+each request, and the exponential-race recovered token of the one row each request actually
+rejects (the reference scores every row and keeps that one), with bonus emission.  Each target
+element is read once, plus the rejected rows' target, draft and noise elements once more.
+``RejectionSampler.forward`` also folds the gather of verify rows, the temperature divide and
+top-k / top-p into that launch when no logits processor needs the processed logits.
+
+The kernel's cross-workgroup waits are bounded.  If one gives up, the affected requests'
+output rows hold INT32_MIN in every entry and ``parse_output``, the path's
+only device-to-host copy, raises ``RuntimeError``; the next call is unaffected.
 
 Randomness is drawn by the same seams as the reference, and both stay monkeypatchable:
 ``generate_uniform_probs`` (fp64 [P]) and the exponential noise of
@@ -293,6 +297,12 @@ class RejectionSampler:
         tokens and logprobs together; ``cu_num_generated_tokens`` gives each request's first
         row (before ``discard_req_indices`` is applied, as in the reference)."""
         out = output_token_ids.cpu().numpy()
+        if (out == nat.POISON).any():
+            bad = np.flatnonzero((out == nat.POISON).any(axis=1)).tolist()
+            raise RuntimeError(
+                f"verification of requests {bad} gave up waiting for partial results inside the "
+                "kernel (output rows poisoned); the call's tokens are unusable, later calls are "
+                "not affected")
         valid = (out != PLACEHOLDER_TOKEN_ID) & (out < vocab_size)
         output_logprobs = None
         if logprobs_tensors is not None:
@@ -761,14 +771,6 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
                   "mvsd_rejection_workspace_init")
         _WORKSPACES[key] = ws
     return ws
-
-
-def workspace_error_flag(device: torch.device) -> int:
-    """The sticky spin-limit flag of this stream's workspace (synchronises; diagnostics)."""
-    key = (device.index if device.index is not None else torch.cuda.current_device(),
-           nat.stream_of(device))
-    ws = _WORKSPACES.get(key)
-    return 0 if ws is None else int(ws[4:8].view(torch.int32).item())
 
 
 def _as(t: torch.Tensor, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
