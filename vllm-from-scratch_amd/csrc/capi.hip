@@ -286,11 +286,12 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
     int64_t grid = units * plan.nc;
     if (grid > cap) grid = cap;
     if (grid < 1) grid = 1;
-    // A request's score unit comes `lag` stats units after its last one: with two tickets per
-    // resident workgroup in hand, that is enough for its stats tasks to have finished (and its
-    // decision to be published), and short enough for the rejected row to be re-read from the
-    // Infinity Cache.
-    q.lag = (int)((grid + plan.nc - 1) / plan.nc) + 2;
+    // A request's score unit comes `lag` stats units after its last one.  Each resident
+    // workgroup holds two tickets, and a decision appears shortly after the request's last stats
+    // task ends, so about three tickets per workgroup between the two (lag stats units and about
+    // as many score units) let the score tasks find their decision published, while the
+    // rejected row is still likely to be in the Infinity Cache.
+    q.lag = (int)((3 * grid + 2 * plan.nc - 1) / (2 * plan.nc)) + 2;
     // every workgroup may claim two tickets past the last task
     if (units * plan.nc > 0x7fffffff - 4 * grid) return MVSD_E_RANGE;
     err = mvsd::launch_verify(q, a->target_dtype, (int)grid, (hipStream_t)stream);

@@ -18,7 +18,7 @@
 //   * Stats units: a group of up to G rows of one request, as NC tasks of one column chunk
 //     each.  Random rows publish, per chunk, a slot with (raw max, sum of
 //     exp2((x - max) * log2(e) / T)); greedy rows publish the chunk's argmax key.
-//   * The last stats task of a request to finish (relaxed atomic count) decides it: per row
+//   * The last stats task of a request to start (relaxed atomic count) decides it: per row
 //     it combines the row's slots into (max, sum) or the argmax, reads the draft id, q[d],
 //     x[d] and the uniform, and finds the first rejection.  Greedy requests and random
 //     requests whose recovered ids are supplied get their output row right there.  Other
@@ -28,11 +28,13 @@
 //     request's last stats unit, so that the decision is normally there when they start.  A
 //     score task reads the decision; with a rejection at row j it streams chunk c of target
 //     row j, draft row j and the request's noise row and publishes the chunk's argmax of
-//     max(p - q, 0) * (1 / E).  The last of them to finish writes the request's output row.
+//     max(p - q, 0) * (1 / E).  The last of them to start writes the request's output row.
 //     Every output row therefore has exactly one writer.
-//   * Progress: waits depend only on lower tickets (a score task on the stats tasks of its
-//     request, a decision on its request's stats slots), and a workgroup settles the decision
-//     it owes before it waits for any decision, so no wait can deadlock.  Every wait is still
+//   * Tasks are counted when they start.  The last stats task of a request to start decides the
+//     request right after its own work, waiting only for the slots of the request's other stats
+//     tasks, which have started and never wait; likewise the last score task to start finishes
+//     the request.  A score task waits for its request's decision, which depends only on stats
+//     tasks holding lower tickets.  So no wait can deadlock.  Every wait is still
 //     bounded: a wait that gives up sets the failure flag, after which the other waits give up
 //     quickly; the writer of each request whose inputs are incomplete fills its output row
 //     with kPoison, and the last workgroup out clears the workspace.
@@ -619,10 +621,13 @@ struct DecideSmem {
 // Decision slot values of a kFull request: first rejected position + 1 in [1, K], K + 1 when
 // every draft is accepted, kDecisionFailed when the decider's waits gave up.
 constexpr int kDecisionFailed = 0x40000000;
-// Score slot of a task that could not score (a wait gave up); below every real key.
+// Score slots of a task that could not score (a wait gave up) and of a task with nothing to
+// score (every draft accepted, or the decider gave up); both below every real key.
 constexpr uint64_t kFailKey = 1;
+constexpr uint64_t kSkipKey = 2;
 
-// Executed by the whole block that finished request r's last stats task.  Combines every
+// Executed by the whole block that ran the last stats task of request r to start, once that
+// task is done.  Combines every
 // row's slots and decides every position in parallel (the chain keeps the prefix up to the
 // first rejection).  Greedy requests and random requests with supplied recovered ids get
 // their output row here (kPoison in every entry if a wait gave up), and every slot of the
@@ -699,30 +704,29 @@ __device__ void decide_request(const VerifyParams& p, const Tables& tb, int r, D
   }
 }
 
-// One wave of the block that finished the last score task of kFull request r, whose decision
-// that task read as `dec` (0 if its wait gave up).  Writes the request's output row: the
-// accepted drafts, then the recovered id from the score slots at the rejected position, or the
-// bonus after a fully accepted chain; kPoison in every entry if any wait gave up.  Then clears
-// everything the request used.
+// One wave of the block that ran the last score task of kFull request r to start, which read
+// the decision as `dec` (0 if its wait gave up).  Waits for every score slot of the request (so
+// every score task has read the decision and the rejected row's statistics), then writes the
+// request's output row: the accepted drafts, then the recovered id at the rejected position,
+// or the bonus after a fully accepted chain; kPoison in every entry if any wait gave up.  Then
+// clears everything the request used.
 __device__ void finish_scores(const VerifyParams& p, const Tables& tb, int r, int dec) {
   if (wave_id() != 0) return;
   const int lane = lane_id();
   const int begin = tb.begin[r];
   const int K = tb.kflags[r] & 0xffff;
   uint64_t* slots = p.score_slots + (int64_t)r * p.nc;
-  bool failed = dec < 1 || dec > K + 1;
-  int first = K, tok = -1;
-  if (!failed && dec <= K) {
-    first = dec - 1;
-    uint64_t v[kKeep];
-    failed = !wave_poll(p, slots, p.nc, v);
-    int bad = 0;
+  uint64_t v[kKeep];
+  bool failed = !wave_poll(p, slots, p.nc, v);
+  int bad = 0;
 #pragma unroll
-    for (int j = 0; j < kKeep; ++j) bad |= v[j] == kFailKey;
-    for (int c = lane + kKeep * kWave; c < p.nc; c += kWave) bad |= slot_load(slots + c) == kFailKey;
-    failed |= __any(bad) != 0;
-    tok = min(max(key_index(combine_keys(slots, p.nc, v)), 0), p.V - 1);
-  }
+  for (int j = 0; j < kKeep; ++j) bad |= v[j] == kFailKey;
+  for (int c = lane + kKeep * kWave; c < p.nc; c += kWave) bad |= slot_load(slots + c) == kFailKey;
+  failed |= __any(bad) != 0;
+  failed |= dec < 1 || dec > K + 1;
+  const int first = failed ? K : dec - 1;
+  int tok = -1;
+  if (!failed && first < K) tok = min(max(key_index(combine_keys(slots, p.nc, v)), 0), p.V - 1);
   int32_t* out = p.out + (int64_t)r * p.out_stride;
   for (int pos = lane; pos <= p.max_spec_len; pos += kWave) {
     int v = -1;
@@ -894,21 +898,10 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
   build_tables(p, tb, s_wave);
   const int total = (tb.groups + tb.nfull) * p.nc;
 
-  // Deferred completion count: the atomic's result is examined after the next task (or before
-  // a score task waits), so its round trip is never waited for on the task path.
-  int pend_kind = 0, pend_cnt = 0, pend_r = 0, pend_target = 0, pend_first = 0;
-  auto settle = [&]() {
-    if (pend_kind) {
-      if (tid == 0) s_last = pend_cnt == pend_target - 1;
-      __syncthreads();
-      if (s_last) {
-        if (pend_kind == kStatsTask) decide_request(p, tb, pend_r, dsm);
-        else finish_scores(p, tb, pend_r, pend_first);
-      }
-      __syncthreads();
-      pend_kind = 0;
-    }
-  };
+  // Every task is counted when it starts, with a relaxed atomic whose result is examined when
+  // the task ends (its round trip overlaps the task).  The last task of a request to start
+  // finishes the request right after its own work: it waits only for the slots of the request's
+  // other tasks, which have all started and never wait themselves.
 
   // The next ticket is claimed when a task starts and decoded once the task's loads are in
   // flight, so the atomic and the decode overlap with HBM traffic.
@@ -931,22 +924,22 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
     const float c1 = __int_as_float(info[6]);
     const int64_t v0 = (int64_t)c * p.chunk;
     const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
+    int started = 0;
     if (kind == kStatsTask) {
       const int nrows = rinfo & 0xff;
       const int ngr = (rinfo >> 8) & 0xff;
+      if (tid == 0) started = atomic_add_relaxed(&p.req_cnt[r], 1);
       if ((rinfo >> 16) & kGreedy)
         task_argmax<DT, EPT, G, MASKED>(p, c, row0, nrows, v0, vend, s_key, prefetch);
       else
         task_stats<DT, EPT, G, MASKED>(p, c, c1, row0, nrows, v0, vend, s_red, s_M, prefetch);
-      settle();
-      if (tid == 0) pend_cnt = atomic_add_relaxed(&p.req_cnt[r], 1);
-      pend_kind = kStatsTask;
-      pend_r = r;
-      pend_target = ngr * p.nc;
+      if (tid == 0) s_last = started == ngr * p.nc - 1;
+      __syncthreads();
+      if (s_last) decide_request(p, tb, r, dsm);
     } else if (kind == kScoreTask) {
-      // no decision may be owed by a workgroup that waits for one
-      settle();
+      // every score task counts, so that exactly one of them finishes the request
       if (tid == 0) {
+        started = atomic_add_relaxed(&p.score_cnt[r], 1);
         int d = info[7];
         for (int spins = 0; d == 0; ++spins) {
           if (spins >= p.spin_limit ||
@@ -962,31 +955,31 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
       __syncthreads();
       const int d = s_dec;
       const int K = rinfo & 0xffff;
+      uint64_t key = d == 0 ? kFailKey : kSkipKey;
       if (d >= 1 && d <= K) {
         // rejection at position d - 1: score this chunk of that row
         const int row = row0 + d - 1;
         const int draft = HAS_DRAFT ? -1 : p.draft_ids[row];
         bool ok;
-        const uint64_t key = task_score<DT, EPT, HAS_DRAFT, MASKED>(
-            p, r, c1, row, draft, v0, vend, s_key, s_ml, ok, prefetch);
-        if (tid == 0) slot_store(p.score_slots + (int64_t)r * p.nc + c, ok ? key : kFailKey);
+        key = task_score<DT, 2 * EPT, HAS_DRAFT, MASKED>(p, r, c1, row, draft, v0, vend, s_key,
+                                                         s_ml, ok, prefetch);
+        if (!ok) key = kFailKey;
       } else {
-        // every draft accepted, or no usable decision: nothing to score
+        // every draft accepted, or no usable decision: nothing to score, but the slot tells
+        // the finisher that this task has read the decision
         prefetch();
-        if (tid == 0 && d == 0) slot_store(p.score_slots + (int64_t)r * p.nc + c, kFailKey);
       }
-      // every score task counts, so that exactly one of them finishes the request
-      if (tid == 0) pend_cnt = atomic_add_relaxed(&p.score_cnt[r], 1);
-      pend_kind = kScoreTask;
-      pend_r = r;
-      pend_target = p.nc;
-      pend_first = d;
+      if (tid == 0) {
+        slot_store(p.score_slots + (int64_t)r * p.nc + c, key);
+        s_last = started == p.nc - 1;
+      }
+      __syncthreads();
+      if (s_last) finish_scores(p, tb, r, d);
     } else {
       prefetch();
     }
     __syncthreads();
   }
-  settle();
 
   // The last workgroup out resets the ticket and the exit counter.  If some wait gave up, the
   // requests concerned already hold kPoison; slots may still have been published after the
@@ -1043,6 +1036,7 @@ hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream) {
 constexpr int kGroup = 4;          // rows per stats group
 constexpr int kMinSubs = 8;        // sub-chunks per task at least
 constexpr int kTasksPerWg = 10;    // tasks per resident workgroup aimed for
+constexpr int64_t kTaskBytes = 512 * 1024;  // target bytes of a stats task at most (about 15 us)
 template <int DT>
 constexpr int ept_of() {
   return DT == MVSD_F32 ? 4 : 8;  // 16 bytes of target per thread and row per sub-chunk
@@ -1058,13 +1052,20 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int 
   // long as possible (fewer ticket claims, longer load pipelines), and at least kMinSubs
   // sub-chunks per task so that small batches do not shred the rows into tasks too short to
   // amortise their start and end.
+  // Long tasks also lengthen the launch's tail, so a stats task reads at most about kTaskBytes.
+  // Score tasks walk sub-chunks of twice the columns, so chunks hold an even number of
+  // sub-chunks.
   const int64_t nc_max = nsub / kMinSubs > 1 ? nsub / kMinSubs : 1;
   int64_t nc = nc_max;
   if (units > 0 && cap > 0) {
+    const int64_t esize = target_dtype == MVSD_F32 ? 4 : 2;
+    const int64_t by_bytes = (vocab_size * kGroup * esize + kTaskBytes - 1) / kTaskBytes;
     nc = ((int64_t)kTasksPerWg * cap + units - 1) / units;
+    nc = nc < by_bytes ? by_bytes : nc;
     nc = nc < 1 ? 1 : (nc > nc_max ? nc_max : nc);
   }
-  const int64_t subs_per_chunk = (nsub + nc - 1) / nc;
+  int64_t subs_per_chunk = (nsub + nc - 1) / nc;
+  if (subs_per_chunk > 1) subs_per_chunk += subs_per_chunk & 1;
   plan.chunk = (int)(subs_per_chunk * plan.sub);
   plan.nc = (int)((vocab_size + plan.chunk - 1) / plan.chunk);
   plan.nc_max = (int)nc_max;
