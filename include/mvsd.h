@@ -47,7 +47,8 @@ enum {
   MVSD_E_ALIGN = -2,       /* pointer/stride alignment the kernel needs is not met */
   MVSD_E_WORKSPACE = -3,   /* workspace missing or too small */
   MVSD_E_HIP = -4,         /* a HIP runtime call failed; see mvsd_last_hip_error() */
-  MVSD_E_RANGE = -5        /* a size exceeds what the kernel supports */
+  MVSD_E_RANGE = -5,       /* a size exceeds what the kernel supports */
+  MVSD_E_SCRATCH = -6      /* the static scratch is too small for the batch */
 };
 
 /* Library version, (major << 16) | (minor << 8) | patch. */
@@ -162,6 +163,21 @@ int mvsd_rejection_workspace_init(void* workspace, int64_t workspace_bytes, mvsd
  * previous limit.  No counterpart in the reference. */
 int mvsd_set_wait_limit(int polls);
 int mvsd_rejection_sample(const mvsd_rejection_args* args, mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* rejection_sample_static — mvsd_rejection_sample without a workspace argument.           */
+/* No counterpart in the reference: it is for callers that cannot allocate device memory  */
+/* (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).   */
+/* The workspace fields of *args are ignored; the scratch is a static device array of      */
+/* mvsd_rejection_static_scratch_bytes() bytes (16 MiB) that the library holds on every    */
+/* device it runs on until the process ends, zero-filled by a kernel on the first call for */
+/* a device.  Nothing is allocated.  A batch whose mvsd_rejection_workspace_bytes(...)      */
+/* exceeds the scratch returns MVSD_E_SCRATCH.  Every call on one device shares that        */
+/* device's scratch, so calls that can overlap on one device (different streams) race.     */
+/* Results, failure behaviour and everything else are those of mvsd_rejection_sample.      */
+/* ------------------------------------------------------------------------------------ */
+int64_t mvsd_rejection_static_scratch_bytes(void);
+int mvsd_rejection_sample_static(const mvsd_rejection_args* args, mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
 /* sampling_masks — the per-row masks mvsd_rejection_sample applies for top_k / top_p.     */

@@ -46,6 +46,9 @@ int elem_size(int dtype) {
 
 constexpr int kMaxDevices = 64;
 
+// Size of the static scratch of mvsd_rejection_sample_static (include/mvsd.h).
+constexpr int64_t kStaticScratchBytes = 16ll << 20;
+
 // Polls before a verify-kernel wait gives up (mvsd_set_wait_limit).
 std::atomic<int> g_wait_limit{mvsd::kSpinLimitDefault};
 
@@ -136,6 +139,9 @@ const char* mvsd_status_string(int status) {
     case MVSD_E_WORKSPACE: return "workspace missing or too small";
     case MVSD_E_HIP: return "HIP runtime error";
     case MVSD_E_RANGE: return "size outside the supported range";
+    case MVSD_E_SCRATCH:
+      return "the batch needs more scratch than the static scratch of "
+             "mvsd_rejection_sample_static holds (see mvsd_rejection_static_scratch_bytes)";
     default: return "unknown status";
   }
 }
@@ -175,7 +181,14 @@ int mvsd_rejection_workspace_init(void* workspace, int64_t workspace_bytes, mvsd
   return hip_status(mvsd::launch_zero_fill(workspace, workspace_bytes, (hipStream_t)stream));
 }
 
-int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// mvsd_rejection_sample with the workspace `ws` of `ws_bytes` bytes (the args' workspace fields
+// are not read).
+int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws_bytes,
+                          mvsd_stream_t stream) {
   if (!a) return MVSD_E_INVALID;
   const int64_t B = a->batch_size, P = a->num_tokens, V = a->vocab_size;
   if (B < 0 || P < 0 || V <= 0 || a->max_spec_len < 0) return MVSD_E_INVALID;
@@ -201,8 +214,8 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   // on the device.
   const mvsd::VerifyPlan size_plan = mvsd::verify_plan(a->target_dtype, V, 0, 0);
   const WorkspaceLayout lay = verify_layout(launch_requests(B), P, size_plan.nc_max);
-  if (!a->workspace || a->workspace_bytes < lay.total) return MVSD_E_WORKSPACE;
-  if ((uintptr_t)a->workspace % 256 != 0) return MVSD_E_ALIGN;
+  if (!ws_ptr || ws_bytes < lay.total) return MVSD_E_WORKSPACE;
+  if ((uintptr_t)ws_ptr % 256 != 0) return MVSD_E_ALIGN;
 
   // Random requests with in-kernel recovered ids get score units (one per request).
   const bool scores = !a->all_greedy && !a->recovered_token_ids;
@@ -214,7 +227,7 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
   const int cap = verify_capacity(device, a->target_dtype, a->draft_probs != nullptr, masked);
   if (cap <= 0) return hip_status(hipErrorInvalidDevice);
 
-  char* ws = static_cast<char*>(a->workspace);
+  char* ws = static_cast<char*>(ws_ptr);
   mvsd::VerifyParams p;
   memset(&p, 0, sizeof(p));
   p.out = a->output_token_ids;
@@ -298,6 +311,69 @@ int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
     if (err != hipSuccess) return hip_status(err);
   }
   return MVSD_OK;
+}
+
+// Static scratch of mvsd_rejection_sample_static: one per device that the library runs on, held
+// until the process ends.  Host code never uses the array's name as an address: the device
+// address comes from hipGetSymbolAddress, once per device, with that device current.
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+struct StaticScratch {
+  std::mutex mu;
+  void* ptr[kMaxDevices] = {};
+};
+
+StaticScratch& static_scratch() {
+  static StaticScratch s;
+  return s;
+}
+
+// The calling thread's current device's scratch address; on the first call for a device also
+// zero-fills the scratch with a kernel on `stream` (the verify workspace contract).
+int static_scratch_for_current_device(void** out, hipStream_t stream) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_status(err);
+  if (device < 0 || device >= kMaxDevices) return MVSD_E_RANGE;
+  StaticScratch& st = static_scratch();
+  std::lock_guard<std::mutex> lock(st.mu);
+  if (!st.ptr[device]) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return hip_status(err);
+    if (!ptr) return hip_status(hipErrorInvalidSymbol);
+    err = mvsd::launch_zero_fill(ptr, kStaticScratchBytes, stream);
+    if (err != hipSuccess) return hip_status(err);
+    st.ptr[device] = ptr;
+  }
+  *out = st.ptr[device];
+  return MVSD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mvsd_rejection_sample(const mvsd_rejection_args* a, mvsd_stream_t stream) {
+  if (!a) return MVSD_E_INVALID;
+  return rejection_sample_impl(a, a->workspace, a->workspace_bytes, stream);
+}
+
+int64_t mvsd_rejection_static_scratch_bytes(void) { return kStaticScratchBytes; }
+
+int mvsd_rejection_sample_static(const mvsd_rejection_args* a, mvsd_stream_t stream) {
+  if (!a) return MVSD_E_INVALID;
+  if (a->batch_size < 0 || a->num_tokens < 0 || a->vocab_size <= 0) return MVSD_E_INVALID;
+  const int64_t need = mvsd_rejection_workspace_bytes(a->batch_size, a->num_tokens,
+                                                      a->vocab_size, a->target_dtype,
+                                                      a->max_spec_len);
+  if (need < 0) return MVSD_E_INVALID;
+  if (need > kStaticScratchBytes) return MVSD_E_SCRATCH;
+  if (a->batch_size == 0) return MVSD_OK;
+  void* ws = nullptr;
+  const int st = static_scratch_for_current_device(&ws, (hipStream_t)stream);
+  if (st != MVSD_OK) return st;
+  return rejection_sample_impl(a, ws, kStaticScratchBytes, stream);
 }
 
 int mvsd_apply_logits_processors(float* logits, int64_t stride, int64_t num_tokens,

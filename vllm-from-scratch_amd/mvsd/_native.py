@@ -84,6 +84,8 @@ SIGNATURES = {
     "mvsd_rejection_workspace_init": (c_int, [c_void_p, c_int64, c_void_p]),
     "mvsd_set_wait_limit": (c_int, [c_int]),
     "mvsd_rejection_sample": (c_int, [ctypes.POINTER(RejectionArgs), c_void_p]),
+    "mvsd_rejection_static_scratch_bytes": (c_int64, []),
+    "mvsd_rejection_sample_static": (c_int, [ctypes.POINTER(RejectionArgs), c_void_p]),
     "mvsd_apply_top_k_top_p": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                                        c_void_p]),
     "mvsd_selftest": (c_int, [c_int, c_void_p, c_void_p]),
