@@ -5,11 +5,20 @@
 A step is one ``rejection_sample`` call (the persistent verify kernel; with top-k / top-p the
 constraints kernel before it) over the whole batch, inputs already resident in HBM; the
 default workload is the headline configuration (B=256, k=4, V=151936, fp32 target logits and
-draft probs, random T=0.8).  Prints ONE JSON line: value = achieved GB/s (algorithmic bytes
-per step / step time over the timed region, which holds only the calls), with verified
-tokens/s, the roofline object (kernel time from HIP events recorded around every launch on
-the launch stream, in a second pass of the same number of steps) and a host-CPU baseline of
-the oracle on a bounded sample.
+draft probs, random T=0.8).  Prints ONE JSON line:
+
+* value = GB/s over the bytes the kernel's algorithm moves (every verify row of the target
+  once, plus target, draft and noise of each request's first rejected row, the decision
+  inputs, metadata and output; from the run's own output, ``configs.kernel_bytes``) per step,
+  step time over the timed region, which holds only the calls;
+* config.reference_algorithm_bytes = the bytes the reference algorithm reads (every row
+  scored, the survey's count), with the step rate on those bytes beside it;
+* verified tokens/s, the accept-length histogram and per-position accept rates;
+* roofline: kernel time from HIP events recorded around every launch on the launch stream, in
+  a second pass of the same number of steps; traffic from the committed rocprofv3 summary when
+  it was measured on the current kernel sources (their sha256), else null;
+* cpu_baseline: the oracle (the reference algorithm on torch-CPU) on all host threads and on
+  one, with each run-to-run spread; parity: the GPU tokens against that oracle run.
 
 ``--pmc-driver`` runs a 1 GiB device copy (the calibration kernel for rocprofv3 counters)
 followed by a few headline steps, and prints nothing else; profiles/ records the rocprofv3
@@ -43,8 +52,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="h", choices=["h", "c1", "c2", "c3", "c4", "c5", "v2"])
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
-                    help="minimum CPU time of the CPU-baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="minimum CPU time of each CPU-baseline sample (all threads, one thread)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-driver", action="store_true",
                     help="run the counter-calibration copy and a few steps, print nothing")
@@ -79,6 +88,22 @@ def run_step(w):
     return step
 
 
+def settle_gpu(seconds=0.1):
+    """Bring the GPU out of its idle clock state before the warm-up steps: device-to-device
+    copies of a 256 MiB buffer for `seconds` (not the workload; nothing from it is kept).
+    Without it the first tens of timed steps of a fresh process run a few percent slower."""
+    a = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            b.copy_(a)
+        torch.cuda.synchronize()
+    del a, b
+    torch.cuda.synchronize()
+
+
 def time_steps(step, steps, warmup):
     """Time `steps` calls after `warmup` untimed ones.  Returns (ms per step over the timed
     region, mean ms between HIP events recorded right before and after each call, wall ms per
@@ -86,6 +111,7 @@ def time_steps(step, steps, warmup):
     per-call events are recorded in a second pass of `steps` calls, so that their markers do
     not inflate the timed region.  All events are recorded on the current stream, the stream
     the kernels are launched on."""
+    settle_gpu()
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -117,14 +143,13 @@ def accept_histogram(outputs, num_draft_tokens, max_k):
     return hist
 
 
-def cpu_baseline(w, min_seconds):
-    """Time the CPU oracle (oracle/rejection.py on torch-CPU, all host threads) over the whole
-    workload, repeated until at least `min_seconds` of CPU work; returns GB/s over the
-    algorithmic bytes processed."""
-    from mvsd.testing import configs
+def cpu_oracle_runner(w):
+    """A callable running the CPU oracle (oracle/rejection.py on torch-CPU, the reference's
+    algorithm step by step) over the whole workload on host copies of the same inputs,
+    uniforms and noise; with top-k / top-p, the processed path (temperature, constraints, then
+    verification)."""
     from oracle import rejection as orc
 
-    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
     ks = w.num_draft_tokens
     rows = w.target_rows.long() if w.target_rows is not None else None
     tl = (w.target_logits if rows is None else w.target_logits[rows]).cpu()
@@ -146,7 +171,7 @@ def cpu_baseline(w, min_seconds):
         row_p = None if w.top_p is None else w.top_p.cpu()[req]
 
     def run():
-        if constrained:  # processed path: temperature, top-k / top-p, then verification
+        if constrained:
             x = otp.apply_top_k_top_p(tl.float() / row_t.unsqueeze(-1), row_k, row_p)
             return orc.rejection_sample(ids, ks, w.max_spec_len, dp, x, bonus, temperature=temp,
                                         all_greedy=w.all_greedy, uniforms=u, exp_noise=noise,
@@ -154,35 +179,79 @@ def cpu_baseline(w, min_seconds):
         return orc.rejection_sample(ids, ks, w.max_spec_len, dp, tl, bonus, temperature=temp,
                                     all_greedy=w.all_greedy, uniforms=u, exp_noise=noise,
                                     apply_temperature=w.apply_temperature)
+    return run
 
-    run()  # warm-up
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        run()
-        reps += 1
-        sec = time.perf_counter() - t0
-        if sec >= min_seconds:
-            break
-    nbytes = configs.algorithmic_bytes(w) * reps
-    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s",
-            "cores": torch.get_num_threads(), "kind": "port",
+
+def cpu_baseline(w, min_seconds):
+    """Time the CPU oracle on all host threads, then on one thread, each repeated until at
+    least `min_seconds` of CPU work; GB/s over the reference algorithm's bytes.  Returns the
+    cpu_baseline object (all threads, with the one-thread figure and the run-to-run spread of
+    both) and the oracle's result for the parity check."""
+    from mvsd.testing import configs
+
+    run = cpu_oracle_runner(w)
+    nbytes = configs.algorithmic_bytes(w)
+    all_threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    figures = []
+    ref = None
+    for threads in (all_threads, 1):
+        torch.set_num_threads(threads)
+        ref = run()  # warm-up (and the parity reference)
+        times = []
+        t0 = time.perf_counter()
+        while True:
+            t1 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t1)
+            if time.perf_counter() - t0 >= min_seconds:
+                break
+        rates = [nbytes / t / 1e9 for t in times]
+        figures.append({"cores": threads, "value": round(nbytes * len(times) / sum(times) / 1e9, 3),
+                        "min": round(min(rates), 3), "max": round(max(rates), 3),
+                        "runs": len(times), "seconds": round(sum(times), 2)})
+    torch.set_num_threads(all_threads)
+    main = figures[0]
+    return {"value": main["value"], "unit": "GB/s", "cores": main["cores"], "kind": "port",
             "sample": f"the whole workload ({w.batch_size} requests, {w.num_tokens} verify rows, "
-                      f"V={w.vocab_size}) through oracle/rejection.py on torch-CPU, {reps} "
-                      f"back-to-back runs in {sec:.1f} s after one warm-up; inputs in host "
+                      f"V={w.vocab_size}) through oracle/rejection.py on torch-CPU (the "
+                      f"reference algorithm: every row scored), repeated back to back after one "
+                      f"warm-up, on {main['cores']} threads and on 1; GB/s over the reference "
+                      f"algorithm's bytes; min/max are the per-run spread; inputs in host "
                       f"memory, same uniforms and noise as the GPU run",
-            "seconds": round(sec, 2)}
+            "by_cores": figures}, ref
+
+
+# Sources whose change invalidates a committed counter summary of the verify kernel.
+KERNEL_SOURCES = ["vllm-from-scratch_amd/csrc/verify.hip", "vllm-from-scratch_amd/csrc/verify.h",
+                  "vllm-from-scratch_amd/csrc/capi.hip", "vllm-from-scratch_amd/csrc/mvsd_device.h",
+                  "vllm-from-scratch_amd/csrc/constraints.hip"]
+
+
+def kernel_sources_sha256():
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()
 
 
 def load_traffic(config):
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-    (a line ``traffic_bytes_per_launch[<config>] = N``), or None."""
-    if TRAFFIC_FILE.exists():
-        key = f"traffic_bytes_per_launch[{config}] = "
-        for line in TRAFFIC_FILE.read_text().splitlines():
-            if line.startswith(key):
-                return int(line[len(key):].strip())
-    return None
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (a
+    line ``traffic_bytes_per_launch[<config>] = N``), used only when the summary's
+    ``kernel_sources_sha256`` matches the current kernel sources; else None."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    value, sha = None, None
+    key = f"traffic_bytes_per_launch[{config}] = "
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith(key):
+            value = int(line[len(key):].strip())
+        if line.startswith("kernel_sources_sha256 = "):
+            sha = line.split("=", 1)[1].strip()
+    if value is None or sha != kernel_sources_sha256():
+        return None
+    return value
 
 
 def bench_ngram(args, device):
@@ -340,8 +409,12 @@ def main():
         torch.cuda.synchronize()
         return
     ms, launch_ms, wall_ms, out = time_steps(step, args.steps, args.warmup)
-    nbytes = configs.algorithmic_bytes(w)
     outputs, _ = RejectionSampler.parse_output(out, w.vocab_size)
+    constrained = w.top_k is not None or w.top_p is not None
+    # the constraints kernel reads each constrained row about twice (top-k: one pass and an
+    # LDS selection; top-p: a histogram pass and a gather pass), counted as two passes
+    nbytes = configs.kernel_bytes(w, outputs, constrained_passes=2 if constrained else 0)
+    ref_bytes = configs.algorithmic_bytes(w)
     tokens = sum(len(o) for o in outputs)
     gbs = nbytes / (ms / 1e3) / 1e9
     kernel_gbs = nbytes / (launch_ms / 1e3) / 1e9
@@ -364,24 +437,54 @@ def main():
                                 "c4": "c4 ragged B=512 bf16, top-k=50 / top-p=0.9 quartiles",
                                 "c5": "c5 eagle B=1024 k=7 bf16 target"}[args.config],
                    "batch_size": w.batch_size, "num_draft_rows": w.num_tokens,
-                   "vocab_size": w.vocab_size, "algorithmic_bytes": nbytes},
+                   "vocab_size": w.vocab_size,
+                   "kernel_bytes": nbytes,
+                   "reference_algorithm_bytes": ref_bytes,
+                   "effective_GBps_on_reference_bytes": round(ref_bytes / (ms / 1e3) / 1e9, 2)},
         "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "verified_tok_per_s": round(tokens / (ms / 1e3), 1),
         "verified_tokens_per_step": tokens,
         "accept_length_hist": hist,
+        "accept_rate_by_position": accept_rates(outputs, w.num_draft_tokens, w.max_spec_len),
         "wall_ms_per_step": round(wall_ms, 5),
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(args.config),
                      "kernel": ("mvsd::verify_kernel"
-                                + (" + constraints_kernel" if w.top_k is not None or w.top_p is not None
-                                   else "") + " per rejection_sample"),
+                                + (" + constraints_kernel" if constrained else "")
+                                + " per rejection_sample"),
                      "kernel_ms": round(launch_ms, 5)},
         "cpu_baseline": None,
+        "parity": None,
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+        line["cpu_baseline"], ref = cpu_baseline(w, args.cpu_seconds)
+        line["parity"] = parity_summary(w, out, ref)
     print(json.dumps(line), flush=True)
+
+
+def accept_rates(outputs, num_draft_tokens, max_k):
+    """Per draft position j: accepted / drafted over the requests with more than j drafts
+    (the per-position counts of SpecDecodingStats.observe_draft)."""
+    drafted = np.zeros(max_k, dtype=np.int64)
+    accepted = np.zeros(max_k, dtype=np.int64)
+    for toks, k in zip(outputs, num_draft_tokens):
+        drafted[:k] += 1
+        accepted[:max(len(toks) - 1, 0)] += 1
+    return [round(float(a) / d, 4) if d else None for a, d in zip(accepted, drafted)]
+
+
+def parity_summary(w, out, ref):
+    """Token parity of the GPU output against the oracle's on the same inputs: requests whose
+    output differs, and how many of those differ only at an acceptance margin below 1e-6 or a
+    recovered-token near-tie (the allowances of the parity bar); anything else is
+    `unexplained` and fails the tests."""
+    from oracle import rejection as orc
+
+    rep = orc.compare(out.cpu().numpy(), ref, w.draft_token_ids.cpu(), w.num_draft_tokens)
+    return {"requests": rep.requests, "mismatched": rep.mismatched,
+            "accept_flips": rep.accept_flips, "recovered_flips": rep.recovered_flips,
+            "unexplained": len(rep.unexplained)}
 
 
 if __name__ == "__main__":

@@ -109,9 +109,9 @@ WorkspaceLayout verify_layout(int64_t Bl, int64_t P, int64_t nc) {
   l.masks = off;  // row masks of the sampling constraints (zeroed again by the verify kernel)
   off = align_up(off + rows * 16, 256);
   l.stat_slots = off;
-  off = align_up(off + rows * nc * 8, 256);
+  off = align_up(off + rows * 2 * nc * 8, 256);  // two slots per chunk (tail halves)
   l.score_slots = off;
-  off = align_up(off + b * nc * 8, 256);
+  off = align_up(off + b * 2 * nc * 8, 256);
   l.total = off;
   return l;
 }
@@ -305,8 +305,11 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
     // as many score units) let the score tasks find their decision published, while the
     // rejected row is still likely to be in the Infinity Cache.
     q.lag = (int)((3 * grid + 2 * plan.nc - 1) / (2 * plan.nc)) + 2;
+    // The last groups' stats tasks and every score task after them cover half chunks, so
+    // that the dependent decisions and scores at the end of the launch are short.
+    q.tail_groups = (int)((grid + 2 * plan.nc - 1) / (2 * plan.nc));
     // every workgroup may claim two tickets past the last task
-    if (units * plan.nc > 0x7fffffff - 4 * grid) return MVSD_E_RANGE;
+    if (units * 2 * plan.nc > 0x7fffffff - 4 * grid) return MVSD_E_RANGE;
     err = mvsd::launch_verify(q, a->target_dtype, (int)grid, (hipStream_t)stream);
     if (err != hipSuccess) return hip_status(err);
   }

@@ -49,18 +49,19 @@ struct VerifyParams {
   int nc;          // chunks per row
   int G;           // rows per stats group
   int lag;         // stats units between a request's last stats unit and its score unit
+  int tail_groups;  // stats groups at the end of the launch run in half-chunk tasks
   int spin_limit;  // polls before a wait gives up (0: every wait gives up at once)
   bool target_aligned;
   bool draft_aligned;
   bool noise_aligned;
   // workspace (every array is zero between calls)
   int* ctrl;             // [0] ticket, [1] wait-failure flag, [2] exit counter
-  int* req_cnt;          // [B] finished stats tasks per request
-  int* score_cnt;        // [B] finished score tasks per request
+  int* req_cnt;          // [B] started stats tasks per request
+  int* score_cnt;        // [B] started score tasks per request
   int* decision;         // [B] first rejected position + 1, or K + 1 (all accepted)
-  uint64_t* stat_slots;  // [P * nc] packed (chunk max, chunk sum); 0 = empty
-  uint64_t* arg_slots;   // [P * nc] greedy rows: chunk argmax keys; 0 = empty
-  uint64_t* score_slots;  // [B * nc] the rejected row's chunk argmax keys; 0 = empty
+  uint64_t* stat_slots;   // [P * 2 nc] per task of a row: packed (max, sum), or the argmax
+                          // key of a greedy row; 0 = empty
+  uint64_t* score_slots;  // [B * 2 nc] per score task: the rejected row's argmax key
   // Sampling constraints (top-k / top-p per request, either may be null).  When set, the
   // constraints kernel writes one row mask per verify row, (A, B, J as bits, 0): entry i of
   // the row, raw value x, is masked iff x < A || (x < B && i <= J).
@@ -106,7 +107,7 @@ struct VerifyPlan {
 // cap = resident workgroups.
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int cap);
 
-// Resident workgroups of the verify kernel per CU, for the kernel variant of this call.
+// The verify kernel variant for a target dtype, draft presence and sampling constraints.
 const void* verify_kernel_ptr(int target_dtype, bool has_draft, bool masked);
 hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream);
 hipError_t launch_verify(const VerifyParams& params, int target_dtype, int grid,

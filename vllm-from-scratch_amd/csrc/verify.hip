@@ -64,6 +64,10 @@ __device__ inline void req_range(const VerifyParams& p, int r, int& begin, int& 
   K = min(e - b, p.max_spec_len);
 }
 
+// Slots per verify row (and per request for the scores): one per task of a row, up to two per
+// chunk (tasks at the end of a launch cover half chunks).
+__device__ inline int64_t slot_stride(const VerifyParams& p) { return 2 * (int64_t)p.nc; }
+
 // log2(e) / T rounded once from double.
 __device__ inline float exp2_scale(float temp) {
   return (float)(1.4426950408889634074 / (double)temp);
@@ -84,6 +88,9 @@ struct Tables {
   int* fpos;   // [F]
   int groups;
   int nfull;
+  // The launch's tail, run in half-chunk tasks: stats units of groups >= gt, score units of
+  // ordinal >= kt; u0 = the first tail unit's position.
+  int gt, kt, u0;
 };
 
 // ------------------------------------------------------------------ loads ------------
@@ -381,7 +388,7 @@ __device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int n
 #pragma unroll
   for (int g = 0; g < G; ++g) key[g] = argmax_key(bv[g], bi[g]);
   const uint64_t best = block_max_key_to_row_thread<G, kVWaves>(key, s_key);
-  if ((int)threadIdx.x < nrows) slot_store(p.stat_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c, best);
+  if ((int)threadIdx.x < nrows) slot_store(p.stat_slots + (row0 + threadIdx.x) * slot_stride(p) + c, best);
 }
 
 // Random rows: per row, the chunk's raw max mx and sum of exp2((x - mx) * c1), kept online per
@@ -450,7 +457,7 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
   const float srow = block_sum_to_row_thread<G, kVWaves>(s, s_red);
   if ((int)threadIdx.x < nrows) {
     const float mrow = s_M[threadIdx.x];
-    slot_store(p.stat_slots + (int64_t)(row0 + threadIdx.x) * p.nc + c,
+    slot_store(p.stat_slots + (row0 + threadIdx.x) * slot_stride(p) + c,
                pack_stats(mrow, mrow == -INFINITY ? 0.f : srow));
   }
 }
@@ -465,12 +472,13 @@ struct ScoreBuf {
 
 // The rejected row `row` of random request r: the chunk-local argmax of max(p - q, 0) * (1 / E)
 // over [v0, vend) (point-mass drafts: p with the draft id d removed, :891-897).  The row's
-// statistics come from its stats slots, polled by wave 0 while the first sub-chunk loads.
+// statistics come from its nslots stats slots, polled by wave 0 while the first sub-chunk
+// loads.
 // Returns the chunk's argmax key in thread 0; ok = false if the statistics wait gave up.
 template <int DT, int EPT, bool HAS_DRAFT, bool MASKED, typename Hook>
-__device__ inline uint64_t task_score(const VerifyParams& p, int r, float c1, int row, int d,
-                                      int64_t v0, int64_t vend, uint64_t* s_key, float* s_ml,
-                                      bool& ok, Hook&& after_loads) {
+__device__ inline uint64_t task_score(const VerifyParams& p, int r, float c1, int row, int nslots,
+                                      int d, int64_t v0, int64_t vend, uint64_t* s_key,
+                                      float* s_ml, bool& ok, Hook&& after_loads) {
   using S = typename Elem<DT>::storage;
   using Buf = ScoreBuf<DT, EPT>;
   const S* tb = static_cast<const S*>(p.target) + target_row(p, row) * p.target_stride;
@@ -492,10 +500,10 @@ __device__ inline uint64_t task_score(const VerifyParams& p, int r, float c1, in
     after_loads();
     if (wave_id() == 0) {
       uint64_t v[kKeep];
-      const uint64_t* slots = p.stat_slots + (int64_t)row * p.nc;
-      const bool polled = wave_poll(p, slots, p.nc, v);
+      const uint64_t* slots = p.stat_slots + row * slot_stride(p);
+      const bool polled = wave_poll(p, slots, nslots, v);
       float mx, sum;
-      combine_stats(slots, p.nc, v, c1, mx, sum);
+      combine_stats(slots, nslots, v, c1, mx, sum);
       if (lane_id() == 0) {
         s_ml[0] = mx;
         s_ml[1] = (float)(-log2((double)sum));
@@ -609,6 +617,11 @@ __device__ inline void decide_position(const VerifyParams& p, int r, bool greedy
   token = accepted ? d : tok;
 }
 
+// Stats slots of row k of request r: nc, or 2 nc when its group is in the tail.
+__device__ inline int row_slot_count(const VerifyParams& p, const Tables& tb, int r, int k) {
+  return tb.goff[r] + k / p.G >= tb.gt ? 2 * p.nc : p.nc;
+}
+
 struct DecideSmem {
   int tok[kMaxSpecLen];
   float M[kMaxSpecLen];
@@ -648,13 +661,14 @@ __device__ void decide_request(const VerifyParams& p, const Tables& tb, int r, D
   if (tid < K) in = load_position(p, greedy, begin + tid);
   bool ok = true;
   for (int k = wave_id(); k < K; k += kVWaves) {
-    const uint64_t* slots = p.stat_slots + (int64_t)(begin + k) * p.nc;
+    const uint64_t* slots = p.stat_slots + (begin + k) * slot_stride(p);
+    const int n = row_slot_count(p, tb, r, k);
     uint64_t v[kKeep];
-    ok &= wave_poll(p, slots, p.nc, v);
+    ok &= wave_poll(p, slots, n, v);
     int tok = 0;
     float M = 0.f, S = 1.f;
-    if (greedy) tok = min(max(key_index(combine_keys(slots, p.nc, v)), 0), p.V - 1);
-    else combine_stats(slots, p.nc, v, c1, M, S);
+    if (greedy) tok = min(max(key_index(combine_keys(slots, n, v)), 0), p.V - 1);
+    else combine_stats(slots, n, v, c1, M, S);
     if (lane == 0) {
       sm.tok[k] = tok;
       sm.M[k] = M;
@@ -697,7 +711,8 @@ __device__ void decide_request(const VerifyParams& p, const Tables& tb, int r, D
       for (int k = tid; k < K; k += kVThreads) p.masks[begin + k] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   for (int k = wave_id(); k < K; k += kVWaves)
-    if (!(scored && k == first)) wave_clear(p.stat_slots + (int64_t)(begin + k) * p.nc, p.nc);
+    if (!(scored && k == first))
+      wave_clear(p.stat_slots + (begin + k) * slot_stride(p), row_slot_count(p, tb, r, k));
   if (tid == 0) {
     atomic_store_relaxed(&p.req_cnt[r], 0);
     if (full) atomic_store_relaxed(&p.decision[r], failed ? kDecisionFailed : first + 1);
@@ -705,28 +720,29 @@ __device__ void decide_request(const VerifyParams& p, const Tables& tb, int r, D
 }
 
 // One wave of the block that ran the last score task of kFull request r to start, which read
-// the decision as `dec` (0 if its wait gave up).  Waits for every score slot of the request (so
+// the decision as `dec` (0 if its wait gave up).  Waits for the nslots score slots of the
+// request (so
 // every score task has read the decision and the rejected row's statistics), then writes the
 // request's output row: the accepted drafts, then the recovered id at the rejected position,
 // or the bonus after a fully accepted chain; kPoison in every entry if any wait gave up.  Then
 // clears everything the request used.
-__device__ void finish_scores(const VerifyParams& p, const Tables& tb, int r, int dec) {
+__device__ void finish_scores(const VerifyParams& p, const Tables& tb, int r, int dec, int nslots) {
   if (wave_id() != 0) return;
   const int lane = lane_id();
   const int begin = tb.begin[r];
   const int K = tb.kflags[r] & 0xffff;
-  uint64_t* slots = p.score_slots + (int64_t)r * p.nc;
+  uint64_t* slots = p.score_slots + r * slot_stride(p);
   uint64_t v[kKeep];
-  bool failed = !wave_poll(p, slots, p.nc, v);
+  bool failed = !wave_poll(p, slots, nslots, v);
   int bad = 0;
 #pragma unroll
   for (int j = 0; j < kKeep; ++j) bad |= v[j] == kFailKey;
-  for (int c = lane + kKeep * kWave; c < p.nc; c += kWave) bad |= slot_load(slots + c) == kFailKey;
+  for (int c = lane + kKeep * kWave; c < nslots; c += kWave) bad |= slot_load(slots + c) == kFailKey;
   failed |= __any(bad) != 0;
   failed |= dec < 1 || dec > K + 1;
   const int first = failed ? K : dec - 1;
   int tok = -1;
-  if (!failed && first < K) tok = min(max(key_index(combine_keys(slots, p.nc, v)), 0), p.V - 1);
+  if (!failed && first < K) tok = min(max(key_index(combine_keys(slots, nslots, v)), 0), p.V - 1);
   int32_t* out = p.out + (int64_t)r * p.out_stride;
   for (int pos = lane; pos <= p.max_spec_len; pos += kWave) {
     int v = -1;
@@ -736,8 +752,9 @@ __device__ void finish_scores(const VerifyParams& p, const Tables& tb, int r, in
     else if (pos == K && first == K) v = p.bonus[r];
     out[pos] = v;
   }
-  wave_clear(slots, p.nc);
-  if (!failed && first < K) wave_clear(p.stat_slots + (int64_t)(begin + first) * p.nc, p.nc);
+  wave_clear(slots, nslots);
+  if (!failed && first < K)
+    wave_clear(p.stat_slots + (begin + first) * slot_stride(p), row_slot_count(p, tb, r, first));
   if (p.masks)
     for (int k = lane; k < K; k += kWave) p.masks[begin + k] = make_float4(0.f, 0.f, 0.f, 0.f);
   if (lane == 0) {
@@ -749,7 +766,10 @@ __device__ void finish_scores(const VerifyParams& p, const Tables& tb, int r, in
 // ------------------------------------------------------------------ tickets ----------
 // Unit order: the stats units of the groups in request order, with the score unit of kFull
 // request r inserted right after the stats unit of group (last group of r) + lag, or at the
-// end.  Unit u holds tickets u * nc .. u * nc + nc - 1 (chunk = ticket - u * nc).
+// end.  Units before the tail (position u < u0) hold nc tickets each, one per chunk; tail
+// units hold 2 nc tickets, one per half chunk, so that the launch ends with short tasks.  The
+// tail is the stats units of the last tail_groups groups and every score unit after the first
+// of them (with tail_groups = 0: the score units after the last stats unit).
 
 // Exclusive scan of one value per thread over the kVThreads-thread block: shuffle scans within
 // the waves, then one barrier for the wave totals.  Returns this thread's exclusive prefix;
@@ -819,17 +839,41 @@ __device__ inline void build_tables(const VerifyParams& p, Tables& tb, int* s_wa
   __syncthreads();
   tb.groups = groups;
   tb.nfull = nfull;
+  // Score unit k follows S_k = (fpos_k >> 12) - k stats units (non-decreasing in k).  The tail
+  // starts at stats unit gt; its score units are those with S_k > tau.
+  tb.gt = max(0, groups - p.tail_groups);
+  const int tau = p.tail_groups > 0 ? tb.gt : groups - 1;
+  int lo = 0, hi = nfull;  // kt = #{k : S_k <= tau}
+  while (lo < hi) {
+    const int mid = (lo + hi) / 2;
+    if ((tb.fpos[mid] >> 12) - mid <= tau) lo = mid + 1;
+    else hi = mid;
+  }
+  tb.kt = lo;
+  tb.u0 = tb.gt + tb.kt;
 }
 
 constexpr int kStatsTask = 1;
 constexpr int kScoreTask = 2;
 
-// Thread 0: decode ticket t into dst[0..7] = {t, chunk, kind, request, first row, rows |
-// groups << 8 | flags << 16 (stats) or K | flags << 16 (score), bits of c1, the request's
-// decision as read now (score units; 0 if not yet published)}.  kind 0: past the last unit.
+// Thread 0: decode ticket t into dst[0..7] = {t, slot (the chunk, or 2 * chunk + half in the
+// tail), kind | tail << 4, request, first row, rows | groups << 8 | flags << 16 (stats) or
+// K | flags << 16 (score), bits of c1, the request's decision as read now (score units; 0 if
+// not yet published)}.  kind 0: past the last unit.
 __device__ inline void fetch_task(const VerifyParams& p, const Tables& tb, int t, int* dst) {
   const int units = tb.groups + tb.nfull;
-  const int u = t / p.nc;
+  const int reg = tb.u0 * p.nc;
+  int u, part, tail;
+  if (t < reg) {
+    u = t / p.nc;
+    part = t - u * p.nc;
+    tail = 0;
+  } else {
+    const int q = (t - reg) / (2 * p.nc);
+    u = tb.u0 + q;
+    part = t - reg - q * 2 * p.nc;
+    tail = 1;
+  }
   int kind = 0, r = 0, row0 = 0, info = 0, dec = 0;
   if (u < units) {
     int lo = 0, hi = tb.nfull;  // score units at positions < u
@@ -863,13 +907,33 @@ __device__ inline void fetch_task(const VerifyParams& p, const Tables& tb, int t
     }
   }
   dst[0] = t;
-  dst[1] = t - u * p.nc;
-  dst[2] = kind;
+  dst[1] = part;
+  dst[2] = kind | tail << 4;
   dst[3] = r;
   dst[4] = row0;
   dst[5] = info;
   dst[6] = __float_as_int(tb.c1[r]);
   dst[7] = dec;
+}
+
+// Columns [v0, vend) of task slot `part`: chunk `part` in full, or in the tail half
+// part & 1 of chunk part >> 1, split at a score sub-chunk boundary (a half may be empty).
+template <int EPT>
+__device__ inline void task_columns(const VerifyParams& p, int part, bool tail, int64_t& v0,
+                                    int64_t& vend) {
+  const int c = tail ? part >> 1 : part;
+  const int64_t cs = (int64_t)c * p.chunk;
+  const int64_t ce = min((int64_t)p.V, cs + p.chunk);
+  if (!tail) {
+    v0 = cs;
+    vend = ce;
+    return;
+  }
+  constexpr int64_t SS = 2 * (int64_t)kVThreads * EPT;
+  const int64_t nsc = (ce - cs + SS - 1) / SS;
+  const int64_t mid = min(ce, cs + (nsc + 1) / 2 * SS);
+  v0 = (part & 1) ? mid : cs;
+  vend = (part & 1) ? ce : mid;
 }
 
 // ------------------------------------------------------------------ main kernel ------
@@ -896,7 +960,7 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
   if (tid == 0) tfirst = atomic_add_relaxed(ticket, 1);
   Tables tb{s_goff, s_begin, s_kf, s_c1, s_fpos, 0, 0};
   build_tables(p, tb, s_wave);
-  const int total = (tb.groups + tb.nfull) * p.nc;
+  const int total = tb.u0 * p.nc + (tb.groups + tb.nfull - tb.u0) * 2 * p.nc;
 
   // Every task is counted when it starts, with a relaxed atomic whose result is examined when
   // the task ends (its round trip overlaps the task).  The last task of a request to start
@@ -916,14 +980,15 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
     auto prefetch = [&]() {
       if (tid == 0) fetch_task(p, tb, tnext, s_info[par ^ 1]);
     };
-    const int kind = info[2];
+    const int kind = info[2] & 0xf;
+    const bool tail = info[2] >> 4;
     const int c = info[1];
     const int r = info[3];
     const int row0 = info[4];
     const int rinfo = info[5];
     const float c1 = __int_as_float(info[6]);
-    const int64_t v0 = (int64_t)c * p.chunk;
-    const int64_t vend = min((int64_t)p.V, v0 + p.chunk);
+    int64_t v0, vend;
+    task_columns<EPT>(p, c, tail, v0, vend);
     int started = 0;
     if (kind == kStatsTask) {
       const int nrows = rinfo & 0xff;
@@ -933,7 +998,10 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
         task_argmax<DT, EPT, G, MASKED>(p, c, row0, nrows, v0, vend, s_key, prefetch);
       else
         task_stats<DT, EPT, G, MASKED>(p, c, c1, row0, nrows, v0, vend, s_red, s_M, prefetch);
-      if (tid == 0) s_last = started == ngr * p.nc - 1;
+      // the request's stats tasks: nc per group, 2 nc per tail group
+      const int g0 = tb.goff[r], g1 = tb.goff[r + 1];
+      const int ntasks = p.nc * (ngr + max(0, g1 - max(g0, tb.gt)));
+      if (tid == 0) s_last = started == ntasks - 1;
       __syncthreads();
       if (s_last) decide_request(p, tb, r, dsm);
     } else if (kind == kScoreTask) {
@@ -961,20 +1029,22 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
         const int row = row0 + d - 1;
         const int draft = HAS_DRAFT ? -1 : p.draft_ids[row];
         bool ok;
-        key = task_score<DT, 2 * EPT, HAS_DRAFT, MASKED>(p, r, c1, row, draft, v0, vend, s_key,
-                                                         s_ml, ok, prefetch);
+        const int nslots = tb.goff[r] + (d - 1) / p.G >= tb.gt ? 2 * p.nc : p.nc;
+        key = task_score<DT, 2 * EPT, HAS_DRAFT, MASKED>(p, r, c1, row, nslots, draft, v0, vend,
+                                                         s_key, s_ml, ok, prefetch);
         if (!ok) key = kFailKey;
       } else {
         // every draft accepted, or no usable decision: nothing to score, but the slot tells
         // the finisher that this task has read the decision
         prefetch();
       }
+      const int ntasks = tail ? 2 * p.nc : p.nc;
       if (tid == 0) {
-        slot_store(p.score_slots + (int64_t)r * p.nc + c, key);
-        s_last = started == p.nc - 1;
+        slot_store(p.score_slots + r * slot_stride(p) + c, key);
+        s_last = started == ntasks - 1;
       }
       __syncthreads();
-      if (s_last) finish_scores(p, tb, r, d);
+      if (s_last) finish_scores(p, tb, r, d, ntasks);
     } else {
       prefetch();
     }
@@ -999,10 +1069,10 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
         int b, k;
         req_range(p, r, b, k);
         for (int j = 0; j < k; ++j) {
-          for (int c = 0; c < p.nc; ++c) slot_store(p.stat_slots + (int64_t)(b + j) * p.nc + c, 0);
+          for (int c = 0; c < slot_stride(p); ++c) slot_store(p.stat_slots + (b + j) * slot_stride(p) + c, 0);
           if (p.masks) p.masks[b + j] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        for (int c = 0; c < p.nc; ++c) slot_store(p.score_slots + (int64_t)r * p.nc + c, 0);
+        for (int c = 0; c < slot_stride(p); ++c) slot_store(p.score_slots + r * slot_stride(p) + c, 0);
         atomic_store_relaxed(&p.req_cnt[r], 0);
         atomic_store_relaxed(&p.score_cnt[r], 0);
         atomic_store_relaxed(&p.decision[r], 0);

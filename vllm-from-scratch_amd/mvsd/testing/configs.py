@@ -213,3 +213,41 @@ def algorithmic_bytes(w: Workload) -> int:
     total += P * 8 + P * 4 + 4 * len(ks) * 4
     total += len(ks) * (w.max_spec_len + 1) * 4
     return int(total)
+
+
+def kernel_bytes(w: Workload, outputs: list[list[int]], *, draft_none: bool = False,
+                 constrained_passes: int = 0) -> int:
+    """Bytes the verify kernel's algorithm must move for workload w, given the run's own output
+    (``parse_output`` lists): every verify row of the target once (softmax statistics or greedy
+    argmax); for each random request that rejects a draft, that one row's target, draft and
+    noise row once more (the recovered-token scores of the first rejected row, the only ones
+    the output uses); the per-row decision inputs (draft id, uniform, q[d], x[d]); the
+    per-request metadata; the output.  With sampling constraints, each constrained verify row
+    is read `constrained_passes` more times by the constraints kernel and its 16-byte row mask
+    is written and read."""
+    V = w.vocab_size
+    ks = np.asarray(w.num_draft_tokens)
+    if w.all_greedy:
+        greedy = np.ones(len(ks), dtype=bool)
+    else:
+        greedy = (w.temperature.cpu().numpy() == 0.0)
+    P = int(ks.sum())
+    t_size = w.target_logits.element_size()
+    d_size = 0 if (draft_none or w.draft_probs is None) else w.draft_probs.element_size()
+    rejected = sum(1 for r, out in enumerate(outputs)
+                   if ks[r] > 0 and not greedy[r] and len(out) <= ks[r])
+    total = P * V * t_size
+    total += rejected * V * (t_size + d_size + 4)
+    total += P * (4 + 8 + d_size + t_size)
+    total += len(ks) * 4 * 4
+    total += len(ks) * (w.max_spec_len + 1) * 4
+    if constrained_passes and (w.top_k is not None or w.top_p is not None):
+        on = np.zeros(len(ks), dtype=bool)
+        if w.top_k is not None:
+            on |= w.top_k.cpu().numpy() < V
+        if w.top_p is not None:
+            on |= w.top_p.cpu().numpy() < 1.0
+        # greedy rows of a batch with random requests are masked too (rejection_sampler.py:549-571)
+        rows = 0 if w.all_greedy else int(ks[on].sum())
+        total += rows * V * t_size * constrained_passes + P * 16 * 2
+    return int(total)
