@@ -137,6 +137,14 @@ typedef struct mvsd_rejection_args {
    * probability 0 and are never a greedy argmax, as the reference's -inf does. */
   const int64_t* top_k;                 /* [batch_size] */
   const float* top_p;                   /* [batch_size] */
+
+  /* Optional read-out (NULL = none), for tests and diagnostics; no counterpart in the
+   * reference.  [num_tokens, 3] fp32: for each verify row of a random request, the row's raw
+   * maximum M, its sum S of exp((x - M) / T) (as combined by the kernel), and the fp32
+   * probability of the draft token that the acceptance test compared, p[d] =
+   * exp(x_d / T - M / T) / S (0 where the sampling constraints mask d).  Rows of greedy
+   * requests are not written. */
+  float* debug_row_stats;
 } mvsd_rejection_args;
 
 /* Workspace contract: zero-filled before its first use (mvsd_rejection_workspace_init, or

@@ -105,6 +105,9 @@ class OracleResult:
     top1: np.ndarray                  # [P] best recovered score (nan when not computed)
     top2: np.ndarray                  # [P] second best recovered score
     greedy_rows: np.ndarray           # [P] bool
+    top1_p: np.ndarray | None = None  # [P] target probability at the best recovered index
+    top1_q: np.ndarray | None = None  # [P] draft probability there (0 for point-mass drafts)
+    top1_scale: np.ndarray | None = None  # [P] |x / T| + |max(x) / T| there (exponent scale)
 
 
 def rejection_sample(draft_token_ids, num_draft_tokens, max_spec_len, draft_probs,
@@ -134,6 +137,9 @@ def rejection_sample(draft_token_ids, num_draft_tokens, max_spec_len, draft_prob
     ratio_out = np.full(P, np.nan)
     top1 = np.full(P, np.nan)
     top2 = np.full(P, np.nan)
+    top1_p = np.full(P, np.nan)
+    top1_q = np.zeros(P)
+    top1_scale = np.zeros(P)
 
     argmax = torch.argmax(logits.to(torch.float32), dim=-1).numpy() if P else np.zeros(0, int)
     probs = None
@@ -151,6 +157,17 @@ def rejection_sample(draft_token_ids, num_draft_tokens, max_spec_len, draft_prob
             if V >= 2:
                 top = torch.topk(scores, 2, dim=-1).values.numpy()
                 top1, top2 = top[:, 0].astype(np.float64), top[:, 1].astype(np.float64)
+                rows = torch.arange(P)
+                ridx = torch.from_numpy(rec)
+                top1_p = probs[rows, ridx].to(torch.float64).numpy()
+                rt = row_temperatures(temps, num_draft_tokens, all_greedy, apply_temperature)
+                xs = logits.to(torch.float32)
+                if rt is not None:
+                    xs = xs / rt.unsqueeze(-1)
+                top1_scale = (xs[rows, ridx].abs() + xs.max(dim=-1).values.abs()).to(
+                    torch.float64).numpy()
+                if dp is not None:
+                    top1_q = dp[rows, ridx].to(torch.float64).numpy()
     rates = None if synthetic_rates is None else np.asarray(
         torch.as_tensor(synthetic_rates).cpu().numpy(), dtype=np.float32)
     dp_np = None if draft_probs is None else torch.as_tensor(draft_probs).cpu().to(
@@ -194,7 +211,7 @@ def rejection_sample(draft_token_ids, num_draft_tokens, max_spec_len, draft_prob
         if not rejected:
             out[r, k] = int(bonus[r])
         start += k
-    return OracleResult(out, ratio_out, u, top1, top2, greedy_rows)
+    return OracleResult(out, ratio_out, u, top1, top2, greedy_rows, top1_p, top1_q, top1_scale)
 
 
 @dataclass
@@ -206,14 +223,30 @@ class ParityReport:
     unexplained: list
 
 
+def recovered_window(p: float, q: float, scale: float = 0.0) -> float:
+    """Relative gap between the two best recovered scores below which fp32 rounding may swap
+    them.  Two fp32 softmax evaluations of one row (torch's exp(x / T - max) against the
+    kernel's exp2((x - M) log2(e) / T - log2 S), different summation orders) agree in p to
+    about 2^-22 (scale + |ln p| + 16) relative, where scale = |x / T| + |M / T|: the
+    exponent's absolute rounding error grows with the magnitudes rounded on the way (x / T is
+    rounded before the maximum is subtracted), and the normaliser's sum over the vocabulary
+    adds a few ulp.  The score (p - q) / E carries that error amplified by p / (p - q); both
+    candidates can move, hence the factor 2."""
+    if not (p > 0.0) or not (p > q):
+        return 0.0
+    eps = 2.0 ** -22 * (scale + abs(np.log(p)) + 16.0)
+    return 2.0 * eps * p / (p - q)
+
+
 def compare(out_device: np.ndarray, res: OracleResult, draft_token_ids, num_draft_tokens, *,
-            accept_tol: float = 1e-6, recovered_rel_tol: float = 1e-5) -> ParityReport:
+            accept_tol: float = 1e-6, recovered_rel_tol: float | None = None) -> ParityReport:
     """Compare device output with the oracle request by request.
 
     A mismatch is allowed only where the first differing position is
       * an accept/reject flip with |u - p/q| < accept_tol, or
-      * a rejection in both with different recovered ids whose top-2 scores are within
-        recovered_rel_tol (relative);
+      * a rejection in both with different recovered ids whose top-2 scores are within the
+        row's rounding window (``recovered_window`` of p and q at the best index; a fixed
+        relative ``recovered_rel_tol`` when given or when the oracle did not record p, q);
     and it is counted.  Greedy rows must match exactly.
     """
     out_device = np.asarray(out_device)
@@ -240,7 +273,12 @@ def compare(out_device: np.ndarray, res: OracleResult, draft_token_ids, num_draf
                                           f"ratio={res.ratio[row]!r}"))
                 else:
                     t1, t2 = res.top1[row], res.top2[row]
-                    if np.isfinite(t1) and t1 - t2 <= recovered_rel_tol * abs(t1):
+                    if recovered_rel_tol is not None or res.top1_p is None:
+                        tol = 1e-5 if recovered_rel_tol is None else recovered_rel_tol
+                    else:
+                        tol = recovered_window(float(res.top1_p[row]), float(res.top1_q[row]),
+                                               float(res.top1_scale[row]))
+                    if np.isfinite(t1) and t1 - t2 <= tol * abs(t1):
                         rec += 1
                     else:
                         bad.append((r, j, f"recovered {a[j]} vs {b[j]} top1={t1!r} top2={t2!r}"))

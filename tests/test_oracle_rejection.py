@@ -206,3 +206,44 @@ def test_compare_counts_only_near_ties():
     assert rep.accept_flips == 1 and not rep.unexplained
     rep = orc.compare(np.array([[4, -1]], dtype=np.int32), res, [7], [1])
     assert rep.unexplained
+
+
+def test_recovered_window_covers_fp32_softmax_disagreement():
+    """The near-tie window of oracle.compare assumes two fp32 evaluations of one softmax agree
+    to 2^-22 (|x / T| + |M / T| + |ln p| + 16) relative.  Check that on vocabulary-sized
+    rows: torch's fp32
+    softmax of x / T (the oracle) against an fp32 evaluation in the kernel's form, raw
+    maximum M, c1 = fl(log2(e) / T), S = sum of exp2((x - M) c1) in a different order, and
+    p = exp2((x - M) c1 - log2 S)."""
+    g = torch.Generator().manual_seed(77)
+    V = 151936
+    worst = 0.0
+    for T in (0.3, 0.8, 1.0, 1.5):
+        x = torch.randn(4, V, generator=g) * 2.0
+        p_torch = torch.softmax(x / T, dim=-1).double().numpy()
+        xf = x.numpy().astype(np.float32)
+        c1 = np.float32(1.4426950408889634 / T)
+        m = xf.max(axis=1, keepdims=True)
+        z = ((xf - m) * c1).astype(np.float32)
+        e = np.exp2(z).astype(np.float32)
+        # a different summation order: 512 interleaved partial sums, then combined
+        s = e.reshape(4, -1, 8).sum(axis=1, dtype=np.float32).sum(axis=1, dtype=np.float32)
+        nl = (-np.log2(s.astype(np.float64))).astype(np.float32)
+        p_kernel = np.exp2((z + nl[:, None]).astype(np.float32)).astype(np.float64)
+        big = p_torch >= 1e-30
+        rel = np.abs(p_kernel[big] / p_torch[big] - 1.0)
+        scale = (np.abs(xf / np.float32(T)) + np.abs(m / np.float32(T)))[big]
+        bound = 2.0 ** -22 * (scale + np.abs(np.log(p_torch[big])) + 16.0)
+        assert (rel <= bound).all(), (T, (rel / bound).max())
+        worst = max(worst, float((rel / bound).max()))
+    print(f"worst disagreement / window eps = {worst:.3f}")
+
+
+def test_recovered_window_shape():
+    from oracle.rejection import recovered_window
+    # point-mass drafts (q = 0): the p-error alone, twice
+    assert recovered_window(0.5, 0.0) == pytest.approx(2 * 2.0 ** -22 * (np.log(2) + 16))
+    # cancellation: q = 0.9 p amplifies by 10
+    assert recovered_window(0.1, 0.09) == pytest.approx(
+        10 * recovered_window(0.1, 0.0), rel=1e-9)
+    assert recovered_window(0.1, 0.1) == 0.0 and recovered_window(0.0, 0.0) == 0.0

@@ -269,6 +269,7 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
   p.masks = masked ? reinterpret_cast<float4*>(ws + lay.masks) : nullptr;
   p.stat_slots = reinterpret_cast<uint64_t*>(ws + lay.stat_slots);
   p.score_slots = reinterpret_cast<uint64_t*>(ws + lay.score_slots);
+  p.debug_row_stats = a->debug_row_stats;
 
   // The row masks of the whole batch, then one verify launch per kMaxLaunchRequests requests
   // (their tables live in LDS); the launches share the workspace, which each leaves zeroed.

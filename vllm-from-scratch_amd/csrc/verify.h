@@ -68,6 +68,9 @@ struct VerifyParams {
   const int64_t* top_k;  // [B]
   const float* top_p;    // [B]
   float4* masks;         // [P], null when no constraint applies
+  // Optional read-out [P, 3] of each random verify row as decided: raw max, sum of
+  // exp2((x - max) log2(e) / T), and the fp32 probability of the draft token.
+  float* debug_row_stats;
 };
 
 // Verify row j's row in the target tensor: target_rows[j] clamped to the tensor, or j.

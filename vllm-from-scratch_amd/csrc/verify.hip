@@ -587,7 +587,7 @@ __device__ inline PosInputs load_position(const VerifyParams& p, bool greedy, in
 // id tok and statistics (M, S).
 __device__ inline void decide_position(const VerifyParams& p, int r, bool greedy, int pos,
                                        const PosInputs& in, int tok, float M, float S,
-                                       bool& accepted, int& token) {
+                                       bool& accepted, int& token, float& pd_out) {
   const bool synthetic = p.synth != nullptr;
   const int d = in.d;
   if (greedy) {
@@ -613,6 +613,7 @@ __device__ inline void decide_position(const VerifyParams& p, int r, bool greedy
     float pd = expf(in.x / temp - M / temp) / S;
     if (p.masks && row_masked(in.mk, in.x, d)) pd = 0.f;  // -inf after the constraints
     accepted = in.q > 0.f && (double)(pd / in.q) >= in.u;
+    pd_out = pd;
   }
   token = accepted ? d : tok;
 }
@@ -681,9 +682,16 @@ __device__ void decide_request(const VerifyParams& p, const Tables& tb, int r, D
   bool accepted = true;
   if (tid < K) {
     int token;
+    float pd = NAN;
     const int tok = greedy ? sm.tok[tid] : (full ? -1 : in.rec);
-    decide_position(p, r, greedy, tid, in, tok, sm.M[tid], sm.S[tid], accepted, token);
+    decide_position(p, r, greedy, tid, in, tok, sm.M[tid], sm.S[tid], accepted, token, pd);
     sm.out_tok[tid] = token;
+    if (p.debug_row_stats && !greedy) {
+      float* o = p.debug_row_stats + 3 * (int64_t)(begin + tid);
+      o[0] = sm.M[tid];
+      o[1] = sm.S[tid];
+      o[2] = pd;
+    }
   }
   static_assert(kMaxSpecLen <= 2 * kWave && kVWaves >= 2, "positions live in waves 0 and 1");
   if (wave_id() < 2) {

@@ -70,6 +70,7 @@ class RejectionArgs(ctypes.Structure):
         ("workspace_bytes", c_int64),
         ("top_k", c_void_p),
         ("top_p", c_void_p),
+        ("debug_row_stats", c_void_p),
     ]
 
 

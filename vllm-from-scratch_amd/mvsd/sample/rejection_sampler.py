@@ -440,6 +440,7 @@ def rejection_sample(
     target_rows: torch.Tensor | None = None,
     apply_temperature: bool = False,
     apply_top_k_top_p: bool = False,
+    debug_row_stats: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Verify a batch of drafts; returns ``[B, max_spec_len + 1]`` int32, -1 padded.
 
@@ -451,7 +452,10 @@ def rejection_sample(
         kernel (greedy T = 0 -> 1), which together replace the gather + ``div_`` that
         RejectionSampler.forward runs before this function;
       * ``apply_top_k_top_p`` applies ``sampling_metadata.top_k`` / ``top_p`` to the (divided)
-        verify rows in the kernels, as ``apply_sampling_constraints`` (:563-571) would.
+        verify rows in the kernels, as ``apply_sampling_constraints`` (:563-571) would;
+      * ``debug_row_stats`` (a [P, 3] fp32 device tensor, diagnostics) receives, for each verify
+        row of a random request, the kernel's row maximum M, sum S of exp((x - M) / T) and the
+        fp32 p[d] its acceptance test compared.
     """
     assert draft_token_ids.ndim == 1
     assert draft_probs is None or draft_probs.ndim == 2
@@ -540,6 +544,11 @@ def rejection_sample(
         assert exp_noise.shape == (batch_size, vocab_size) and exp_noise.stride(1) == 1
     if target_logits.stride(1) != 1:
         target_logits = target_logits.contiguous()
+    if debug_row_stats is not None:
+        nat.require_device_tensor(debug_row_stats, "debug_row_stats")
+        if (debug_row_stats.dtype != torch.float32 or tuple(debug_row_stats.shape) != (num_tokens, 3)
+                or not debug_row_stats.is_contiguous()):
+            raise ValueError("debug_row_stats must be a contiguous [P, 3] float32 tensor")
 
     dtype = nat.dtype_code(target_logits.dtype)
     handle = nat.lib()
@@ -576,6 +585,7 @@ def rejection_sample(
         workspace_bytes=workspace.numel(),
         top_k=nat.ptr(top_k),
         top_p=nat.ptr(top_p),
+        debug_row_stats=nat.ptr(debug_row_stats),
     )
     nat.check(handle.mvsd_rejection_sample(args, nat.stream_of(device)), "mvsd_rejection_sample")
     return output_token_ids
