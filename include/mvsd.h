@@ -99,8 +99,9 @@ typedef struct mvsd_rejection_args {
   const int32_t* target_rows;
   int64_t target_num_rows;              /* rows addressable from target_logits (indices are clamped) */
 
-  /* draft probabilities [P, V], dtype F32 (other dtype codes return MVSD_E_INVALID), or NULL
-   * for point-mass drafts
+  /* draft probabilities [P, V], dtype F32, BF16 or F16 (upcast to fp32 in-kernel, as the
+   * reference's kernels load them in their own dtype, :797-806, :882-890), or NULL for
+   * point-mass drafts
    * (ngram: q[d] = 1, recovered distribution = p with the draft id removed, :793-795,:891-897) */
   const void* draft_probs;
   int draft_dtype;
@@ -325,7 +326,7 @@ int mvsd_apply_logits_processors(float* logits, int64_t stride, int64_t num_toke
 /* log-softmax (x - max) - log(sum exp(x - max)) of the row (logits_mode != 0: lp(x) = x): */
 /*   ids[n, 0] = token, lps[n, 0] = lp(x_token); ids / lps[n, 1 .. k] = the k largest lp    */
 /*   by (value desc, index asc); ranks[n] = #{i : lp(x_i) >= lp(x_token)};                  */
-/* n = r * width + j; ids / lps are [batch_size * width, k + 1].  0 <= k <= 32, k <= V.     */
+/* n = r * width + j; ids / lps are [batch_size * width, k + 1].  0 <= k <= V.                */
 /* ------------------------------------------------------------------------------------ */
 int mvsd_spec_logprobs(int32_t* ids, float* lps, int32_t* ranks, const float* target,
                        int64_t target_stride, const int32_t* target_rows, const float* bonus,

@@ -41,10 +41,21 @@ def gather_logprobs(logprobs: torch.Tensor, k: int, token_ids: torch.Tensor):
     return ids, lps, ranks.to(torch.int32)
 
 
+def rank_slack(logprobs: torch.Tensor, token_ids: torch.Tensor, ulps: int = 4) -> torch.Tensor:
+    """Per row, the entries other than the token whose value lies within `ulps` fp32 ulps of
+    the token's: the rank #{x >= x_token} may count them or not depending on the rounding of
+    two otherwise correct fp32 log-softmax evaluations, so a rank computed elsewhere may
+    differ from this one by at most that many."""
+    token_lp = logprobs.gather(-1, token_ids.to(torch.int64).unsqueeze(-1))
+    ulp = torch.nextafter(token_lp.abs(), torch.tensor(float("inf"))) - token_lp.abs()
+    near = (logprobs - token_lp).abs() <= ulps * ulp
+    return (near.sum(-1) - 1).clamp(min=0).to(torch.int32)
+
+
 def get_logprobs_tensors(k: int, cu_num_sampled_tokens, target_logits_indices,
                          bonus_logits_indices, target_rows: torch.Tensor,
                          bonus_rows: torch.Tensor, sampled_token_ids: torch.Tensor,
-                         logits_mode: bool = False):
+                         logits_mode: bool = False, return_slack: bool = False):
     target_rows = torch.as_tensor(target_rows).to(torch.float32).cpu()
     bonus_rows = torch.as_tensor(bonus_rows).to(torch.float32).cpu()
     t_idx = torch.as_tensor(target_logits_indices).cpu().to(torch.int64)
@@ -64,4 +75,7 @@ def get_logprobs_tensors(k: int, cu_num_sampled_tokens, target_logits_indices,
     tokens[tokens == PLACEHOLDER_TOKEN_ID] = 0
     rows = final[idx]
     lps = rows if logits_mode else compute_logprobs(rows)
-    return gather_logprobs(lps, k, tokens)
+    out = gather_logprobs(lps, k, tokens)
+    if return_slack:
+        return (*out, rank_slack(lps, tokens))
+    return out

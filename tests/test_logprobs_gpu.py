@@ -84,15 +84,25 @@ def test_reference_kats_on_device(case, device):
 
 
 def _check(got, want, label):
+    """ids exact; ranks exact except by at most the oracle's rank slack (entries within 4 ulp
+    of the sampled token's logprob, which either fp32 evaluation may round onto either side);
+    logprobs within 2e-6 absolute."""
     ids, lps, ranks = (x.cpu() for x in tuple(got)[:3])
-    wids, wlps, wranks = want
+    wids, wlps, wranks = want[:3]
     assert torch.equal(ids, wids), f"{label}: ids differ"
-    assert torch.equal(ranks, wranks), f"{label}: ranks differ"
+    if len(want) > 3 and not torch.equal(ranks, wranks):
+        diff = (ranks - wranks).abs()
+        slack = want[3]
+        assert (diff <= slack).all(), f"{label}: ranks differ beyond the rounding slack"
+        print(f"[{label}] {int((diff > 0).sum())} ranks differ within the rounding slack",
+              flush=True)
+    else:
+        assert torch.equal(ranks, wranks), f"{label}: ranks differ"
     assert torch.allclose(lps, wlps, atol=2e-6, rtol=1e-6), \
         f"{label}: max |diff| {float((lps - wlps).abs().max())}"
 
 
-@pytest.mark.parametrize("k", [0, 1, 5, 20, 32])
+@pytest.mark.parametrize("k", [0, 1, 5, 20, 32, 33, 50, 100])
 @pytest.mark.parametrize("V,mode", [(1000, "raw_logprobs"), (151936, "raw_logprobs"),
                                     (4096, "raw_logits"), (151936, "processed_logprobs")])
 def test_random_rows_match_oracle(device, k, V, mode):
@@ -109,7 +119,8 @@ def test_random_rows_match_oracle(device, k, V, mode):
     got = sampler._get_logprobs_tensors(k, meta, logits, target, bonus, sampled)
     want = olp.get_logprobs_tensors(k, meta.cu_num_sampled_tokens, meta.target_logits_indices,
                                     meta.bonus_logits_indices, target.cpu(), bonus.cpu(),
-                                    sampled.cpu(), logits_mode=mode.endswith("logits"))
+                                    sampled.cpu(), logits_mode=mode.endswith("logits"),
+                                    return_slack=True)
     _check(got, want, f"k={k} V={V} {mode}")
     # the raw modes can read the verify rows straight from the compact logits
     if mode.startswith("raw"):
@@ -189,3 +200,24 @@ def test_masked_rows_match_oracle(device, V):
                                     sampled.cpu())
     assert not torch.isnan(got.logprobs).any()
     _check(got, want, f"masked V={V}")
+
+
+@pytest.mark.parametrize("k,V", [(64, 64), (200, 257), (70, 151936)])
+def test_large_k_with_ties_match_oracle(device, k, V):
+    """k above one 32-key round (up to k = V), on rows with heavy ties, so that round
+    boundaries fall inside runs of equal values (order: value, then index)."""
+    rng = np.random.default_rng(k + V)
+    drafts = [list(rng.integers(0, V, n)) for n in [2, 3, 0, 1]]
+    meta = make_metadata(drafts, device=device)
+    B, W = len(drafts), meta.max_spec_len + 1
+    rows = meta.target_logits_indices.numel() + B
+    logits = torch.from_numpy(rng.integers(0, 5, (rows, V)).astype(np.float32)).to(device)
+    sampled = torch.from_numpy(rng.integers(-1, V, (B, W)).astype(np.int32)).to(device)
+    target = logits[meta.target_logits_indices]
+    bonus = logits[meta.bonus_logits_indices]
+    sampler = rs.RejectionSampler(BonusSampler("raw_logprobs"))
+    got = sampler._get_logprobs_tensors(k, meta, logits, target, bonus, sampled)
+    want = olp.get_logprobs_tensors(k, meta.cu_num_sampled_tokens, meta.target_logits_indices,
+                                    meta.bonus_logits_indices, target.cpu(), bonus.cpu(),
+                                    sampled.cpu(), logits_mode=False, return_slack=True)
+    _check(got, want, f"ties k={k} V={V}")

@@ -65,3 +65,12 @@ def test_closed_forms():
     # logits mode reports the values themselves
     ids, lps, ranks = olp.gather_logprobs(rows, 2, torch.tensor([0]))
     assert lps.tolist() == [[1.0, 3.0, 3.0]] and ranks.tolist() == [3]
+
+
+def test_rank_slack_counts_only_rounding_neighbours():
+    from oracle.logprobs import rank_slack
+    lp = torch.tensor([[-1.0, np.nextafter(np.float32(-1.0), np.float32(0)), -1.5, -1.0 - 1e-3]],
+                      dtype=torch.float32)
+    tok = torch.tensor([0])
+    assert rank_slack(lp, tok).tolist() == [1]       # the 1-ulp neighbour only
+    assert rank_slack(lp, torch.tensor([2])).tolist() == [0]

@@ -475,3 +475,17 @@ def test_corrected_reciprocal_equals_ieee_division(device):
     nat.check(nat.lib().mvsd_selftest(0, failures.data_ptr(), nat.stream_of(device)),
               "mvsd_selftest")
     assert int(failures.item()) == 0
+
+
+@pytest.mark.parametrize("ddtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", ["c2", "odd_v", "c4_bf16_target"])
+def test_16bit_draft_probs(device, ddtype, case):
+    """draft_probs in bf16 / fp16, upcast in the kernel (the reference's kernels load them in
+    their own dtype and compute in fp32, rejection_sampler.py:797-806, :882-890): against the
+    oracle on the same 16-bit values upcast.  fp32 targets take 8-byte draft loads, 16-bit
+    targets 16-byte loads; odd V takes the bounds-checked loads."""
+    w = {"c2": lambda: configs.random_c2(device, B=48, k=4, seed=301),
+         "odd_v": lambda: configs.random_c2(device, B=24, k=3, V=4097, seed=302),
+         "c4_bf16_target": lambda: configs.ragged_c4(device, B=96, seed=303)}[case]()
+    w = replace(w, draft_probs=w.draft_probs.to(ddtype))
+    check_parity(w, run_workload(w), oracle_for(w), f"{case} draft {ddtype}")

@@ -53,17 +53,19 @@ constexpr int64_t kStaticScratchBytes = 16ll << 20;
 std::atomic<int> g_wait_limit{mvsd::kSpinLimitDefault};
 
 // Resident-workgroup capacity of the verify kernel variant per device (CUs x occupancy).
-int verify_capacity(int device, int dtype, bool has_draft, bool masked) {
+int verify_capacity(int device, int dtype, int draft_dtype, bool masked) {
   static std::mutex mu;
-  static int cache[kMaxDevices][3][4];
-  if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2) return 0;
+  static int cache[kMaxDevices][3][4][2];
+  if (device < 0 || device >= kMaxDevices || dtype < 0 || dtype > 2 || draft_dtype < -1 ||
+      draft_dtype > 2)
+    return 0;
   std::lock_guard<std::mutex> lock(mu);
-  int& slot = cache[device][dtype][(masked ? 2 : 0) + (has_draft ? 1 : 0)];
+  int& slot = cache[device][dtype][draft_dtype + 1][masked ? 1 : 0];
   if (slot > 0) return slot;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     return 0;
-  const void* fn = mvsd::verify_kernel_ptr(dtype, has_draft, masked);
+  const void* fn = mvsd::verify_kernel_ptr(dtype, draft_dtype, masked);
   if (!fn) return 0;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, mvsd::kVThreads, 0) != hipSuccess)
@@ -200,7 +202,9 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
   if (P > 0 && (!a->target_logits || !a->draft_token_ids)) return MVSD_E_INVALID;
   if (a->target_dtype != MVSD_F32 && a->target_dtype != MVSD_BF16 && a->target_dtype != MVSD_F16)
     return MVSD_E_INVALID;
-  if (a->draft_probs && a->draft_dtype != MVSD_F32) return MVSD_E_INVALID;
+  if (a->draft_probs && a->draft_dtype != MVSD_F32 && a->draft_dtype != MVSD_BF16 &&
+      a->draft_dtype != MVSD_F16)
+    return MVSD_E_INVALID;
   if (!a->all_greedy && !a->temperature) return MVSD_E_INVALID;
   if (P > 0 && a->target_stride < V) return MVSD_E_INVALID;
   if (P > 0 && a->target_rows && a->target_num_rows < 1) return MVSD_E_INVALID;
@@ -224,7 +228,8 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
   int device = 0;
   hipError_t err = hipGetDevice(&device);
   if (err != hipSuccess) return hip_status(err);
-  const int cap = verify_capacity(device, a->target_dtype, a->draft_probs != nullptr, masked);
+  const int draft_dtype = a->draft_probs ? a->draft_dtype : -1;
+  const int cap = verify_capacity(device, a->target_dtype, draft_dtype, masked);
   if (cap <= 0) return hip_status(hipErrorInvalidDevice);
 
   char* ws = static_cast<char*>(ws_ptr);
@@ -236,8 +241,9 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
   p.target_stride = a->target_stride;
   p.target_rows = a->target_rows;
   p.target_num_rows = a->target_num_rows;
-  p.draft = static_cast<const float*>(a->draft_probs);
+  p.draft = a->draft_probs;
   p.draft_stride = a->draft_stride;
+  p.draft_dtype = draft_dtype;
   p.noise = a->exp_noise;
   p.noise_stride = a->noise_stride;
   p.uniforms = a->uniform_probs;
@@ -258,7 +264,8 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
   p.spin_limit = g_wait_limit.load();
   const int esz = elem_size(a->target_dtype);
   p.target_aligned = aligned16(a->target_logits, a->target_stride * esz);
-  p.draft_aligned = a->draft_probs ? aligned16(a->draft_probs, a->draft_stride * 4) : false;
+  p.draft_aligned =
+      a->draft_probs ? aligned16(a->draft_probs, a->draft_stride * elem_size(draft_dtype)) : false;
   p.noise_aligned = a->exp_noise ? aligned16(a->exp_noise, a->noise_stride * 4) : false;
   p.ctrl = reinterpret_cast<int*>(ws + lay.ctrl);
   p.req_cnt = reinterpret_cast<int*>(ws + lay.req_cnt);
@@ -424,7 +431,7 @@ int mvsd_spec_logprobs(int32_t* ids, float* lps, int32_t* ranks, const float* ta
   if (batch_size < 0 || num_tokens < 0 || vocab_size <= 0 || width < 0 || k < 0)
     return MVSD_E_INVALID;
   if (batch_size == 0 || width == 0) return MVSD_OK;
-  if (k > mvsd::logprobs_max_k() || k > vocab_size) return MVSD_E_RANGE;
+  if (k > vocab_size) return MVSD_E_RANGE;
   if (batch_size * width > 0x7fffffff || num_tokens > 0x7fffffff || vocab_size > 0x7fffffff)
     return MVSD_E_RANGE;
   if (!ids || !lps || !ranks || !bonus || !cu_num_sampled_tokens || !sampled_token_ids)

@@ -23,7 +23,6 @@ struct LogprobParams {
 };
 
 // Largest k the kernel supports.
-int logprobs_max_k();
 hipError_t launch_spec_logprobs(const LogprobParams& p, hipStream_t stream);
 
 }  // namespace mvsd

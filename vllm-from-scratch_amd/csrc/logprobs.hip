@@ -14,7 +14,8 @@
 //   rank = #{i : lp(x_i) >= lp(x_token)}.
 // One 512-thread workgroup per position: pass 1 reduces (M, S); pass 2 keeps per-thread lists
 // of the KMAX largest (value, index) keys, counts the rank, then merges the lists per wave and
-// across waves by k rounds of key maxima.
+// across waves by rounds of key maxima.  For k > KMAX, pass 2 repeats over the keys below the
+// last one found, KMAX at a time (ceil(k / 32) passes for k > 8).
 #include "logprobs.h"
 #include "mvsd_device.h"
 
@@ -31,6 +32,7 @@ __global__ __launch_bounds__(kLpThreads) void spec_logprobs_kernel(LogprobParams
   __shared__ float s_m[kLpWaves], s_s[kLpWaves];
   __shared__ uint64_t s_cand[kLpWaves * KMAX];
   __shared__ int s_cnt[kLpWaves];
+  __shared__ uint64_t s_bound;
   const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
   const int n = blockIdx.x;  // position r * W + j
   const int r = n / p.W, j = n - r * p.W;
@@ -88,88 +90,106 @@ __global__ __launch_bounds__(kLpThreads) void spec_logprobs_kernel(LogprobParams
   auto lp = [&](float v) { return p.logits_mode ? v : (v - lpm) - L; };
   const float tlp = lp(x[token]);
 
-  // ---- pass 2: per-thread top-KMAX keys and the rank count ----
-  uint64_t key[KMAX];
-#pragma unroll
-  for (int i = 0; i < KMAX; ++i) key[i] = 0;
-  int cnt = 0;
-  for (int i = tid; i < p.V; i += kLpThreads) {
-    const float v = lp(x[i]);
-    cnt += v >= tlp ? 1 : 0;
-    uint64_t k = argmax_key(v, i);
-    if (k > key[KMAX - 1]) {
-      // insertion into the descending list (one compare-exchange step per slot)
-#pragma unroll
-      for (int s2 = 0; s2 < KMAX; ++s2) {
-        const uint64_t a = key[s2];
-        const bool sw = k > a;
-        key[s2] = sw ? k : a;
-        k = sw ? a : k;
-      }
-    }
-  }
-  // rank: block sum of the counts
-  int c2 = cnt;
-  for (int off = kWave / 2; off > 0; off >>= 1) c2 += __shfl_xor(c2, off, kWave);
-  if (lane == 0) s_cnt[wid] = c2;
-
-  // per-wave merge: k rounds, the lane holding the largest head pops it
+  // ---- pass 2 (repeated): per-thread top-KMAX keys below `bound`, and the rank count ----
+  // Round t collects the next min(KMAX, k - done) largest keys strictly below the last key of
+  // round t - 1; keys are distinct (the index is in the low word), so the rounds partition
+  // the top-k exactly.
   const int k = p.k;
-  for (int round = 0; round < k; ++round) {
-    const uint64_t best = wave_max_u64(key[0]);
-    if (lane == 0) s_cand[wid * KMAX + round] = best;
-    if (key[0] == best && best != 0) {  // keys are distinct (index in the low word)
-#pragma unroll
-      for (int s2 = 0; s2 + 1 < KMAX; ++s2) key[s2] = key[s2 + 1];
-      key[KMAX - 1] = 0;
-    }
-  }
-  __syncthreads();
-  // block merge by wave 0: lanes hold the waves' sorted candidate lists
   const int n_out = k + 1;
-  if (wid == 0) {
-    constexpr int PER = (kLpWaves * KMAX + kWave - 1) / kWave;
-    uint64_t cand[PER];
+  uint64_t bound = ~0ull;
+  int done = 0;
+  bool first_pass = true;
+  while (first_pass || done < k) {
+    const int need = min(KMAX, k - done);
+    uint64_t key[KMAX];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int ci = lane * PER + i;
-      cand[i] = ci < kLpWaves * KMAX && (ci % KMAX) < k ? s_cand[ci] : 0;
-    }
-    // sort each lane's few candidates (descending)
+    for (int i = 0; i < KMAX; ++i) key[i] = 0;
+    int cnt = 0;
+    for (int i = tid; i < p.V; i += kLpThreads) {
+      const float v = lp(x[i]);
+      cnt += v >= tlp ? 1 : 0;
+      uint64_t kk = argmax_key(v, i);
+      if (kk < bound && kk > key[KMAX - 1]) {
+        // insertion into the descending list (one compare-exchange step per slot)
 #pragma unroll
-    for (int a = 0; a < PER; ++a)
-#pragma unroll
-      for (int b = a + 1; b < PER; ++b) {
-        const uint64_t hi2 = umax_key(cand[a], cand[b]);
-        const uint64_t lo2 = cand[a] ^ cand[b] ^ hi2;
-        cand[a] = hi2;
-        cand[b] = lo2;
+        for (int s2 = 0; s2 < KMAX; ++s2) {
+          const uint64_t a = key[s2];
+          const bool sw = kk > a;
+          key[s2] = sw ? kk : a;
+          kk = sw ? a : kk;
+        }
       }
-    for (int round = 0; round < k; ++round) {
-      const uint64_t best = wave_max_u64(cand[0]);
+    }
+    if (first_pass) {
+      // rank: block sum of the counts
+      int c2 = cnt;
+      for (int off = kWave / 2; off > 0; off >>= 1) c2 += __shfl_xor(c2, off, kWave);
+      if (lane == 0) s_cnt[wid] = c2;
+    }
+
+    // per-wave merge: `need` rounds, the lane holding the largest head pops it
+    for (int round = 0; round < need; ++round) {
+      const uint64_t best = wave_max_u64(key[0]);
+      if (lane == 0) s_cand[wid * KMAX + round] = best;
+      if (key[0] == best && best != 0) {
+#pragma unroll
+        for (int s2 = 0; s2 + 1 < KMAX; ++s2) key[s2] = key[s2 + 1];
+        key[KMAX - 1] = 0;
+      }
+    }
+    __syncthreads();
+    // block merge by wave 0: lanes hold the waves' sorted candidate lists
+    if (wid == 0) {
+      constexpr int PER = (kLpWaves * KMAX + kWave - 1) / kWave;
+      uint64_t cand[PER];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int ci = lane * PER + i;
+        cand[i] = ci < kLpWaves * KMAX && (ci % KMAX) < need ? s_cand[ci] : 0;
+      }
+      // sort each lane's few candidates (descending)
+#pragma unroll
+      for (int a = 0; a < PER; ++a)
+#pragma unroll
+        for (int b = a + 1; b < PER; ++b) {
+          const uint64_t hi2 = umax_key(cand[a], cand[b]);
+          const uint64_t lo2 = cand[a] ^ cand[b] ^ hi2;
+          cand[a] = hi2;
+          cand[b] = lo2;
+        }
+      uint64_t last = bound;
+      for (int round = 0; round < need; ++round) {
+        const uint64_t best = wave_max_u64(cand[0]);
+        if (lane == 0) {
+          // the value is recomputed from the index (the key's order bits merge -0.0 and +0.0)
+          const int idx = min(max(key_index(best), 0), p.V - 1);
+          p.ids[(int64_t)n * n_out + 1 + done + round] = idx;
+          p.lps[(int64_t)n * n_out + 1 + done + round] = lp(x[idx]);
+        }
+        last = best;
+        if (cand[0] == best && best != 0) {
+#pragma unroll
+          for (int s2 = 0; s2 + 1 < PER; ++s2) cand[s2] = cand[s2 + 1];
+          cand[PER - 1] = 0;
+        }
+      }
       if (lane == 0) {
-        // the value is recomputed from the index (the key's order bits merge -0.0 and +0.0)
-        const int idx = min(max(key_index(best), 0), p.V - 1);
-        p.ids[(int64_t)n * n_out + 1 + round] = idx;
-        p.lps[(int64_t)n * n_out + 1 + round] = lp(x[idx]);
-      }
-      if (cand[0] == best && best != 0) {
-#pragma unroll
-        for (int s2 = 0; s2 + 1 < PER; ++s2) cand[s2] = cand[s2 + 1];
-        cand[PER - 1] = 0;
+        s_bound = last;
+        if (first_pass) {
+          int rank = 0;
+          for (int w = 0; w < kLpWaves; ++w) rank += s_cnt[w];
+          p.ids[(int64_t)n * n_out] = token;
+          p.lps[(int64_t)n * n_out] = tlp;
+          p.ranks[n] = rank;
+        }
       }
     }
-    if (lane == 0) {
-      int rank = 0;
-      for (int w = 0; w < kLpWaves; ++w) rank += s_cnt[w];
-      p.ids[(int64_t)n * n_out] = token;
-      p.lps[(int64_t)n * n_out] = tlp;
-      p.ranks[n] = rank;
-    }
+    __syncthreads();
+    bound = s_bound;
+    done += need;
+    first_pass = false;
   }
 }
-
-int logprobs_max_k() { return 32; }
 
 hipError_t launch_spec_logprobs(const LogprobParams& p, hipStream_t stream) {
   const int n = p.B * p.W;

@@ -26,8 +26,9 @@ struct VerifyParams {
   int64_t target_stride;
   const int32_t* target_rows;
   int64_t target_num_rows;
-  const float* draft;
+  const void* draft;     // [P, V] draft probabilities (dtype draft_dtype), or null
   int64_t draft_stride;
+  int draft_dtype;
   const float* noise;
   int64_t noise_stride;
   const double* uniforms;
@@ -110,8 +111,9 @@ struct VerifyPlan {
 // cap = resident workgroups.
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int cap);
 
-// The verify kernel variant for a target dtype, draft presence and sampling constraints.
-const void* verify_kernel_ptr(int target_dtype, bool has_draft, bool masked);
+// The verify kernel variant for a target dtype, draft dtype (-1: point-mass drafts) and
+// sampling constraints.
+const void* verify_kernel_ptr(int target_dtype, int draft_dtype, bool masked);
 hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream);
 hipError_t launch_verify(const VerifyParams& params, int target_dtype, int grid,
                          hipStream_t stream);

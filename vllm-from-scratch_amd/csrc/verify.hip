@@ -197,6 +197,67 @@ __device__ inline void load_raw_f32(const float* __restrict__ base, int64_t s0, 
   }
 }
 
+// Draft probabilities of a thread's EPT elements in one sub-chunk, in the target's column
+// layout: fp32 (one word per element) or bf16 / fp16 (two per word), upcast when consumed.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+template <int DD, int EPT>
+struct DraftBuf {
+  static constexpr int kWords = DD == MVSD_F32 ? EPT : EPT / 2;
+  uint32_t w[kWords];
+};
+
+template <int DD>
+__device__ inline float draft_elem(const uint32_t* w, int k) {
+  if constexpr (DD == MVSD_F32) {
+    return __uint_as_float(w[k]);
+  } else {
+    const uint16_t h = (uint16_t)(w[k / 2] >> (16 * (k % 2)));
+    return Elem<DD>::cvt(__builtin_bit_cast(typename Elem<DD>::storage, h));
+  }
+}
+
+// Draft sub-chunk for the columns of the DT layout; FAST: full and aligned, else
+// bounds-checked (columns at or past vend read as 0).
+template <int DT, int DD, int EPT, bool FAST>
+__device__ inline void load_draft(const void* base_v, int64_t s0, int64_t vend, bool aligned,
+                                  DraftBuf<DD, EPT>& q) {
+  constexpr int VEC = Elem<DT>::kVec;
+  if constexpr (DD == MVSD_F32) {
+    u32x4 raw[EPT / 4];
+    load_raw_f32<DT, EPT, FAST>(static_cast<const float*>(base_v), s0, vend, aligned, 0.f, raw);
+#pragma unroll
+    for (int m = 0; m < EPT / 4; ++m)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q.w[4 * m + j] = raw[m][j];
+  } else {
+    using S = typename Elem<DD>::storage;
+    const S* base = static_cast<const S*>(base_v);
+#pragma unroll
+    for (int i = 0; i < EPT / VEC; ++i) {
+      const int64_t col = vec_col<DT>(s0, i);
+      if (FAST || (aligned && col + VEC <= vend)) {
+        if constexpr (VEC == 4) {
+          const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(base + col));
+          q.w[2 * i] = v[0];
+          q.w[2 * i + 1] = v[1];
+        } else {
+          const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + col));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) q.w[4 * i + j] = v[j];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC / 2; ++j) {
+          const uint32_t lo = col + 2 * j < vend ? bits16(base[col + 2 * j]) : 0u;
+          const uint32_t hi = col + 2 * j + 1 < vend ? bits16(base[col + 2 * j + 1]) : 0u;
+          q.w[i * (VEC / 2) + j] = lo | hi << 16;
+        }
+      }
+    }
+  }
+}
+
 // Walk [v0, vend) in SUB-column sub-chunks: load(buf, s0, Fast<bool>) issues a sub-chunk's
 // loads, body(buf, s0, Fast<bool>) consumes them.  hook() runs once, after the first loads
 // are issued.  Unaligned inputs and the partial last sub-chunk take the checked path.
@@ -463,10 +524,10 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
 }
 
 // ------------------------------------------------------------------ score tasks ------
-template <int DT, int EPT>
+template <int DT, int DD, int EPT>
 struct ScoreBuf {
   u32x4 x[EPT / Elem<DT>::kVec];
-  u32x4 q[EPT / 4];
+  DraftBuf<DD < 0 ? MVSD_F32 : DD, DD < 0 ? 4 : EPT> q;  // unused without draft probs
   u32x4 e[EPT / 4];
 };
 
@@ -475,14 +536,17 @@ struct ScoreBuf {
 // statistics come from its nslots stats slots, polled by wave 0 while the first sub-chunk
 // loads.
 // Returns the chunk's argmax key in thread 0; ok = false if the statistics wait gave up.
-template <int DT, int EPT, bool HAS_DRAFT, bool MASKED, typename Hook>
+template <int DT, int EPT, int DD, bool MASKED, typename Hook>
 __device__ inline uint64_t task_score(const VerifyParams& p, int r, float c1, int row, int nslots,
                                       int d, int64_t v0, int64_t vend, uint64_t* s_key,
                                       float* s_ml, bool& ok, Hook&& after_loads) {
   using S = typename Elem<DT>::storage;
-  using Buf = ScoreBuf<DT, EPT>;
+  using Buf = ScoreBuf<DT, DD, EPT>;
+  constexpr bool HAS_DRAFT = DD >= 0;
+  constexpr int DE = DD == MVSD_F32 ? 4 : 2;  // draft element bytes
   const S* tb = static_cast<const S*>(p.target) + target_row(p, row) * p.target_stride;
-  const float* qb = HAS_DRAFT ? p.draft + (int64_t)row * p.draft_stride : nullptr;
+  const void* qb = HAS_DRAFT ? static_cast<const char*>(p.draft) + (int64_t)row * p.draft_stride * DE
+                             : nullptr;
   const float* eb = p.noise + (int64_t)r * p.noise_stride;
   const float4 mk = MASKED ? p.masks[row] : make_float4(0.f, 0.f, 0.f, 0.f);
   const bool aligned = p.target_aligned && p.noise_aligned && (p.draft_aligned || !HAS_DRAFT);
@@ -491,7 +555,7 @@ __device__ inline uint64_t task_score(const VerifyParams& p, int r, float c1, in
     constexpr bool F = decltype(fast)::value;
     if constexpr (F) load_raw<DT, EPT, true>(tb, s0, buf.x);
     else load_raw_checked<DT, EPT, true>(tb, s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x);
-    if constexpr (HAS_DRAFT) load_raw_f32<DT, EPT, F>(qb, s0, vend, p.draft_aligned, 0.f, buf.q);
+    if constexpr (HAS_DRAFT) load_draft<DT, DD, EPT, F>(qb, s0, vend, p.draft_aligned, buf.q);
     load_raw_f32<DT, EPT, F>(eb, s0, vend, p.noise_aligned, 1.f, buf.e);
   };
 
@@ -531,7 +595,7 @@ __device__ inline uint64_t task_score(const VerifyParams& p, int r, float c1, in
       float prob = __builtin_amdgcn_exp2f(fmaf(x - MX, c1, NL));  // softmax
       if constexpr (MASKED) prob = row_masked(mk, x, idx) ? 0.f : prob;
       float w;
-      if constexpr (HAS_DRAFT) w = prob - raw_f32(buf.q, k);  // clamp folded into bv >= 0
+      if constexpr (HAS_DRAFT) w = prob - draft_elem<DD>(buf.q.w, k);  // clamp folded into bv >= 0
       else w = idx == d ? 0.f : prob;
       const float score = w * inv[k];
       // columns rise with s0 and k, so a strict compare keeps the first maximum
@@ -568,7 +632,12 @@ __device__ inline PosInputs load_position(const VerifyParams& p, bool greedy, in
   const bool synthetic = p.synth != nullptr;
   if (!greedy || synthetic) in.u = p.uniforms[row];
   if (!greedy && !synthetic && in.d >= 0 && in.d < p.V) {
-    if (p.draft) in.q = p.draft[row * p.draft_stride + in.d];
+    if (p.draft) {
+      const int64_t at = row * p.draft_stride + in.d;
+      if (p.draft_dtype == MVSD_F32) in.q = static_cast<const float*>(p.draft)[at];
+      else if (p.draft_dtype == MVSD_BF16) in.q = Elem<MVSD_BF16>::cvt(static_cast<const uint16_t*>(p.draft)[at]);
+      else in.q = Elem<MVSD_F16>::cvt(static_cast<const _Float16*>(p.draft)[at]);
+    }
     const int64_t trow = target_row(p, (int)row);
     if (p.target_dtype == MVSD_F32) {
       in.x = static_cast<const float*>(p.target)[trow * p.target_stride + in.d];
@@ -945,7 +1014,9 @@ __device__ inline void task_columns(const VerifyParams& p, int part, bool tail, 
 }
 
 // ------------------------------------------------------------------ main kernel ------
-template <int DT, int EPT, int G, bool HAS_DRAFT, bool MASKED>
+// DD: the draft probabilities' dtype (MVSD_F32, MVSD_BF16, MVSD_F16), or -1 for point-mass
+// drafts.
+template <int DT, int EPT, int G, int DD, bool MASKED>
 __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
   static_assert(EPT % Elem<DT>::kVec == 0, "EPT must be a multiple of the vector width");
   __shared__ float s_red[G * kVWaves];
@@ -1035,10 +1106,10 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
       if (d >= 1 && d <= K) {
         // rejection at position d - 1: score this chunk of that row
         const int row = row0 + d - 1;
-        const int draft = HAS_DRAFT ? -1 : p.draft_ids[row];
+        const int draft = DD >= 0 ? -1 : p.draft_ids[row];
         bool ok;
         const int nslots = tb.goff[r] + (d - 1) / p.G >= tb.gt ? 2 * p.nc : p.nc;
-        key = task_score<DT, 2 * EPT, HAS_DRAFT, MASKED>(p, r, c1, row, nslots, draft, v0, vend,
+        key = task_score<DT, 2 * EPT, DD, MASKED>(p, r, c1, row, nslots, draft, v0, vend,
                                                          s_key, s_ml, ok, prefetch);
         if (!ok) key = kFailKey;
       } else {
@@ -1150,21 +1221,28 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int 
   return plan;
 }
 
-template <int DT>
-const void* kernel_for(bool has_draft, bool masked) {
+template <int DT, bool MASKED>
+const void* kernel_for_mask(int draft_dtype) {
   constexpr int E = ept_of<DT>();
-  if (masked)
-    return has_draft ? reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, true, true>)
-                     : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false, true>);
-  return has_draft ? reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, true, false>)
-                   : reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, false, false>);
+  switch (draft_dtype) {
+    case -1: return reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, -1, MASKED>);
+    case MVSD_F32: return reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, MVSD_F32, MASKED>);
+    case MVSD_BF16: return reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, MVSD_BF16, MASKED>);
+    case MVSD_F16: return reinterpret_cast<const void*>(&verify_kernel<DT, E, kGroup, MVSD_F16, MASKED>);
+    default: return nullptr;
+  }
 }
 
-const void* verify_kernel_ptr(int target_dtype, bool has_draft, bool masked) {
+template <int DT>
+const void* kernel_for(int draft_dtype, bool masked) {
+  return masked ? kernel_for_mask<DT, true>(draft_dtype) : kernel_for_mask<DT, false>(draft_dtype);
+}
+
+const void* verify_kernel_ptr(int target_dtype, int draft_dtype, bool masked) {
   switch (target_dtype) {
-    case MVSD_F32: return kernel_for<MVSD_F32>(has_draft, masked);
-    case MVSD_BF16: return kernel_for<MVSD_BF16>(has_draft, masked);
-    case MVSD_F16: return kernel_for<MVSD_F16>(has_draft, masked);
+    case MVSD_F32: return kernel_for<MVSD_F32>(draft_dtype, masked);
+    case MVSD_BF16: return kernel_for<MVSD_BF16>(draft_dtype, masked);
+    case MVSD_F16: return kernel_for<MVSD_F16>(draft_dtype, masked);
     default: return nullptr;
   }
 }
@@ -1172,7 +1250,8 @@ const void* verify_kernel_ptr(int target_dtype, bool has_draft, bool masked) {
 hipError_t launch_verify(const VerifyParams& params, int target_dtype, int grid,
                          hipStream_t stream) {
   if (params.B == 0) return hipSuccess;
-  const void* fn = verify_kernel_ptr(target_dtype, params.draft != nullptr, params.masks != nullptr);
+  const void* fn = verify_kernel_ptr(target_dtype, params.draft ? params.draft_dtype : -1,
+                                     params.masks != nullptr);
   if (!fn) return hipErrorInvalidValue;
   void* args[] = {const_cast<VerifyParams*>(&params)};
   hipError_t err = hipLaunchKernel(fn, dim3(grid), dim3(kVThreads), args, 0, stream);

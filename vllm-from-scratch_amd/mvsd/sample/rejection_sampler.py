@@ -189,8 +189,8 @@ class RejectionSampler:
         B, W = sampled_token_ids.shape
         V = int(bonus_logits.shape[-1])
         num_tokens = int(metadata.draft_token_ids.shape[0])
-        if not 0 <= max_num_logprobs <= min(LOGPROBS_MAX_K, V):
-            raise ValueError(f"logprobs={max_num_logprobs} outside [0, {min(LOGPROBS_MAX_K, V)}]")
+        if not 0 <= max_num_logprobs <= V:
+            raise ValueError(f"logprobs={max_num_logprobs} outside [0, {V}]")
         keep = []
         rows = None
         if target_logits is None:
@@ -536,8 +536,10 @@ def rejection_sample(
         recovered_token_ids = _as(recovered_token_ids, torch.int32, device)
     if draft_probs is not None:
         nat.require_device_tensor(draft_probs, "draft_probs")
-        if draft_probs.dtype != torch.float32:
-            raise TypeError(f"draft_probs must be float32, got {draft_probs.dtype}")
+        # the reference's kernels load draft_probs in its own dtype and compute in fp32
+        # (:797-806, :882-890); 16-bit probabilities are upcast exactly in the kernel
+        if draft_probs.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise TypeError(f"draft_probs dtype {draft_probs.dtype} is not supported")
         assert draft_probs.shape == (num_tokens, vocab_size)
     if exp_noise is not None:
         exp_noise = _as(exp_noise, torch.float32, device)
@@ -564,7 +566,7 @@ def rejection_sample(
         target_rows=nat.ptr(rows),
         target_num_rows=target_logits.shape[0],
         draft_probs=nat.ptr(draft_probs),
-        draft_dtype=nat.F32,
+        draft_dtype=nat.dtype_code(draft_probs.dtype) if draft_probs is not None else nat.F32,
         draft_stride=draft_probs.stride(0) if draft_probs is not None else 0,
         exp_noise=nat.ptr(exp_noise),
         noise_stride=exp_noise.stride(0) if exp_noise is not None else 0,
@@ -759,9 +761,6 @@ _SAMPLE_RECOVERED_TOKENS = sample_recovered_tokens
 
 
 # --------------------------------------------------------------------------- helpers
-
-# Largest logprobs=k of the speculative path (the kernel's per-thread candidate lists).
-LOGPROBS_MAX_K = 32
 
 # One zero-initialised verification workspace per (device, stream).  The kernel leaves it
 # zeroed after every call (include/mvsd.h), so it is reused without clearing; it only grows.
