@@ -360,10 +360,11 @@ int mvsd_sampler_rows(int op, int32_t* ids, float* out, int64_t out_stride, floa
 int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
-/* v2_rejection_sample — the V2 model runner's verification, non-block path.              */
+/* v2_rejection_sample — the V2 model runner's verification, standard or block.          */
 /* Replaces: rejection_sample (minivllm/worker/gpu/spec_decode/rejection_sampler_utils.py: */
-/*           935-1201) with use_block_verification=False: _compute_local_logits_stats_     */
-/*           kernel (:206-316), _rejection_kernel (:497-706), _resample_kernel (:709-866), */
+/*           935-1201): _compute_local_logits_stats_kernel (:206-316),                    */
+/*           _compute_cumulative_log_p_kernel (:318-384), _compute_local_residual_mass_     */
+/*           kernel (:387-446), _rejection_kernel (:497-706), _resample_kernel (:709-866), */
 /*           _insert_resampled_kernel (:869-932), and the counter draws of                  */
 /*           minivllm/worker/gpu/sample/gumbel.py:72-131 (Philox4x32-10, as Triton's        */
 /*           tl.randint4x / tl.rand).                                                       */
@@ -371,13 +372,16 @@ int mvsd_selftest(int test, uint64_t* failures, mvsd_stream_t stream);
 /* reference assumes); draft_logits [states, K, V] pre-temperature or NULL; draft_sampled  */
 /* [num_logits] int32 (entry j+1 is the draft at row j); cu_num_logits [num_reqs + 1]      */
 /* int32 with a leading 0; pos [num_logits] int64; idx_mapping [num_reqs] and              */
-/* expanded_idx_mapping / expanded_local_pos [num_logits] int32; temperature [states] f32; */
-/* seed [states] int64; synthetic_conditional_rates [K] f32 or NULL.  Writes sampled       */
-/* [num_reqs, >= K+1] int64 (entries at or past num_sampled[r] are left as they were) and  */
-/* num_sampled [num_reqs] int32.  workspace: mvsd_v2_workspace_bytes() bytes, 256-byte    */
-/* aligned, caller-owned, no initial contents needed.  Draft ids >= V count as invalid     */
-/* (the reference does not check them); a request whose cu_num_logits span is empty, out  */
-/* of range or longer than K+1 gets num_sampled 0.                                          */
+/* expanded_idx_mapping / expanded_local_pos [num_logits] int32 (row j of request r has    */
+/* state idx_mapping[r] and local position j - cu_num_logits[r], as the V2 runner builds   */
+/* them); temperature [states] f32; seed [states] int64; synthetic_conditional_rates [K]   */
+/* f32 or NULL.  use_block_verification selects block verification (Sun et al. 2024) for  */
+/* random requests; it cannot be combined with synthetic rates (MVSD_E_INVALID).  Writes   */
+/* sampled [num_reqs, >= K+1] int64 (entries at or past num_sampled[r] are left as they    */
+/* were, or hold a rejected draft) and num_sampled [num_reqs] int32.  workspace:           */
+/* mvsd_v2_workspace_bytes() bytes, 256-byte aligned, caller-owned, no initial contents    */
+/* needed.  Draft ids >= V count as invalid (the reference does not check them); a request */
+/* whose cu_num_logits span is empty, out of range or longer than K+1 gets num_sampled 0.  */
 /* ------------------------------------------------------------------------------------ */
 int64_t mvsd_v2_workspace_bytes(int64_t num_logits, int64_t num_reqs, int64_t vocab_size);
 
@@ -389,7 +393,8 @@ int mvsd_v2_rejection_sample(
     const int32_t* expanded_idx_mapping, const int32_t* expanded_local_pos,
     const float* temperature, const int64_t* seed, int64_t num_req_states, int64_t num_reqs,
     int64_t vocab_size, int32_t num_speculative_steps, const float* synthetic_conditional_rates,
-    int use_fp64, void* workspace, int64_t workspace_bytes, mvsd_stream_t stream);
+    int use_fp64, int use_block_verification, void* workspace, int64_t workspace_bytes,
+    mvsd_stream_t stream);
 
 #ifdef __cplusplus
 }

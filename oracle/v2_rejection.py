@@ -128,17 +128,156 @@ def _lse(maxes, sums):
     return np.float32(g + np.log(np.float32((sums * np.exp(maxes - g)).sum(dtype=np.float32))))
 
 
+class Stats:
+    """Per-block statistics of every verify row (rejection_sampler_utils.py:206-316): the
+    greedy rows' (max, first argmax), the random rows' (max, sum exp) of the target row and of
+    the temperature-scaled draft row."""
+
+    def __init__(self, t, dl, exp_idx, exp_local, temp_all, K, V):
+        num_logits = t.shape[0]
+        nb = -(-V // STATS_BLOCK)
+        self.tmax = np.full((num_logits, nb), -np.inf, np.float32)
+        self.targ = np.zeros((num_logits, nb), np.int64)
+        self.tsum = np.zeros((num_logits, nb), np.float32)
+        self.dmax = np.full((num_logits, nb), -np.inf, np.float32)
+        self.dsum = np.zeros((num_logits, nb), np.float32)
+        for row in range(num_logits):
+            step = int(exp_local[row])
+            if step >= K:
+                continue
+            st = int(exp_idx[row])
+            tt = temp_all[st]
+            for b in range(nb):
+                blk = t[row, b * STATS_BLOCK:min(V, (b + 1) * STATS_BLOCK)]
+                if tt == 0.0:
+                    j = int(np.argmax(blk))
+                    self.tmax[row, b], self.targ[row, b] = blk[j], b * STATS_BLOCK + j
+                else:
+                    self.tmax[row, b], self.tsum[row, b] = _max_sumexp(blk)
+                    if dl is not None:
+                        cols = slice(b * STATS_BLOCK, min(V, (b + 1) * STATS_BLOCK))
+                        d = (dl[st, step, cols] / tt).astype(np.float32)
+                        self.dmax[row, b], self.dsum[row, b] = _max_sumexp(d)
+
+    def target_lse(self, row):
+        return _lse(self.tmax[row], self.tsum[row])
+
+    def draft_lse(self, row):
+        return _lse(self.dmax[row], self.dsum[row])
+
+
+def _valid(d, V):
+    """A draft id the chain verifies: -1 is the reference's placeholder; ids >= V are treated
+    as placeholders too (the HIP path refuses to read past the row)."""
+    return 0 <= d < V
+
+
+def _logprobs_at(t, dl, stats, row, st, step, tt, tok):
+    """(log p(tok), log q(tok)) of verify row ``row`` (rejection_sampler_utils.py:134-203);
+    log q = 0 for one-hot drafts."""
+    tlp = np.float32(t[row, tok] - stats.target_lse(row))
+    if dl is None:
+        return tlp, np.float32(0.0)
+    return tlp, np.float32(np.float32(dl[st, step, tok] / tt) - stats.draft_lse(row))
+
+
+def cumulative_log_p(t, dl, ds, cu, idx_mapping, temp_all, stats, V):
+    """log of the running joint ratio, _compute_cumulative_log_p_kernel
+    (rejection_sampler_utils.py:318-384): for every random request, row start + i holds
+    min(log p_i + log p(d) - log q(d), 0) after draft i; placeholder drafts carry the value.
+    Rows of greedy requests and bonus rows stay NaN (never read)."""
+    cum = np.full(t.shape[0], np.nan, np.float32)
+    for r in range(cu.shape[0] - 1):
+        st = int(idx_mapping[r])
+        tt = temp_all[st]
+        if tt == 0.0:
+            continue
+        start, end = int(cu[r]), int(cu[r + 1])
+        log_p = np.float32(0.0)
+        for step in range(end - start - 1):
+            li = start + step
+            d = int(ds[li + 1])
+            if _valid(d, V):
+                tlp, dlp = _logprobs_at(t, dl, stats, li, st, step, tt, d)
+                log_p = np.float32(min(np.float32(log_p + np.float32(tlp - dlp)), np.float32(0.0)))
+            cum[li] = log_p
+    return cum
+
+
+def local_residual_mass(t, dl, ds, cum, exp_idx, exp_local, temp_all, K, stats, V):
+    """Residual mass sum_x max(p_i M_b(x) - M_s(x), 0) of the rows that the block threshold
+    looks ahead to, _compute_local_residual_mass_kernel (rejection_sampler_utils.py:387-446),
+    summed over the reference's 8192-column blocks in fp32 as _compute_global_residual_mass
+    does (:60-85).  Only rows at draft step 1..K-1 whose own draft is verifiable, of random
+    requests; other rows stay NaN."""
+    num_logits = t.shape[0]
+    mass = np.full(num_logits, np.nan, np.float32)
+    nb = -(-V // STATS_BLOCK)
+    for row in range(num_logits):
+        step = int(exp_local[row])
+        if step == 0 or step >= K or row + 1 >= num_logits or not _valid(int(ds[row + 1]), V):
+            continue
+        st = int(exp_idx[row])
+        tt = temp_all[st]
+        if tt == 0.0:
+            continue
+        prefix = np.float32(np.exp(cum[row - 1]))
+        t_lse, d_lse = stats.target_lse(row), stats.draft_lse(row)
+        total = np.float32(0.0)
+        for b in range(nb):
+            cols = slice(b * STATS_BLOCK, min(V, (b + 1) * STATS_BLOCK))
+            m_b = np.exp((t[row, cols] - t_lse).astype(np.float32)).astype(np.float32)
+            d = (dl[st, step, cols] / tt).astype(np.float32)
+            m_s = np.exp((d - d_lse).astype(np.float32)).astype(np.float32)
+            part = np.maximum((prefix * m_b - m_s).astype(np.float32), np.float32(0.0))
+            total = np.float32(total + part.sum(dtype=np.float32))
+        mass[row] = total
+    return mass
+
+
+def block_threshold(prefix, residual_mass):
+    """Acceptance threshold h of a block position with a verifiable next draft
+    (rejection_sampler_utils.py:633-634): R / (R + 1 - p_i), or 1 when that denominator is
+    not positive (p_i = 1 and R = 0: the draft equals the target)."""
+    prefix, residual_mass = np.float32(prefix), np.float32(residual_mass)
+    denom = np.float32(np.float32(residual_mass + np.float32(1.0)) - prefix)
+    return np.float32(residual_mass / denom) if denom > 0.0 else np.float32(1.0)
+
+
+def residual_logits(row, rej, t_lse=0.0, d_row=None, d_lse=0.0, log_p_tau=0.0):
+    """Logits the rejected row is resampled from (rejection_sampler_utils.py:800-842).
+    ``row`` is the target row [V]; ``d_row`` the temperature-scaled draft row or None
+    (one-hot drafts); ``rej`` the rejected draft id, or a negative value for the bonus row or
+    a placeholder (then the target row itself).  With draft logits the result is
+    log max(p_tau p - q, 0), where ``log_p_tau`` is 0 outside block verification."""
+    row = np.asarray(row, dtype=np.float32)
+    V = row.shape[0]
+    if rej < 0:
+        return row
+    if d_row is None:
+        return np.where(np.arange(V) != rej, row, -np.inf).astype(np.float32)
+    tlp = ((row - np.float32(t_lse)).astype(np.float32) + np.float32(log_p_tau)).astype(np.float32)
+    dlp = (np.asarray(d_row, dtype=np.float32) - np.float32(d_lse)).astype(np.float32)
+    ratio = np.exp(dlp - tlp).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return np.where(ratio < 1.0, tlp + np.log1p(-ratio), -np.inf).astype(np.float32)
+
+
 def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, pos, idx_mapping,
                      expanded_idx_mapping, expanded_local_pos, temperature, seed,
                      num_speculative_steps: int, synthetic_conditional_rates=None,
-                     use_fp64: bool = False, return_margins: bool = False):
-    """V2 ``rejection_sample`` (non-block) on numpy arrays.
+                     use_fp64: bool = False, use_block_verification: bool = False,
+                     return_margins: bool = False, return_details: bool = False):
+    """V2 ``rejection_sample`` on numpy arrays, standard or block verification.
 
     Returns ``(sampled [R, K+1] int64, num_sampled [R] int32)`` where entries at or past
     ``num_sampled[r]`` are -1 (the reference leaves them undefined).  With ``return_margins``
-    also returns, per request, the list of acceptance margins |log p - log u - log q| of the
-    random steps that were decided, and the gap between the best and second-best resampled
-    scores (a near-tie measure)."""
+    also returns, per request, the list of decision margins of the random steps that were
+    decided (|log p - log u - log q| for the standard test, |u - h| for the block test), and
+    the gap between the best and second-best resampled scores (a near-tie measure).  With
+    ``return_details`` (block verification) the last element returned is a dict with the
+    per-request thresholds ``h``, the ``cumulative_log_p`` and ``residual_mass`` arrays and
+    the ``stats``."""
     t = np.asarray(target_logits, dtype=np.float32)
     num_logits, V = t.shape
     dl = None if draft_logits is None else np.asarray(draft_logits, dtype=np.float32)
@@ -151,37 +290,25 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
     seed_all = np.asarray(seed).astype(np.int64)
     K = int(num_speculative_steps)
     R = cu.shape[0] - 1
-    nb = -(-V // STATS_BLOCK)
+    rates = None if synthetic_conditional_rates is None else np.asarray(
+        synthetic_conditional_rates, dtype=np.float32)
+    block = bool(use_block_verification)
+    if block:
+        assert rates is None, "Block verification is incompatible with synthetic acceptance rates."
 
-    # Per-block statistics (rejection_sampler_utils.py:206-316).
-    tmax = np.full((num_logits, nb), -np.inf, np.float32)
-    targ = np.zeros((num_logits, nb), np.int64)
-    tsum = np.zeros((num_logits, nb), np.float32)
-    dmax = np.full((num_logits, nb), -np.inf, np.float32)
-    dsum = np.zeros((num_logits, nb), np.float32)
-    for row in range(num_logits):
-        step = int(expanded_local_pos[row])
-        if step >= K:
-            continue
-        st = int(expanded_idx_mapping[row])
-        tt = temp_all[st]
-        for b in range(nb):
-            blk = t[row, b * STATS_BLOCK:min(V, (b + 1) * STATS_BLOCK)]
-            if tt == 0.0:
-                j = int(np.argmax(blk))
-                tmax[row, b], targ[row, b] = blk[j], b * STATS_BLOCK + j
-            else:
-                tmax[row, b], tsum[row, b] = _max_sumexp(blk)
-                if dl is not None:
-                    d = (dl[st, step, b * STATS_BLOCK:min(V, (b + 1) * STATS_BLOCK)] / tt).astype(np.float32)
-                    dmax[row, b], dsum[row, b] = _max_sumexp(d)
+    stats = Stats(t, dl, expanded_idx_mapping, expanded_local_pos, temp_all, K, V)
+    cum = mass = None
+    if block:
+        cum = cumulative_log_p(t, dl, ds, cu, idx_mapping, temp_all, stats, V)
+        if dl is not None:
+            mass = local_residual_mass(t, dl, ds, cum, expanded_idx_mapping,
+                                       expanded_local_pos, temp_all, K, stats, V)
 
     sampled = np.full((R, K + 1), -1, np.int64)
     num_sampled = np.zeros(R, np.int32)
     margins = [[] for _ in range(R)]
+    thresholds = [[] for _ in range(R)]
     gaps = np.full(R, np.inf)
-    rates = None if synthetic_conditional_rates is None else np.asarray(
-        synthetic_conditional_rates, dtype=np.float32)
     for r in range(R):
         st = int(idx_mapping[r])
         start, end = int(cu[r]), int(cu[r + 1])
@@ -193,26 +320,46 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
         for i in range(nd):
             li = start + i
             d = int(ds[li + 1])
-            valid = d >= 0
-            d = max(0, d)
+            valid = _valid(d, V)
+            d = d if valid else 0
             if not greedy:
                 verifying &= valid
             if not verifying:
                 continue
             u = tl_rand32(s, np.int64(pos[li]))
             if greedy:
-                m = np.where(np.isnan(tmax[li]), -np.inf, tmax[li])
-                am = int(targ[li, int(np.argmax(m))])
+                m = np.where(np.isnan(stats.tmax[li]), -np.inf, stats.tmax[li])
+                am = int(stats.targ[li, int(np.argmax(m))])
                 ok = (u < rates[i]) if rates is not None else (am == d)
                 ok = bool(ok) and valid
                 verifying = ok
                 acc += ok
                 sampled[r, i] = d if ok else am
+            elif block:
+                # Block verification (:608-640): accept i + 1 tokens when u <= h; the last
+                # position that passes decides.
+                prefix = np.float32(np.exp(cum[li]))
+                nxt = int(ds[li + 2]) if i < nd - 1 else -1
+                if _valid(nxt, V):
+                    if dl is not None:
+                        res = mass[li + 1]
+                    else:
+                        # one-hot drafts: p_i (1 - M_b(next)) in closed form (:87-104)
+                        m_b = np.float32(np.exp(np.float32(t[li + 1, nxt] - stats.target_lse(li + 1))))
+                        res = np.float32(prefix * np.float32(1.0 - m_b))
+                    h = block_threshold(prefix, res)
+                else:
+                    h = prefix
+                thresholds[r].append(float(h))
+                margins[r].append(abs(float(u) - float(h)))
+                if u <= h:
+                    acc = i + 1
+                sampled[r, i] = d
             else:
-                t_lse = _lse(tmax[li], tsum[li])
+                t_lse = stats.target_lse(li)
                 tlp = np.float32(t[li, d] - t_lse)
                 if dl is not None:
-                    d_lse = _lse(dmax[li], dsum[li])
+                    d_lse = stats.draft_lse(li)
                     dlp = np.float32(np.float32(dl[st, i, d] / tt) - d_lse)
                 else:
                     dlp, d_lse = np.float32(0.0), np.float32(0.0)
@@ -226,6 +373,10 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
                 acc += ok
                 sampled[r, i] = d
         num_sampled[r] = acc
+        if block and not greedy and acc < nd:
+            # (:683-700) the statistics of the row the block rejected
+            t_lse = stats.target_lse(start + acc)
+            d_lse = stats.draft_lse(start + acc) if dl is not None else np.float32(0.0)
 
         # Resample the rejected or bonus row (:709-866) and insert it (:869-932).
         ri = start + acc
@@ -233,19 +384,11 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
         if greedy and not is_bonus:
             num_sampled[r] = acc + 1
             continue
-        rej = int(ds[ri + 1]) if not is_bonus else 0
-        row = t[ri, :V]
-        if is_bonus or rej < 0:
-            resid = row
-        elif dl is not None:
-            d = (dl[st, acc, :V] / tt).astype(np.float32)
-            tlp = (row - t_lse).astype(np.float32)
-            dlp = (d - d_lse).astype(np.float32)
-            ratio = np.exp(dlp - tlp).astype(np.float32)
-            with np.errstate(divide="ignore", invalid="ignore"):
-                resid = np.where(ratio < 1.0, tlp + np.log1p(-ratio), -np.inf).astype(np.float32)
-        else:
-            resid = np.where(np.arange(V) != rej, row, -np.inf).astype(np.float32)
+        rej = int(ds[ri + 1]) if not is_bonus else -1
+        rej = rej if _valid(rej, V) else -1
+        d_row = None if (dl is None or rej < 0) else (dl[st, acc, :V] / tt).astype(np.float32)
+        log_p_tau = np.float32(cum[ri - 1]) if (block and acc > 0) else np.float32(0.0)
+        resid = residual_logits(t[ri, :V], rej, t_lse, d_row, d_lse, log_p_tau)
         tok, _ = gumbel_argmax(resid, int(s), int(pos[ri]), float(tt), use_fp64)
         if return_margins and tt != 0.0:
             x = np.asarray(resid, dtype=np.float64)
@@ -261,6 +404,9 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
                 gaps[r] = float(top2[1] - top2[0])
         sampled[r, acc] = tok
         num_sampled[r] = acc + 1
+    out = (sampled, num_sampled)
     if return_margins:
-        return sampled, num_sampled, margins, gaps
-    return sampled, num_sampled
+        out = out + (margins, gaps)
+    if return_details:
+        out = out + (dict(h=thresholds, cumulative_log_p=cum, residual_mass=mass, stats=stats),)
+    return out

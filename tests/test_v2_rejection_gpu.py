@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import v2_rejection as o
-from v2_cases import make_case, oracle_args
+from v2_cases import make_case, oracle_args, repeat_case
 
 pytestmark = pytest.mark.gpu
 
@@ -98,12 +98,72 @@ def test_odd_vocab_and_unaligned_rows():
     _compare(case, "odd vocab")
 
 
-def test_block_verification_raises():
-    from mvsd.worker.gpu.spec_decode import rejection_sample
-    case = make_case([1], [1.0], 1, 64, seed=1)
-    dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
-    with pytest.raises(NotImplementedError):
-        rejection_sample(**dev, use_block_verification=True)
+@pytest.mark.parametrize("use_fp64", [False, True])
+def test_block_with_draft_logits(use_fp64):
+    temps = [0.8, 1.0, 0.0, 1.3, 0.5, 0.0, 1.0, 0.9]
+    case = make_case([4, 4, 4, 2, 4, 0, 3, 4], temps, 4, V, seed=7, invalid={(6, 2)})
+    _compare(case, f"block draft_logits fp64={use_fp64}", use_fp64=use_fp64,
+             use_block_verification=True)
+
+
+def test_block_one_hot_drafts():
+    temps = [0.8, 1.0, 0.0, 1.2, 0.6, 1.0]
+    case = make_case([3, 3, 3, 3, 1, 3], temps, 3, V, seed=9, draft_logits=False,
+                     invalid={(5, 2)})
+    _compare(case, "block one-hot drafts", use_block_verification=True)
+
+
+def test_block_bf16_logits():
+    temps = [0.8, 1.0, 0.0, 1.3]
+    case = make_case([4, 4, 4, 4], temps, 4, V, seed=13, dtype=torch.bfloat16)
+    _compare(case, "block bf16 target and draft", use_block_verification=True)
+
+
+@pytest.mark.parametrize("draft_logits", [True, False])
+def test_block_ragged_batch_many_requests(draft_logits):
+    g = np.random.default_rng(22)
+    R, K = 48, 6
+    nd = [int(x) for x in g.integers(0, K + 1, R)]
+    temps = [0.0 if x < 0.3 else float(x) for x in g.uniform(0.0, 1.5, R)]
+    invalid = {(r, int(g.integers(0, K))) for r in range(0, R, 7)}
+    case = make_case(nd, temps, K, V, seed=22, states=64, draft_logits=draft_logits,
+                     invalid=invalid)
+    _compare(case, f"block ragged 48 requests draft_logits={draft_logits}",
+             use_block_verification=True)
+
+
+def test_block_hand_case_many_seeds():
+    """The residual design of tests/step75/test_block_verification.py:80-95 (V = 8, K = 2,
+    p_tau < 1 at tau = 1) drawn 512 times: every request matches the oracle, every acceptance
+    length occurs, and the block residual differs from the standard one on the same draws."""
+    target = [[0.0] * 8, [1.0, 0.5, 0.0, -1.0, 0.0, 0.5, 1.5, 0.0],
+              [4.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0]]
+    draft = [[0.0, 0.6, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0],
+             [0.0, 0.0, 0.0, 2.0, 0.0, 0.0, 0.0, 0.0]]
+    case = repeat_case(target, draft, [1, 3], 1.0, 512, seed=75)
+    s, n, _, _ = _compare(case, "block hand case x512", use_block_verification=True)
+    assert set(n.tolist()) == {1, 2, 3}
+    s_std, n_std = _run(case)
+    assert (n != n_std).any()
+
+
+@pytest.mark.parametrize("block", [False, True])
+def test_chains_longer_than_a_wavefront(block):
+    """K = 100 > 64 steps: the chain decides in pages of one step per lane.  Greedy requests
+    whose drafts are all the argmax accept all 100 and cross the page boundary."""
+    Vs = 4096 + 3
+    temps = [0.0, 0.9, 1.0, 0.0, 0.7]
+    case = make_case([100, 100, 70, 65, 100], temps, 100, Vs, seed=41, greedy_match=1.0)
+    s, n, es, en = _compare(case, f"K=100 block={block}", use_block_verification=block)
+    assert n[0] == 101 and n[3] == 66
+
+
+def test_block_and_standard_differ():
+    temps = [0.9] * 16
+    case = make_case([4] * 16, temps, 4, 4096, seed=43)
+    _, n_blk = _run(case, use_block_verification=True)
+    _, n_std = _run(case)
+    assert (n_blk != n_std).any()
 
 
 def test_no_host_synchronisation():

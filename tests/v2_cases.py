@@ -66,3 +66,28 @@ def oracle_args(case):
         else:
             out[k] = v
     return out
+
+
+def repeat_case(target, draft, tokens, temp, n, *, seed=0):
+    """``n`` requests with the same rows (target [K+1, V], draft [K, V] or None, draft ids
+    ``tokens``) and temperature, each with its own state, seed and positions: n independent
+    draws of one design (the layout of tests/step75/test_block_verification.py:176-204)."""
+    target = torch.as_tensor(np.asarray(target, np.float32))
+    K = len(tokens)
+    rows = K + 1
+    g = torch.Generator().manual_seed(seed)
+    ds = torch.zeros(n * rows, dtype=torch.int32)
+    for i, tok in enumerate(tokens):
+        ds[i + 1::rows] = tok
+    return dict(
+        target_logits=target.repeat(n, 1).contiguous(),
+        draft_logits=None if draft is None else
+        torch.as_tensor(np.asarray(draft, np.float32))[None].repeat(n, 1, 1).contiguous(),
+        draft_sampled=ds, cu_num_logits=torch.arange(0, (n + 1) * rows, rows, dtype=torch.int32),
+        pos=torch.arange(n * rows, dtype=torch.int64) + 100,
+        idx_mapping=torch.arange(n, dtype=torch.int32),
+        expanded_idx_mapping=torch.arange(n, dtype=torch.int32).repeat_interleave(rows),
+        expanded_local_pos=torch.arange(rows, dtype=torch.int32).repeat(n),
+        temperature=torch.full((n,), float(temp)),
+        seed=torch.randint(0, 2**62, (n,), generator=g, dtype=torch.int64),
+        num_speculative_steps=K)

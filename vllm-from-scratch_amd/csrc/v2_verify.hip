@@ -1,26 +1,33 @@
 // V2 speculative-decoding verification (the V2 model runner's rejection sampler) for gfx950.
 //
 // Replaces rejection_sample (minivllm/worker/gpu/spec_decode/rejection_sampler_utils.py:935-1201),
-// non-block path, with four launches on the caller's stream:
+// standard and block verification, with these launches on the caller's stream:
 //   1. v2_stats_kernel     one workgroup per (verify row, 4096-column chunk): greedy rows keep
 //                          the chunk's (max, first argmax); random rows keep (max, sum exp) of
 //                          the target row and of the temperature-scaled draft row (:206-316);
-//   2. v2_chain_kernel     one wavefront per request walks its draft chain (:497-706): the
-//                          chunk partials are combined across lanes, the acceptance uniform
-//                          is drawn from the request's counter stream at the row's position;
-//   3. v2_resample_kernel  one workgroup per (request, chunk) scores the rejected (or bonus)
-//                          row: residual log-probabilities log(p - q) (or the target row, or
-//                          the target row without the rejected draft) plus Gumbel noise drawn
+//   2. v2_rowstat_kernel   one wavefront per verify row combines the chunk partials: a greedy
+//                          row's argmax; a random row's target and draft log-sum-exp and the
+//                          log-probabilities of the row's draft token (:134-203);
+//   3. v2_residual_kernel  block verification with draft logits only: one workgroup per
+//                          (verify row, chunk) sums max(p_i M_b(x) - M_s(x), 0) over the chunk,
+//                          p_i the running joint ratio of the rows before it (:318-446);
+//   4. v2_chain_kernel     one wavefront per request decides its chain (:497-706): the
+//                          per-step inputs and acceptance uniforms are loaded and drawn one step
+//                          per lane, the decisions then run in order over the lanes;
+//   5. v2_resample_kernel  one workgroup per (request, chunk) scores the rejected (or bonus)
+//                          row: residual log-probabilities log(p_tau p - q) (or the target row,
+//                          or the target row without the rejected draft) plus Gumbel noise drawn
 //                          per vocabulary index (:709-866, gumbel.py:95-131);
-//   4. v2_insert_kernel    one wavefront per request takes the first chunk maximum and writes
+//   6. v2_insert_kernel    one wavefront per request takes the first chunk maximum and writes
 //                          the resampled token and the sampled count (:869-932).
 // The counter stream is Philox4x32 with ten rounds keyed by the 64-bit seed and counted by
 // the 64-bit position (or the 32-bit vocabulary index), the generator behind Triton's
 // tl.randint4x / tl.rand that gumbel.py:72-91 uses (Salmon et al., SC 2011).
 //
 // HBM traffic per call: every verify row of the target once (and the draft row of random
-// requests once) in pass 1, one target row (and one draft row) per request in pass 3; the
-// partials are a few hundred bytes per row.
+// requests once) in pass 1, again in pass 3 for block verification with draft logits, one
+// target row (and one draft row) per request in pass 5; the partials are a few hundred bytes
+// per row.
 
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -109,12 +116,18 @@ struct V2Params {
   int64_t num_logits;
   int32_t num_reqs, num_states, vocab, K, nchunks;
   int use_fp64;
+  int use_block;  // block verification (Sun et al. 2024) instead of the per-token test
   bool target_aligned, draft_aligned;
   // workspace
-  float *tmax, *tsum, *dmax, *dsum;
+  float *tmax, *tsum, *dmax, *dsum;  // [num_logits, nchunks] chunk partials
   int32_t* targ;
+  float *rtl, *rdl;      // [num_logits] target / draft log-sum-exp of a random verify row
+  float *rtlp, *rdlp;    // [num_logits] log p and log q of the row's draft token
+  int32_t* rarg;         // [num_logits] target argmax of a greedy verify row
+  float* rmass;          // [num_logits, nchunks] block residual-mass partials
   int32_t* acc;  // accepted length per request, -1 for a malformed request
-  float *tlse, *dlse;
+  float *tlse, *dlse;    // [num_reqs] log-sum-exp of the rejected row
+  float* lpt;            // [num_reqs] log p_tau: the joint ratio of the accepted block
   double* rval;
   int32_t* ridx;
 };
@@ -253,7 +266,113 @@ __device__ inline float wave_lse(const float* maxes, const float* sums, int64_t 
   return gm + logf(s);
 }
 
+__device__ inline bool draft_valid(int d, int vocab) { return d >= 0 && d < vocab; }
+
+// Per verify row: the greedy row's global argmax (first index among equal maxima,
+// :106-131), or the random row's log-sum-exps and the log-probabilities of its draft token
+// (:134-203).  Draft ids outside [0, V) are placeholders; their log-probabilities are
+// written from column 0 and never read.
 template <int TDT, int DDT, bool HAS_DRAFT>
+__global__ __launch_bounds__(kThreads) void v2_rowstat_kernel(V2Params p) {
+  const int64_t row = (int64_t)blockIdx.x * kWaves + wave_id();
+  if (row >= p.num_logits) return;
+  const int step = p.exp_local_pos[row];
+  if (step < 0 || step >= p.K) return;
+  const int st = clamp_state(p.exp_idx_mapping[row], p.num_states);
+  const float temp = p.temperature[st];
+  const int64_t base = row * p.nchunks;
+  if (temp == 0.f) {
+    float bv = -INFINITY;
+    int bc = 0x7fffffff;
+    for (int c = lane_id(); c < p.nchunks; c += kWave) {
+      float v = p.tmax[base + c];
+      v = v != v ? -INFINITY : v;
+      argmax_update(bv, bc, v, c, true);
+    }
+    wave_argmax(bv, bc);
+    if (lane_id() == 0) p.rarg[row] = p.targ[base + (bc == 0x7fffffff ? 0 : bc)];
+    return;
+  }
+  int d = row + 1 < p.num_logits ? p.draft_sampled[row + 1] : -1;
+  d = draft_valid(d, p.vocab) ? d : 0;
+  using TS = typename Elem<TDT>::storage;
+  const float xt = Elem<TDT>::cvt(reinterpret_cast<const TS*>(p.target)[row * p.target_stride + d]);
+  float xd = 0.f;
+  if constexpr (HAS_DRAFT) {
+    using DS = typename Elem<DDT>::storage;
+    xd = Elem<DDT>::cvt(reinterpret_cast<const DS*>(
+        p.draft)[(int64_t)st * p.draft_stride0 + (int64_t)step * p.draft_stride1 + d]);
+  }
+  const float t_lse = wave_lse(p.tmax, p.tsum, base, p.nchunks);
+  float d_lse = 0.f, dlp = 0.f;
+  if constexpr (HAS_DRAFT) {
+    d_lse = wave_lse(p.dmax, p.dsum, base, p.nchunks);
+    dlp = xd / temp - d_lse;
+  }
+  if (lane_id() == 0) {
+    p.rtl[row] = t_lse;
+    p.rdl[row] = d_lse;
+    p.rtlp[row] = xt - t_lse;
+    p.rdlp[row] = dlp;
+  }
+}
+
+// One step of the running joint ratio, log p_{i+1} = min(log p_i + log p - log q, 0)
+// (:365-381).  The residual pass and the chain fold the same values in the same order.
+__device__ inline float fold_log_ratio(float log_p, float tlp, float dlp) {
+  return fminf(log_p + (tlp - dlp), 0.f);
+}
+
+// ------------------------------------------------------------------ pass 3 (block) ----
+
+// Residual mass of the rows the block threshold looks ahead to (:387-446): rows at draft
+// step 1..K-1 of a random request whose own draft is verifiable.  Each wave folds the joint
+// ratio of the rows before this one (one step per lane, then in order over the lanes).
+template <int TDT, int DDT>
+__global__ __launch_bounds__(kThreads) void v2_residual_kernel(V2Params p) {
+  __shared__ float s_sum[kWaves];
+  const int64_t row = blockIdx.x;
+  const int c = blockIdx.y;
+  const int step = p.exp_local_pos[row];
+  if (step < 1 || step >= p.K || step > row || row + 1 >= p.num_logits) return;
+  if (!draft_valid(p.draft_sampled[row + 1], p.vocab)) return;
+  const int st = clamp_state(p.exp_idx_mapping[row], p.num_states);
+  const float temp = p.temperature[st];
+  if (temp == 0.f) return;
+  const int64_t start = row - step;
+  float log_p = 0.f;
+  for (int b = 0; b < step; b += kWave) {
+    const int j = b + lane_id();
+    const bool in = j < step;
+    const bool v = in && draft_valid(p.draft_sampled[start + j + 1], p.vocab);
+    const float tlp = in ? p.rtlp[start + j] : 0.f;
+    const float dlp = in ? p.rdlp[start + j] : 0.f;
+    const uint64_t vm = __ballot(v);
+    const int n = step - b < kWave ? step - b : kWave;
+    for (int k = 0; k < n; ++k)
+      if ((vm >> k) & 1) log_p = fold_log_ratio(log_p, readlane_f32(tlp, k), readlane_f32(dlp, k));
+  }
+  const float prefix = expf(log_p);
+  const float t_lse = p.rtl[row], d_lse = p.rdl[row];
+  const int c0 = c * kV2Chunk;
+  float x[kV2PerThread], q[kV2PerThread];
+  load_chunk<TDT>(p.target, row * p.target_stride, c0, p.vocab, p.target_aligned, x);
+  load_chunk<DDT>(p.draft, (int64_t)st * p.draft_stride0 + (int64_t)step * p.draft_stride1, c0,
+                  p.vocab, p.draft_aligned, q);
+  float part[1] = {0.f};
+#pragma unroll
+  for (int k = 0; k < kV2PerThread; ++k) {
+    const float m_b = expf(x[k] - t_lse);
+    const float m_s = expf(q[k] / temp - d_lse);
+    part[0] += fmaxf(prefix * m_b - m_s, 0.f);
+  }
+  block_sum<1>(part, s_sum);
+  if (threadIdx.x == 0) p.rmass[row * p.nchunks + c] = part[0];
+}
+
+// ------------------------------------------------------------------ pass 4 ------------
+
+template <int TDT, bool HAS_DRAFT>
 __global__ __launch_bounds__(kThreads) void v2_chain_kernel(V2Params p) {
   const int r = blockIdx.x * kWaves + wave_id();
   if (r >= p.num_reqs) return;
@@ -267,63 +386,100 @@ __global__ __launch_bounds__(kThreads) void v2_chain_kernel(V2Params p) {
   const int64_t seed = p.seed[st];
   const float temp = p.temperature[st];
   const bool greedy = temp == 0.f;
+  const bool block = p.use_block && !greedy;
   using TS = typename Elem<TDT>::storage;
-  using DS = typename Elem<DDT>::storage;
   const TS* tgt = reinterpret_cast<const TS*>(p.target);
   int acc = 0;
   bool verifying = true;
-  float t_lse = 0.f, d_lse = 0.f;
+  float log_p = 0.f, lpt = 0.f;
   int64_t* out = p.sampled + (int64_t)r * p.sampled_stride;
-  for (int i = 0; i < nd; ++i) {
-    const int64_t li = start + i;
-    int d = p.draft_sampled[li + 1];
-    const bool valid = d >= 0 && d < p.vocab;
-    d = valid ? d : 0;
-    if (!greedy) verifying = verifying && valid;
-    if (!verifying) continue;
-    const float u = uniform_f32(randint4x64(seed, p.pos[li]).x);
-    const int64_t base = li * p.nchunks;
-    if (greedy) {
-      float bv = -INFINITY;
-      int bc = 0x7fffffff;
-      for (int c = lane_id(); c < p.nchunks; c += kWave) {
-        float v = p.tmax[base + c];
-        v = v != v ? -INFINITY : v;
-        argmax_update(bv, bc, v, c, true);
+  for (int b = 0; b < nd && verifying; b += kWave) {
+    // one step per lane: draft id, acceptance uniform and the row's precomputed inputs
+    const int j = b + lane_id();
+    const bool in = j < nd;
+    const int64_t li = start + j;
+    const int d = in ? p.draft_sampled[li + 1] : -1;
+    const bool valid = draft_valid(d, p.vocab);
+    const float u = in ? uniform_f32(randint4x64(seed, p.pos[li]).x) : 1.f;
+    int am = 0;
+    float tlp = 0.f, dlp = 0.f, res = 0.f, tnext = 0.f, lse_next = 0.f;
+    bool next_valid = false;
+    if (in && greedy) am = p.rarg[li];
+    if (in && !greedy) {
+      tlp = p.rtlp[li];
+      dlp = p.rdlp[li];
+    }
+    if (in && block && j + 1 < nd) {
+      // the block threshold looks at the next row (:612-634)
+      const int nx = p.draft_sampled[li + 2];
+      next_valid = draft_valid(nx, p.vocab);
+      if (next_valid) {
+        if constexpr (HAS_DRAFT) {
+          const int64_t base = (li + 1) * p.nchunks;
+          for (int c = 0; c < p.nchunks; ++c) res += p.rmass[base + c];
+        } else {
+          tnext = Elem<TDT>::cvt(tgt[(li + 1) * p.target_stride + nx]);
+          lse_next = p.rtl[li + 1];
+        }
       }
-      wave_argmax(bv, bc);
-      const int am = p.targ[base + (bc == 0x7fffffff ? 0 : bc)];
-      bool ok = p.rates ? (u < p.rates[i]) : (am == d);
-      ok = ok && valid;
-      verifying = ok;
-      acc += ok;
-      if (lane_id() == 0) out[i] = ok ? d : am;
-    } else {
-      t_lse = wave_lse(p.tmax, p.tsum, base, p.nchunks);
-      const float tlp = Elem<TDT>::cvt(tgt[li * p.target_stride + d]) - t_lse;
-      float dlp = 0.f;
-      d_lse = 0.f;
-      if constexpr (HAS_DRAFT) {
-        const DS* drf = reinterpret_cast<const DS*>(p.draft);
-        d_lse = wave_lse(p.dmax, p.dsum, base, p.nchunks);
-        const float dv =
-            Elem<DDT>::cvt(drf[(int64_t)st * p.draft_stride0 + (int64_t)i * p.draft_stride1 + d]);
-        dlp = dv / temp - d_lse;
+    }
+    const uint64_t vm = __ballot(valid), nm = __ballot(next_valid);
+    const int n = nd - b < kWave ? nd - b : kWave;
+    for (int k = 0; k < n; ++k) {
+      const bool v = (vm >> k) & 1;
+      const int dk = __builtin_amdgcn_readlane(valid ? d : 0, k);
+      const float uk = readlane_f32(u, k);
+      if (!greedy) verifying = verifying && v;
+      if (!verifying) break;
+      if (greedy) {
+        const int amk = __builtin_amdgcn_readlane(am, k);
+        bool ok = p.rates ? (uk < p.rates[b + k]) : (amk == dk);
+        ok = ok && v;
+        verifying = ok;
+        acc += ok;
+        if (lane_id() == 0) out[b + k] = ok ? dk : amk;
+      } else if (block) {
+        // Sun et al. 2024 (:608-640): accept b + k + 1 tokens when u <= h; the last
+        // position that passes decides.
+        log_p = fold_log_ratio(log_p, readlane_f32(tlp, k), readlane_f32(dlp, k));
+        const float prefix = expf(log_p);
+        float h = prefix;
+        if ((nm >> k) & 1) {
+          float rm;
+          if constexpr (HAS_DRAFT) {
+            rm = readlane_f32(res, k);
+          } else {
+            // one-hot drafts: p_i (1 - M_b(next draft)) in closed form (:87-104)
+            rm = prefix * (1.f - expf(readlane_f32(tnext, k) - readlane_f32(lse_next, k)));
+          }
+          const float denom = rm + 1.f - prefix;
+          h = denom > 0.f ? rm / denom : 1.f;
+        }
+        if (uk <= h) {
+          acc = b + k + 1;
+          lpt = log_p;
+        }
+        if (lane_id() == 0) out[b + k] = dk;
+      } else {
+        const bool ok = p.rates ? (uk < p.rates[b + k])
+                                : (readlane_f32(tlp, k) > logf(uk) + readlane_f32(dlp, k));
+        verifying = ok;
+        acc += ok;
+        if (lane_id() == 0) out[b + k] = dk;
       }
-      const bool ok = p.rates ? (u < p.rates[i]) : (tlp > logf(u) + dlp);
-      verifying = ok;
-      acc += ok;
-      if (lane_id() == 0) out[i] = d;
     }
   }
   if (lane_id() == 0) {
     p.acc[r] = acc;
-    p.tlse[r] = t_lse;
-    p.dlse[r] = d_lse;
+    p.lpt[r] = lpt;
+    // statistics of the rejected row for its resampling (:683-700)
+    const bool rejected = !greedy && acc < nd;
+    p.tlse[r] = rejected ? p.rtl[start + acc] : 0.f;
+    p.dlse[r] = rejected ? p.rdl[start + acc] : 0.f;
   }
 }
 
-// ------------------------------------------------------------------ pass 3 ------------
+// ------------------------------------------------------------------ pass 5 ------------
 
 template <int TDT, int DDT, bool HAS_DRAFT>
 __global__ __launch_bounds__(kThreads) void v2_resample_kernel(V2Params p) {
@@ -351,9 +507,11 @@ __global__ __launch_bounds__(kThreads) void v2_resample_kernel(V2Params p) {
       load_chunk<DDT>(p.draft, (int64_t)st * p.draft_stride0 + (int64_t)acc * p.draft_stride1, c0,
                       p.vocab, p.draft_aligned, q);
       const float tl = p.tlse[r], dlz = p.dlse[r];
+      // block verification scales the target by p_tau (:820-829); p_0 = 1
+      const float shift = p.use_block && acc > 0 ? p.lpt[r] : 0.f;
 #pragma unroll
       for (int k = 0; k < kV2PerThread; ++k) {
-        const float tlp = x[k] - tl;
+        const float tlp = (x[k] - tl) + shift;
         const float dlp = q[k] / temp - dlz;
         const float ratio = expf(dlp - tlp);
         x[k] = ratio < 1.f ? tlp + log1pf(-ratio) : -INFINITY;
@@ -394,7 +552,7 @@ __global__ __launch_bounds__(kThreads) void v2_resample_kernel(V2Params p) {
   }
 }
 
-// ------------------------------------------------------------------ pass 4 ------------
+// ------------------------------------------------------------------ pass 6 ------------
 
 __global__ __launch_bounds__(kThreads) void v2_insert_kernel(V2Params p) {
   const int r = blockIdx.x * kWaves + wave_id();
@@ -437,8 +595,18 @@ hipError_t launch_all(const V2Params& p, hipStream_t stream) {
     hipLaunchKernelGGL((v2_stats_kernel<TDT, DDT, HAS_DRAFT>),
                        dim3((unsigned)p.num_logits, p.nchunks), dim3(kThreads), 0, stream, p);
   }
+  if (p.num_logits > 0 && p.K > 0) {
+    const unsigned rw = (unsigned)((p.num_logits + kWaves - 1) / kWaves);
+    hipLaunchKernelGGL((v2_rowstat_kernel<TDT, DDT, HAS_DRAFT>), dim3(rw), dim3(kThreads), 0,
+                       stream, p);
+    if constexpr (HAS_DRAFT) {
+      if (p.use_block)
+        hipLaunchKernelGGL((v2_residual_kernel<TDT, DDT>), dim3((unsigned)p.num_logits, p.nchunks),
+                           dim3(kThreads), 0, stream, p);
+    }
+  }
   const unsigned wg = (unsigned)((p.num_reqs + kWaves - 1) / kWaves);
-  hipLaunchKernelGGL((v2_chain_kernel<TDT, DDT, HAS_DRAFT>), dim3(wg), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((v2_chain_kernel<TDT, HAS_DRAFT>), dim3(wg), dim3(kThreads), 0, stream, p);
   hipLaunchKernelGGL((v2_resample_kernel<TDT, DDT, HAS_DRAFT>),
                      dim3((unsigned)p.num_reqs, p.nchunks), dim3(kThreads), 0, stream, p);
   hipLaunchKernelGGL(v2_insert_kernel, dim3(wg), dim3(kThreads), 0, stream, p);
@@ -467,8 +635,8 @@ int64_t mvsd_v2_workspace_bytes(int64_t num_logits, int64_t num_reqs, int64_t vo
   if (num_logits < 0 || num_reqs < 0 || vocab_size <= 0) return -1;
   const int64_t nch = (vocab_size + mvsd::kV2Chunk - 1) / mvsd::kV2Chunk;
   const int64_t rows = num_logits * nch, reqs = num_reqs * nch;
-  return 5 * mvsd::align256(rows * 4) + 3 * mvsd::align256(num_reqs * 4) +
-         mvsd::align256(reqs * 8) + mvsd::align256(reqs * 4);
+  return 6 * mvsd::align256(rows * 4) + 5 * mvsd::align256(num_logits * 4) +
+         4 * mvsd::align256(num_reqs * 4) + mvsd::align256(reqs * 8) + mvsd::align256(reqs * 4);
 }
 
 int mvsd_v2_rejection_sample(
@@ -479,7 +647,8 @@ int mvsd_v2_rejection_sample(
     const int32_t* expanded_idx_mapping, const int32_t* expanded_local_pos,
     const float* temperature, const int64_t* seed, int64_t num_req_states, int64_t num_reqs,
     int64_t vocab_size, int32_t num_speculative_steps, const float* synthetic_conditional_rates,
-    int use_fp64, void* workspace, int64_t workspace_bytes, mvsd_stream_t stream) {
+    int use_fp64, int use_block_verification, void* workspace, int64_t workspace_bytes,
+    mvsd_stream_t stream) {
   using namespace mvsd;
   if (num_reqs < 0 || num_logits < 0 || num_speculative_steps < 0) return MVSD_E_INVALID;
   if (num_reqs == 0) return MVSD_OK;
@@ -494,6 +663,8 @@ int mvsd_v2_rejection_sample(
     return MVSD_E_INVALID;
   if (draft_logits && draft_dtype != MVSD_F32 && draft_dtype != MVSD_BF16 && draft_dtype != MVSD_F16)
     return MVSD_E_INVALID;
+  // block verification is incompatible with synthetic acceptance rates (:1043-1045)
+  if (use_block_verification && synthetic_conditional_rates) return MVSD_E_INVALID;
   if (draft_logits && (draft_stride1 < vocab_size || draft_stride0 < draft_stride1 * num_speculative_steps))
     return MVSD_E_INVALID;
   if (vocab_size > 0x7fffffff - kV2Chunk || num_reqs > 0x7fffffff || num_req_states > 0x7fffffff ||
@@ -529,6 +700,7 @@ int mvsd_v2_rejection_sample(
   p.K = num_speculative_steps;
   p.nchunks = nch;
   p.use_fp64 = use_fp64 != 0;
+  p.use_block = use_block_verification != 0;
   const int tsz = target_dtype == MVSD_F32 ? 4 : 2;
   const int dsz = draft_dtype == MVSD_F32 ? 4 : 2;
   p.target_aligned = ((uintptr_t)target_logits % 16 == 0) && ((target_stride * tsz) % 16 == 0);
@@ -546,9 +718,16 @@ int mvsd_v2_rejection_sample(
   p.dmax = reinterpret_cast<float*>(take(rows * 4));
   p.dsum = reinterpret_cast<float*>(take(rows * 4));
   p.targ = reinterpret_cast<int32_t*>(take(rows * 4));
+  p.rmass = reinterpret_cast<float*>(take(rows * 4));
+  p.rtl = reinterpret_cast<float*>(take(num_logits * 4));
+  p.rdl = reinterpret_cast<float*>(take(num_logits * 4));
+  p.rtlp = reinterpret_cast<float*>(take(num_logits * 4));
+  p.rdlp = reinterpret_cast<float*>(take(num_logits * 4));
+  p.rarg = reinterpret_cast<int32_t*>(take(num_logits * 4));
   p.acc = reinterpret_cast<int32_t*>(take(num_reqs * 4));
   p.tlse = reinterpret_cast<float*>(take(num_reqs * 4));
   p.dlse = reinterpret_cast<float*>(take(num_reqs * 4));
+  p.lpt = reinterpret_cast<float*>(take(num_reqs * 4));
   p.rval = reinterpret_cast<double*>(take(reqs * 8));
   p.ridx = reinterpret_cast<int32_t*>(take(reqs * 4));
 

@@ -114,7 +114,7 @@ SIGNATURES = {
                                          c_int64, c_void_p, c_int, c_int64, c_int64, c_void_p,
                                          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                          c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int32,
-                                         c_void_p, c_int, c_void_p, c_int64, c_void_p]),
+                                         c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p]),
     "mvsd_ngram_valid_sampled": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
                                          c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                          c_void_p, c_int64, c_int64, c_void_p]),

@@ -16,9 +16,11 @@ Acceptance draws ``u = tl_rand32(seed, pos)`` and the resampling's Gumbel noise
 ``tl_rand32(tl.randint(seed, pos), vocab index)`` (or the fp64 forms with ``use_fp64``) come
 from the same Philox4x32-10 counter stream as Triton's ``tl.randint4x`` / ``tl.rand``
 (minivllm/worker/gpu/sample/gumbel.py:72-131), so a draft and its verification can agree on
-noise.  Block verification (``use_block_verification=True``, :318-493) is not built and
-raises ``NotImplementedError``.  No host synchronisation; every launch is on the current
-stream of the target's device.
+noise.  ``use_block_verification=True`` selects block verification (Sun et al. 2024,
+arXiv:2403.10444; :318-493, :608-640, :800-866) for the random requests: the running joint
+ratio, the look-ahead residual mass, the last passing position, and the residual
+max(p_tau p - q, 0).  No host synchronisation; every launch is on the current stream of the
+target's device.
 """
 
 from __future__ import annotations
@@ -65,15 +67,12 @@ def rejection_sample(
     use_fp64: bool = False,
     use_block_verification: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """V2 verification (rejection_sampler_utils.py:935-1201), non-block path."""
+    """V2 verification (rejection_sampler_utils.py:935-1201)."""
     assert target_logits.ndim == 2 and target_logits.stride(-1) == 1
     assert draft_logits is None or (draft_logits.ndim == 3 and draft_logits.stride(-1) == 1)
     if use_block_verification:
         assert synthetic_conditional_rates is None, (
             "Block verification is incompatible with synthetic acceptance rates.")
-        raise NotImplementedError(
-            "block verification (rejection_sampler_utils.py:318-493) is not built in this "
-            "implementation; use use_block_verification=False")
     require_device_tensor(target_logits, "target_logits")
     if target_logits.dtype not in _FLOAT_DTYPES:
         raise TypeError(f"target_logits dtype {target_logits.dtype} is not supported")
@@ -132,29 +131,8 @@ def rejection_sample(
         num_logits, ptr(draft_logits), d_code, d_stride0, d_stride1, sampled_i32.data_ptr(),
         cu.data_ptr(), pos64.data_ptr(), idx.data_ptr(), eidx.data_ptr(), elpos.data_ptr(),
         temp.data_ptr(), seeds.data_ptr(), num_states, num_reqs, vocab_size, K, ptr(rates),
-        int(bool(use_fp64)), workspace.data_ptr(), workspace.numel(), stream_of(device)),
+        int(bool(use_fp64)), int(bool(use_block_verification)), workspace.data_ptr(),
+        workspace.numel(), stream_of(device)),
         "mvsd_v2_rejection_sample")
     del keep  # the launch is enqueued; stream-ordered frees are safe from here on
-    return sampled, num_sampled
-    rates = None
-    if synthetic_conditional_rates is not None:
-        rates = _as(synthetic_conditional_rates, torch.float32)
-    temp = _as(temperature, torch.float32)
-    seeds = _as(seed, torch.int64)
-    num_states = min(temp.numel(), seeds.numel())
-    if draft_logits is not None:
-        num_states = min(num_states, draft_logits.shape[0])
-    ws_bytes = lib().mvsd_v2_workspace_bytes(num_logits, num_reqs, vocab_size)
-    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
-    check(lib().mvsd_v2_rejection_sample(
-        sampled.data_ptr(), sampled.stride(0), num_sampled.data_ptr(),
-        target_logits.data_ptr(), dtype_code(target_logits.dtype), target_logits.stride(0),
-        num_logits, ptr(draft_logits), d_code, d_stride0, d_stride1,
-        _as(draft_sampled, torch.int32).data_ptr(), _as(cu_num_logits, torch.int32).data_ptr(),
-        _as(pos, torch.int64).data_ptr(), _as(idx_mapping, torch.int32).data_ptr(),
-        _as(expanded_idx_mapping, torch.int32).data_ptr(),
-        _as(expanded_local_pos, torch.int32).data_ptr(), temp.data_ptr(), seeds.data_ptr(),
-        num_states, num_reqs, vocab_size, K, ptr(rates), int(bool(use_fp64)),
-        workspace.data_ptr(), workspace.numel(), stream_of(device)),
-        "mvsd_v2_rejection_sample")
     return sampled, num_sampled
