@@ -396,6 +396,47 @@ int mvsd_v2_rejection_sample(
     int use_fp64, int use_block_verification, void* workspace, int64_t workspace_bytes,
     mvsd_stream_t stream);
 
+/* ------------------------------------------------------------------------------------ */
+/* v2_flatten_sampled — the V2 sampled tokens, one per logits row.                         */
+/* Replaces: flatten_sampled / _flatten_sampled_kernel (minivllm/worker/gpu/spec_decode/   */
+/*           rejection_sampler.py:73-108).  Row cu_num_logits[r] + j of flat_sampled       */
+/* [num_logits] int64 gets sampled[r * sampled_stride + j] for j < num_sampled[r], 0 for   */
+/* the other rows of the request.                                                          */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_v2_flatten_sampled(int64_t* flat_sampled, const int64_t* sampled, int64_t sampled_stride,
+                            const int32_t* num_sampled, const int32_t* cu_num_logits,
+                            int64_t num_reqs, int64_t num_logits, mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* v2_num_sampled_and_rejected — per-request counts after a V2 verification.              */
+/* Replaces: get_num_sampled_and_rejected (minivllm/worker/gpu/input_batch.py:507-553).   */
+/* In place on num_sampled [num_reqs] int32; writes num_rejected [num_reqs] int32 =       */
+/* (cu_num_logits[r+1] - cu_num_logits[r]) - num_sampled[r]; both 0 for a request still   */
+/* prefilling (seq_lens[r] < prefill_len[idx_mapping[r]]).  seq_lens, cu_num_logits,       */
+/* idx_mapping and prefill_len [num_req_states] are int32.                                 */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_v2_num_sampled_and_rejected(int32_t* num_sampled, int32_t* num_rejected,
+                                     const int32_t* seq_lens, const int32_t* cu_num_logits,
+                                     const int32_t* idx_mapping, const int32_t* prefill_len,
+                                     int64_t num_reqs, int64_t num_req_states,
+                                     mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* topk_scores — logprobs of the V2 sampled tokens and of each row's top k.               */
+/* Replaces: compute_topk_scores (minivllm/worker/gpu/sample/logprob.py:140-216), the      */
+/* path without per-request logprob token ids, with _topk_log_softmax_kernel (:44-83) and  */
+/* _ranks_kernel (:86-104).  Row n of logits [num_rows, V] fp32 (stride logits_stride),     */
+/* token t = token_ids[n] (-1 read as 0):                                                  */
+/*   ids[n, 0] = t; ids[n, 1 .. k] = the k largest raw logits by (value desc, index asc);  */
+/*   scores[n, c] = the fp32 log-softmax (x - max) - log(sum exp(x - max)) at ids[n, c], or */
+/*   the logit itself when logits_mode != 0;                                                */
+/*   ranks[n] = #{i : x_i >= x_t} over the raw logits.                                      */
+/* ids / scores are [num_rows, k + 1]; 0 <= k <= V.                                        */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_topk_scores(int32_t* ids, float* scores, int32_t* ranks, const float* logits,
+                     int64_t logits_stride, const int32_t* token_ids, int64_t num_rows,
+                     int64_t vocab_size, int64_t k, int logits_mode, mvsd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -79,3 +79,24 @@ def get_logprobs_tensors(k: int, cu_num_sampled_tokens, target_logits_indices,
     if return_slack:
         return (*out, rank_slack(lps, tokens))
     return out
+
+
+def topk_scores(logits, k: int, token_ids, logits_mode: bool = False):
+    """V2 ``compute_topk_scores`` (minivllm/worker/gpu/sample/logprob.py:140-216), the path
+    without per-request logprob token ids: row n scores ``[token_n, top-k of the raw logits]``
+    with the fp32 log-softmax (``_topk_log_softmax_kernel``, :44-83: (x - max) - log(sum
+    exp(x - max))) or the logits themselves, and ranks the token by ``#{x_i >= x_token}`` over
+    the raw logits (``_ranks_kernel``, :86-104).  Equal logits are taken in index order.
+    Returns (ids [N, k+1] int64, scores [N, k+1] fp32, ranks [N] int64)."""
+    x = torch.as_tensor(logits).to(torch.float32).cpu()
+    tok = torch.as_tensor(token_ids).cpu().to(torch.int64).reshape(-1, 1)
+    _, order = torch.sort(x, dim=-1, descending=True, stable=True)
+    ids = torch.cat((tok, order[:, :k]), dim=1)
+    if logits_mode:
+        scores = x.gather(-1, ids)
+    else:
+        m = x.max(dim=-1, keepdim=True).values
+        lse = torch.log(torch.exp(x - m).sum(dim=-1, keepdim=True))
+        scores = (x.gather(-1, ids) - m) - lse
+    ranks = (x >= x.gather(-1, tok)).sum(-1)
+    return ids, scores, ranks

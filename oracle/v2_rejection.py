@@ -3,9 +3,12 @@
 This module is the checker for ``mvsd.worker.gpu.spec_decode.rejection_sampler_utils`` and is
 imported only by ``tests/`` (never by the product path).  It follows, step by step:
 
-* ``rejection_sample`` (minivllm/worker/gpu/spec_decode/rejection_sampler_utils.py:935-1201),
-  non-block path: per-block logits statistics (:206-316), the per-request chain (:497-706),
-  the Gumbel-max resampling of the rejected/bonus row (:709-866) and its insertion (:869-932);
+* ``rejection_sample`` (minivllm/worker/gpu/spec_decode/rejection_sampler_utils.py:935-1201):
+  per-block logits statistics (:206-316), the per-request chain (:497-706), the Gumbel-max
+  resampling of the rejected/bonus row (:709-866) and its insertion (:869-932); for block
+  verification also the running joint ratio (:318-384), the look-ahead residual mass
+  (:387-446, :60-104), the threshold of the chain's block branch (:608-640) and the
+  p_tau-shifted residual (:820-829);
 * the counter-based draws of minivllm/worker/gpu/sample/gumbel.py: ``tl_rand32`` (:87-91),
   ``tl_rand64`` (:72-83) and ``gumbel_noised_argmax`` (:95-131), whose generator is Triton's
   ``tl.randint4x`` / ``tl.rand`` (Philox4x32, 10 rounds; triton/language/random.py of the
@@ -24,6 +27,12 @@ Pinning:
   draft == argmax; random accept iff log p(d) > log u + log q(d); the residual argmax
   equals brute force over max(p - q, 0) with the same noise) and the semantics pins of the
   reference's tests (tests/step73/test_v2_rejection_diff.py:318-327, :357-360);
+* block verification — the hand-computed values of the reference's tests
+  (tests/step75/test_block_verification.py:80-170) against float64 closed forms, and an
+  exhaustive losslessness check on tiny vocabularies (Sun et al. 2024: summed over draft
+  sequences, acceptance lengths and residuals, the output is distributed as the target),
+  which a dropped p_tau shift or a threshold without the look-ahead mass fails
+  (tests/test_oracle_v2_block.py);
 * float rounding of exp/log is not pinned bit for bit (numpy vs device libm): decisions are
   compared with a margin and near-ties are counted.
 """
@@ -410,3 +419,14 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
     if return_details:
         out = out + (dict(h=thresholds, cumulative_log_p=cum, residual_mass=mass, stats=stats),)
     return out
+
+
+def flatten_sampled(sampled, num_sampled, cu_num_logits, num_logits):
+    """``flatten_sampled`` (minivllm/worker/gpu/spec_decode/rejection_sampler.py:73-108): row
+    ``cu[r] + j`` holds ``sampled[r, j]`` for ``j < num_sampled[r]``; every other row is 0."""
+    flat = np.zeros(int(num_logits), np.int64)
+    cu = np.asarray(cu_num_logits).astype(np.int64)
+    for r in range(cu.shape[0] - 1):
+        n = int(num_sampled[r])
+        flat[cu[r]:cu[r] + n] = np.asarray(sampled)[r, :n]
+    return flat

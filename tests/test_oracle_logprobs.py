@@ -74,3 +74,30 @@ def test_rank_slack_counts_only_rounding_neighbours():
     tok = torch.tensor([0])
     assert rank_slack(lp, tok).tolist() == [1]       # the 1-ulp neighbour only
     assert rank_slack(lp, torch.tensor([2])).tolist() == [0]
+
+
+def test_v2_topk_scores_closed_forms():
+    """oracle.logprobs.topk_scores (V2 compute_topk_scores) against float64: the log-softmax
+    at the listed ids, the top-k of the raw logits in (value desc, index asc) order with
+    planted ties, and the rank as a brute-force count over the raw logits."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(6, 50, generator=g) * 3
+    x[1, 7] = x[1, 3] = x[1].max() + 1.0          # tie at the top: index 3 first
+    x[2, :] = 0.5                                  # all equal
+    tok = torch.tensor([0, 7, 49, 10, 3, 22])
+    ids, sc, rk = olp.topk_scores(x, 5, tok)
+    x64 = x.double()
+    lsm = x64 - x64.max(-1, keepdim=True).values
+    lsm = lsm - torch.log(torch.exp(lsm).sum(-1, keepdim=True))
+    assert torch.allclose(sc.double(), lsm.gather(-1, ids), atol=2e-6)
+    assert ids[:, 0].tolist() == tok.tolist()
+    assert ids[1, 1:3].tolist() == [3, 7]
+    assert ids[2, 1:].tolist() == [0, 1, 2, 3, 4]
+    for n in range(6):
+        row = x[n].tolist()
+        order = sorted(range(50), key=lambda i: (-row[i], i))[:5]
+        assert ids[n, 1:].tolist() == order
+        assert int(rk[n]) == sum(v >= row[int(tok[n])] for v in row)
+    ids2, sc2, rk2 = olp.topk_scores(x, 0, tok, logits_mode=True)
+    assert ids2.shape == (6, 1) and torch.equal(sc2[:, 0], x.gather(-1, tok[:, None])[:, 0])
+    assert torch.equal(rk2, rk)

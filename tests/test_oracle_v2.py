@@ -165,3 +165,10 @@ def test_planted_mistake_is_caught():
     b["draft_logits"] = None
     _, n_wrong = o.rejection_sample(**b)
     assert (n != n_wrong).any()
+
+
+def test_flatten_sampled_by_hand():
+    """Rows past a request's sampled tokens are 0 (the reference zero-fills first)."""
+    sampled = np.array([[5, 6, 7], [8, -1, -1], [9, 10, -1]])
+    flat = o.flatten_sampled(sampled, [3, 1, 2], [0, 3, 5, 8], 8)
+    assert flat.tolist() == [5, 6, 7, 8, 0, 9, 10, 0]

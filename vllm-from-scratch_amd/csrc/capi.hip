@@ -453,8 +453,36 @@ int mvsd_spec_logprobs(int32_t* ids, float* lps, int32_t* ranks, const float* ta
   p.W = (int)width;
   p.k = (int)k;
   p.logits_mode = logits_mode ? 1 : 0;
+  p.flat = 0;
+  p.rank_raw = 0;
   p.ids = ids;
   p.lps = lps;
+  p.ranks = ranks;
+  return hip_status(mvsd::launch_spec_logprobs(p, (hipStream_t)stream));
+}
+
+int mvsd_topk_scores(int32_t* ids, float* scores, int32_t* ranks, const float* logits,
+                     int64_t logits_stride, const int32_t* token_ids, int64_t num_rows,
+                     int64_t vocab_size, int64_t k, int logits_mode, mvsd_stream_t stream) {
+  if (num_rows < 0 || vocab_size <= 0 || k < 0) return MVSD_E_INVALID;
+  if (num_rows == 0) return MVSD_OK;
+  if (k > vocab_size) return MVSD_E_RANGE;
+  if (num_rows > 0x7fffffff || vocab_size > 0x7fffffff) return MVSD_E_RANGE;
+  if (!ids || !scores || !ranks || !logits || !token_ids || logits_stride < vocab_size)
+    return MVSD_E_INVALID;
+  mvsd::LogprobParams p{};
+  p.bonus = logits;
+  p.bstride = logits_stride;
+  p.tokens = token_ids;
+  p.B = (int)num_rows;
+  p.W = 1;
+  p.V = (int)vocab_size;
+  p.k = (int)k;
+  p.logits_mode = logits_mode ? 1 : 0;
+  p.flat = 1;
+  p.rank_raw = 1;
+  p.ids = ids;
+  p.lps = scores;
   p.ranks = ranks;
   return hip_status(mvsd::launch_spec_logprobs(p, (hipStream_t)stream));
 }

@@ -17,6 +17,8 @@ struct LogprobParams {
   int64_t tok_stride;
   int B, P, V, W, k;
   int logits_mode;             // 1: report the values themselves, 0: their log-softmax
+  int flat;                    // 1: position n reads row bonus + n * bstride, token tokens[n]
+  int rank_raw;                // 1: top-k order and rank compare raw values, not log-softmax
   int32_t* ids;                // [B * W, k + 1]
   float* lps;                  // [B * W, k + 1]
   int32_t* ranks;              // [B * W]

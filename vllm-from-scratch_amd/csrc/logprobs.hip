@@ -35,29 +35,35 @@ __global__ __launch_bounds__(kLpThreads) void spec_logprobs_kernel(LogprobParams
   __shared__ uint64_t s_bound;
   const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
   const int n = blockIdx.x;  // position r * W + j
-  const int r = n / p.W, j = n - r * p.W;
-  const int start = r == 0 ? 0 : p.cu_sampled[r - 1];
-  const int last = p.P + p.B - 1;
-  const int c = min(start + j, last);
-  // request owning compact row c: the first q with cu_sampled[q] > c
-  int lo = 0, hi = p.B - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi) / 2;
-    if (p.cu_sampled[mid] > c) hi = mid;
-    else lo = mid + 1;
-  }
-  const int q = lo;
-  const int qstart = q == 0 ? 0 : p.cu_sampled[q - 1];
-  const int kq = p.cu_sampled[q] - qstart - 1;  // verify rows of request q
   const float* x;
-  if (c - qstart < kq) {
-    const int vrow = c - q;  // verify rows before c: c minus the bonus rows of requests < q
-    const int64_t trow = p.target_rows ? p.target_rows[vrow] : vrow;
-    x = p.target + trow * p.tstride;
+  int token;
+  if (p.flat) {
+    x = p.bonus + (int64_t)n * p.bstride;
+    token = p.tokens[n];
   } else {
-    x = p.bonus + (int64_t)q * p.bstride;
+    const int r = n / p.W, j = n - r * p.W;
+    const int start = r == 0 ? 0 : p.cu_sampled[r - 1];
+    const int last = p.P + p.B - 1;
+    const int c = min(start + j, last);
+    // request owning compact row c: the first q with cu_sampled[q] > c
+    int lo = 0, hi = p.B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) / 2;
+      if (p.cu_sampled[mid] > c) hi = mid;
+      else lo = mid + 1;
+    }
+    const int q = lo;
+    const int qstart = q == 0 ? 0 : p.cu_sampled[q - 1];
+    const int kq = p.cu_sampled[q] - qstart - 1;  // verify rows of request q
+    if (c - qstart < kq) {
+      const int vrow = c - q;  // verify rows before c: c minus the bonus rows of requests < q
+      const int64_t trow = p.target_rows ? p.target_rows[vrow] : vrow;
+      x = p.target + trow * p.tstride;
+    } else {
+      x = p.bonus + (int64_t)q * p.bstride;
+    }
+    token = p.tokens[(int64_t)r * p.tok_stride + j];
   }
-  int token = p.tokens[(int64_t)r * p.tok_stride + j];
   token = token == -1 ? 0 : min(max(token, 0), p.V - 1);
 
   // ---- pass 1: row max and sum of exp(x - max) ----
@@ -89,6 +95,9 @@ __global__ __launch_bounds__(kLpThreads) void spec_logprobs_kernel(LogprobParams
   }
   auto lp = [&](float v) { return p.logits_mode ? v : (v - lpm) - L; };
   const float tlp = lp(x[token]);
+  // the order the top-k and the rank use: the log-softmax, or the raw values
+  auto ord = [&](float v) { return p.rank_raw ? v : lp(v); };
+  const float tord = ord(x[token]);
 
   // ---- pass 2 (repeated): per-thread top-KMAX keys below `bound`, and the rank count ----
   // Round t collects the next min(KMAX, k - done) largest keys strictly below the last key of
@@ -106,8 +115,8 @@ __global__ __launch_bounds__(kLpThreads) void spec_logprobs_kernel(LogprobParams
     for (int i = 0; i < KMAX; ++i) key[i] = 0;
     int cnt = 0;
     for (int i = tid; i < p.V; i += kLpThreads) {
-      const float v = lp(x[i]);
-      cnt += v >= tlp ? 1 : 0;
+      const float v = ord(x[i]);
+      cnt += v >= tord ? 1 : 0;
       uint64_t kk = argmax_key(v, i);
       if (kk < bound && kk > key[KMAX - 1]) {
         // insertion into the descending list (one compare-exchange step per slot)

@@ -589,6 +589,44 @@ __global__ __launch_bounds__(kThreads) void v2_insert_kernel(V2Params p) {
   if (lane_id() == 0) p.sampled[(int64_t)r * p.sampled_stride + acc] = p.ridx[base + (bc == 0x7fffffff ? 0 : bc)];
 }
 
+// ------------------------------------------------------------------ after the call ----
+
+// flatten_sampled (minivllm/worker/gpu/spec_decode/rejection_sampler.py:73-108): one
+// wavefront per request writes its logits rows [start, end) of flat: the first num_sampled
+// from sampled[r], 0 after them (the reference zero-fills flat first).
+__global__ __launch_bounds__(kThreads) void v2_flatten_kernel(int64_t* flat, const int64_t* sampled,
+                                                               int64_t stride, const int32_t* num_sampled,
+                                                               const int32_t* cu, int32_t num_reqs,
+                                                               int64_t num_logits) {
+  const int r = blockIdx.x * kWaves + wave_id();
+  if (r >= num_reqs) return;
+  int64_t start = cu[r], end = cu[r + 1];
+  start = start < 0 ? 0 : start;
+  end = end > num_logits ? num_logits : end;
+  const int64_t ns = num_sampled[r];
+  for (int64_t i = start + lane_id(); i < end; i += kWave) {
+    const int64_t j = i - start;
+    flat[i] = j < ns && j < stride ? sampled[(int64_t)r * stride + j] : 0;
+  }
+}
+
+// get_num_sampled_and_rejected (minivllm/worker/gpu/input_batch.py:507-553): a request
+// still prefilling (seq_len < prefill_len of its state) samples and rejects nothing; else it
+// rejects num_logits - num_sampled.
+__global__ __launch_bounds__(kThreads) void v2_counts_kernel(int32_t* num_sampled, int32_t* num_rejected,
+                                                              const int32_t* seq_lens, const int32_t* cu,
+                                                              const int32_t* idx_mapping,
+                                                              const int32_t* prefill_len,
+                                                              int32_t num_reqs, int32_t num_states) {
+  const int r = blockIdx.x * kThreads + threadIdx.x;
+  if (r >= num_reqs) return;
+  const int st = clamp_state(idx_mapping[r], num_states);
+  const bool prefilling = seq_lens[r] < prefill_len[st];
+  const int ns = prefilling ? 0 : num_sampled[r];
+  num_sampled[r] = ns;
+  num_rejected[r] = prefilling ? 0 : (cu[r + 1] - cu[r]) - ns;
+}
+
 template <int TDT, int DDT, bool HAS_DRAFT>
 hipError_t launch_all(const V2Params& p, hipStream_t stream) {
   if (p.num_logits > 0 && p.K > 0) {
@@ -738,6 +776,39 @@ int mvsd_v2_rejection_sample(
     case MVSD_F16: err = dispatch_draft<MVSD_F16>(p, draft_dtype, (hipStream_t)stream); break;
   }
   return record_hip_error(err);
+}
+
+int mvsd_v2_flatten_sampled(int64_t* flat_sampled, const int64_t* sampled, int64_t sampled_stride,
+                            const int32_t* num_sampled, const int32_t* cu_num_logits,
+                            int64_t num_reqs, int64_t num_logits, mvsd_stream_t stream) {
+  using namespace mvsd;
+  if (num_reqs < 0 || num_logits < 0 || sampled_stride < 0) return MVSD_E_INVALID;
+  if (num_reqs == 0 || num_logits == 0) return MVSD_OK;
+  if (!flat_sampled || !sampled || !num_sampled || !cu_num_logits) return MVSD_E_INVALID;
+  if (num_reqs > 0x7fffffff) return MVSD_E_RANGE;
+  const unsigned wg = (unsigned)((num_reqs + kWaves - 1) / kWaves);
+  hipLaunchKernelGGL(v2_flatten_kernel, dim3(wg), dim3(kThreads), 0, (hipStream_t)stream,
+                     flat_sampled, sampled, sampled_stride, num_sampled, cu_num_logits,
+                     (int32_t)num_reqs, num_logits);
+  return record_hip_error(hipGetLastError());
+}
+
+int mvsd_v2_num_sampled_and_rejected(int32_t* num_sampled, int32_t* num_rejected,
+                                     const int32_t* seq_lens, const int32_t* cu_num_logits,
+                                     const int32_t* idx_mapping, const int32_t* prefill_len,
+                                     int64_t num_reqs, int64_t num_req_states,
+                                     mvsd_stream_t stream) {
+  using namespace mvsd;
+  if (num_reqs < 0 || num_req_states <= 0) return MVSD_E_INVALID;
+  if (num_reqs == 0) return MVSD_OK;
+  if (!num_sampled || !num_rejected || !seq_lens || !cu_num_logits || !idx_mapping || !prefill_len)
+    return MVSD_E_INVALID;
+  if (num_reqs > 0x7fffffff || num_req_states > 0x7fffffff) return MVSD_E_RANGE;
+  const unsigned wg = (unsigned)((num_reqs + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(v2_counts_kernel, dim3(wg), dim3(kThreads), 0, (hipStream_t)stream,
+                     num_sampled, num_rejected, seq_lens, cu_num_logits, idx_mapping, prefill_len,
+                     (int32_t)num_reqs, (int32_t)num_req_states);
+  return record_hip_error(hipGetLastError());
 }
 
 }  // extern "C"

@@ -115,6 +115,13 @@ SIGNATURES = {
                                          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                          c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int32,
                                          c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p]),
+    "mvsd_v2_flatten_sampled": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
+                                        c_int64, c_int64, c_void_p]),
+    "mvsd_v2_num_sampled_and_rejected": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                 c_void_p, c_void_p, c_int64, c_int64,
+                                                 c_void_p]),
+    "mvsd_topk_scores": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
+                                 c_int64, c_int64, c_int64, c_int, c_void_p]),
     "mvsd_ngram_valid_sampled": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
                                          c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                          c_void_p, c_int64, c_int64, c_void_p]),
