@@ -33,6 +33,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "mvsd_device.h"
 
 namespace mvsd {
@@ -92,6 +94,20 @@ __device__ inline double uniform_f64(uint32_t lo, uint32_t hi) {
   const uint64_t r = ((uint64_t)hi << 32) | lo;
   const double u = (double)r * 5.421010862427522170037e-20;
   return fmax(u, 2.2250738585072014e-308);
+}
+
+// ------------------------------------------------------------------ fast math ---------
+// The per-vocabulary-entry work uses the hardware exponential and logarithm (v_exp_f32 /
+// v_log_f32 through __expf / __logf, within about 2.3 ulp over the normal range; __expf
+// flushes results below 2^-126 to 0).  The reference's Triton kernels likewise use the
+// approximate tl.exp / tl.log forms.
+
+// log(1 + a) for -1 <= a <= 0: w = 1 + a rounded, and the rounding of w corrected by the
+// factor a / (w - 1) (Goldberg, "What every computer scientist should know about
+// floating-point arithmetic", 1991, Theorem 4); within about 3 ulp.  log1p(-1) = -inf.
+__device__ inline float fast_log1p(float a) {
+  const float w = 1.f + a;
+  return w == 1.f ? a : __logf(w) * __fdividef(a, w - 1.f);
 }
 
 // ------------------------------------------------------------------ arguments ---------
@@ -167,7 +183,7 @@ __device__ inline void block_max_sumexp(float (&x)[kV2PerThread], float* s_max, 
   float sv[1] = {0.f};
   if (m > -INFINITY) {
 #pragma unroll
-    for (int k = 0; k < kV2PerThread; ++k) sv[0] += expf(x[k] - m);
+    for (int k = 0; k < kV2PerThread; ++k) sv[0] += __expf(x[k] - m);
   }
   block_sum<1>(sv, s_sum);
   s = m > -INFINITY ? sv[0] : 0.f;
@@ -243,8 +259,9 @@ __global__ __launch_bounds__(kThreads) void v2_stats_kernel(V2Params p) {
     __syncthreads();
     load_chunk<DDT>(p.draft, (int64_t)st * p.draft_stride0 + (int64_t)step * p.draft_stride1, c0,
                     p.vocab, p.draft_aligned, x);
+    const Divider dv = make_divider(temp);
 #pragma unroll
-    for (int k = 0; k < kV2PerThread; ++k) x[k] = x[k] / temp;
+    for (int k = 0; k < kV2PerThread; ++k) x[k] = divide(dv, x[k]);
     block_max_sumexp(x, s_a, s_b, m, s);
     if (threadIdx.x == 0) {
       p.dmax[slot] = m;
@@ -307,7 +324,7 @@ __global__ __launch_bounds__(kThreads) void v2_rowstat_kernel(V2Params p) {
   float d_lse = 0.f, dlp = 0.f;
   if constexpr (HAS_DRAFT) {
     d_lse = wave_lse(p.dmax, p.dsum, base, p.nchunks);
-    dlp = xd / temp - d_lse;
+    dlp = divide(make_divider(temp), xd) - d_lse;
   }
   if (lane_id() == 0) {
     p.rtl[row] = t_lse;
@@ -360,10 +377,11 @@ __global__ __launch_bounds__(kThreads) void v2_residual_kernel(V2Params p) {
   load_chunk<DDT>(p.draft, (int64_t)st * p.draft_stride0 + (int64_t)step * p.draft_stride1, c0,
                   p.vocab, p.draft_aligned, q);
   float part[1] = {0.f};
+  const Divider dv = make_divider(temp);
 #pragma unroll
   for (int k = 0; k < kV2PerThread; ++k) {
-    const float m_b = expf(x[k] - t_lse);
-    const float m_s = expf(q[k] / temp - d_lse);
+    const float m_b = __expf(x[k] - t_lse);
+    const float m_s = __expf(divide(dv, q[k]) - d_lse);
     part[0] += fmaxf(prefix * m_b - m_s, 0.f);
   }
   block_sum<1>(part, s_sum);
@@ -481,10 +499,27 @@ __global__ __launch_bounds__(kThreads) void v2_chain_kernel(V2Params p) {
 
 // ------------------------------------------------------------------ pass 5 ------------
 
-template <int TDT, int DDT, bool HAS_DRAFT>
+// Gumbel score of residual logit x at vocabulary index col: x + (-log(-log(u))) with u the
+// request's counter draw for col (gumbel.py:95-131): tl_rand32 and -log(-log1p(-u)) in fp32,
+// or tl_rand64 and -log(-log(u)) in fp64.
+template <bool FP64>
+__device__ inline auto gumbel_score(float x, uint32_t gseed, int col) {
+  if constexpr (FP64) {
+    const U32x4 rn = randint4x32(gseed, col);
+    return (double)x + (-log(-log(uniform_f64(rn.x, rn.y))));
+  } else {
+    const float u = uniform_f32(randint4x32(gseed, col).x);
+    return x + (-__logf(-fast_log1p(-u)));
+  }
+}
+
+template <int TDT, int DDT, bool HAS_DRAFT, bool FP64>
 __global__ __launch_bounds__(kThreads) void v2_resample_kernel(V2Params p) {
   __shared__ double s_v[kWaves];
   __shared__ int s_i[kWaves];
+  // per wave: the live entries of its 1024 columns (residual logit, column offset)
+  __shared__ float s_x[kWaves][kWave * kV2PerThread];
+  __shared__ uint16_t s_c[kWaves][kWave * kV2PerThread];
   const int r = blockIdx.x;
   const int c = blockIdx.y;
   const int acc = p.acc[r];
@@ -509,12 +544,14 @@ __global__ __launch_bounds__(kThreads) void v2_resample_kernel(V2Params p) {
       const float tl = p.tlse[r], dlz = p.dlse[r];
       // block verification scales the target by p_tau (:820-829); p_0 = 1
       const float shift = p.use_block && acc > 0 ? p.lpt[r] : 0.f;
+      const Divider dv = make_divider(temp);
 #pragma unroll
       for (int k = 0; k < kV2PerThread; ++k) {
         const float tlp = (x[k] - tl) + shift;
-        const float dlp = q[k] / temp - dlz;
-        const float ratio = expf(dlp - tlp);
-        x[k] = ratio < 1.f ? tlp + log1pf(-ratio) : -INFINITY;
+        const float dlp = divide(dv, q[k]) - dlz;
+        // log max(p - q, 0) = log p + log(1 - q / p) (:831-842)
+        const float ratio = __expf(dlp - tlp);
+        x[k] = ratio < 1.f ? tlp + fast_log1p(-ratio) : -INFINITY;
       }
     } else {
 #pragma unroll
@@ -522,32 +559,52 @@ __global__ __launch_bounds__(kThreads) void v2_resample_kernel(V2Params p) {
         x[k] = chunk_col(c0, k, TV) == rej ? -INFINITY : x[k];
     }
   }
-  double bv = -INFINITY;
+  using Score = typename std::conditional<FP64, double, float>::type;
+  Score bv = -INFINITY;
   int bi = 0x7fffffff;
-  uint32_t gseed = 0;
-  if (temp != 0.f) gseed = randint4x64(p.seed[st], p.pos[ri]).x;
+  if (temp == 0.f) {
 #pragma unroll
-  for (int k = 0; k < kV2PerThread; ++k) {
-    const int col = chunk_col(c0, k, TV);
-    if (col >= p.vocab) continue;
-    double sc;
-    if (temp == 0.f) {
-      sc = (double)x[k];
-    } else if (p.use_fp64) {
-      const U32x4 rn = randint4x32(gseed, col);
-      sc = (double)x[k] + (-log(-log(uniform_f64(rn.x, rn.y))));
-    } else {
-      const float uu = uniform_f32(randint4x32(gseed, col).x);
-      sc = (double)(x[k] + (-logf(-log1pf(-uu))));
+    for (int k = 0; k < kV2PerThread; ++k) {
+      const int col = chunk_col(c0, k, TV);
+      const bool take = col < p.vocab && ((x[k] > bv) | ((x[k] == bv) & (col < bi)));
+      bv = take ? x[k] : bv;
+      bi = take ? col : bi;
     }
-    const bool take = (sc > bv) | ((sc == bv) & (col < bi));
-    bv = take ? sc : bv;
-    bi = take ? col : bi;
+  } else {
+    // Entries whose residual logit is -inf (or NaN) score -inf (or NaN) and cannot win: only
+    // the live ones draw noise.  Each wave packs its live entries into LDS and then scores
+    // them one per lane, so a rejected row with half its vocabulary dead runs half the draws.
+    const uint32_t gseed = randint4x64(p.seed[st], p.pos[ri]).x;
+    float* wx = s_x[wave_id()];
+    uint16_t* wc = s_c[wave_id()];
+    int n = 0;
+#pragma unroll
+    for (int k = 0; k < kV2PerThread; ++k) {
+      const int col = chunk_col(c0, k, TV);
+      const bool live = col < p.vocab && x[k] > -INFINITY;
+      const uint64_t m = __ballot(live);
+      if (live) {
+        const int o = n + (int)__builtin_amdgcn_mbcnt_hi(
+                              (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        wx[o] = x[k];
+        wc[o] = (uint16_t)(col - c0);
+      }
+      n += __popcll(m);
+    }
+    __syncthreads();
+    for (int i = lane_id(); i < n; i += kWave) {
+      const int col = c0 + wc[i];
+      const Score sc = gumbel_score<FP64>(wx[i], gseed, col);
+      const bool take = (sc > bv) | ((sc == bv) & (col < bi));
+      bv = take ? sc : bv;
+      bi = take ? col : bi;
+    }
   }
-  block_best(bv, bi, s_v, s_i);
+  double bvd = (double)bv;
+  block_best(bvd, bi, s_v, s_i);
   if (threadIdx.x == 0) {
     const int64_t slot = (int64_t)r * p.nchunks + c;
-    p.rval[slot] = bv;
+    p.rval[slot] = bvd;
     p.ridx[slot] = bi == 0x7fffffff ? c0 : bi;
   }
 }
@@ -645,8 +702,12 @@ hipError_t launch_all(const V2Params& p, hipStream_t stream) {
   }
   const unsigned wg = (unsigned)((p.num_reqs + kWaves - 1) / kWaves);
   hipLaunchKernelGGL((v2_chain_kernel<TDT, HAS_DRAFT>), dim3(wg), dim3(kThreads), 0, stream, p);
-  hipLaunchKernelGGL((v2_resample_kernel<TDT, DDT, HAS_DRAFT>),
-                     dim3((unsigned)p.num_reqs, p.nchunks), dim3(kThreads), 0, stream, p);
+  if (p.use_fp64)
+    hipLaunchKernelGGL((v2_resample_kernel<TDT, DDT, HAS_DRAFT, true>),
+                       dim3((unsigned)p.num_reqs, p.nchunks), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((v2_resample_kernel<TDT, DDT, HAS_DRAFT, false>),
+                       dim3((unsigned)p.num_reqs, p.nchunks), dim3(kThreads), 0, stream, p);
   hipLaunchKernelGGL(v2_insert_kernel, dim3(wg), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
