@@ -70,16 +70,45 @@ __device__ inline U32x4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uin
   return {c0, c1, c2, c3};
 }
 
+// a ^ b ^ k in one VALU instruction: gfx950's three-input bitwise op v_bitop3_b32 with the
+// truth table of a three-way xor (0x96).  k is read from a scalar register, so it must be
+// uniform across the wavefront.
+__device__ inline uint32_t xor3_uniform(uint32_t a, uint32_t b, uint32_t k) {
+  uint32_t r;
+  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(r) : "v"(a), "v"(b), "s"(k));
+  return r;
+}
+
+// philox4x32_10 for a key (k0, k1) that is uniform across the wavefront: the same rounds,
+// with each round's pair of xors fused from round 3 on (the first two rounds of the races'
+// counters (col, 0, 0, 0) fold to fewer operations, which the compiler finds itself).
+__device__ inline U32x4 philox4x32_10_uniform_key(uint32_t c0, uint32_t c1, uint32_t c2,
+                                                  uint32_t c3, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)0xCD9E8D57u * c2, p2 = (uint64_t)0xD2511F53u * c0;
+    if (r < 2) {
+      c0 = (uint32_t)(p0 >> 32) ^ c1 ^ k0;
+      c2 = (uint32_t)(p2 >> 32) ^ c3 ^ k1;
+    } else {
+      c0 = xor3_uniform((uint32_t)(p0 >> 32), c1, k0);
+      c2 = xor3_uniform((uint32_t)(p2 >> 32), c3, k1);
+    }
+    c1 = (uint32_t)p0;
+    c3 = (uint32_t)p2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return {c0, c1, c2, c3};
+}
+
 // tl.randint4x(seed, offset) with a 64-bit offset: counter (lo, hi, 0, 0), key (seed lo, hi).
 __device__ inline U32x4 randint4x64(int64_t seed, int64_t offset) {
   return philox4x32_10((uint32_t)offset, (uint32_t)((uint64_t)offset >> 32), 0u, 0u,
                        (uint32_t)seed, (uint32_t)((uint64_t)seed >> 32));
 }
 
-// tl.randint4x(seed32, offset32) with a 32-bit seed and a 32-bit offset.
-__device__ inline U32x4 randint4x32(uint32_t seed, int32_t offset) {
-  return philox4x32_10((uint32_t)offset, 0u, 0u, 0u, seed, 0u);
-}
+
 
 // uint_to_uniform_float for 32 bits, clamped away from zero (tl_rand32, includes_zero=False).
 __device__ inline float uniform_f32(uint32_t bits) {
@@ -97,20 +126,50 @@ __device__ inline double uniform_f64(uint32_t lo, uint32_t hi) {
 }
 
 // ------------------------------------------------------------------ fast math ---------
-// The per-vocabulary-entry work uses the hardware exponential and logarithm (v_exp_f32 /
-// v_log_f32 through __expf / __logf, within about 2.3 ulp over the normal range; __expf
-// flushes results below 2^-126 to 0).  The reference's Triton kernels likewise use the
-// approximate tl.exp / tl.log forms.
+// The per-vocabulary-entry work uses the hardware exponential and logarithm: __expf, and
+// v_log_f32 (base 2, within 1 ulp over the normal range) scaled by ln 2.  The reference's
+// Triton kernels likewise use the approximate tl.exp / tl.log forms.
+
+// Natural logarithm of a positive normal x (0 gives -inf).
+__device__ inline float hw_log(float x) { return __builtin_amdgcn_logf(x) * 0.693147182f; }
 
 // log(1 + a) for -1 <= a <= 0: w = 1 + a rounded, and the rounding of w corrected by the
 // factor a / (w - 1) (Goldberg, "What every computer scientist should know about
-// floating-point arithmetic", 1991, Theorem 4); within about 3 ulp.  log1p(-1) = -inf.
+// floating-point arithmetic", 1991, Theorem 4), a itself when w rounds to 1; within about
+// 3 ulp.  log1p(-1) = -inf.  Both branches are computed and one is selected.
 __device__ inline float fast_log1p(float a) {
   const float w = 1.f + a;
-  return w == 1.f ? a : __logf(w) * __fdividef(a, w - 1.f);
+  const float r = hw_log(w) * (a * __builtin_amdgcn_rcpf(w - 1.f));
+  return w == 1.f ? a : r;
 }
 
 // ------------------------------------------------------------------ arguments ---------
+
+// What the resampling pass does for one request, written by the chain kernel so that a
+// resampling workgroup starts its row loads after one descriptor load.
+enum ResampleMode : int32_t {
+  kResampleNone = 0,      // greedy request with a rejection: the chain wrote the argmax
+  kResampleArgmax = 1,    // greedy bonus row: argmax of the target row
+  kResampleTarget = 2,    // bonus row, or a placeholder draft: the target row as it is
+  kResampleResidual = 3,  // rejected draft with draft logits: log max(p_tau p - q, 0)
+  kResampleExclude = 4,   // rejected one-hot draft: the target row without that id
+};
+
+struct ResampleDesc {
+  int64_t row;     // target row
+  int64_t draft;   // element offset of the draft row (draft logits)
+  float tl, dl;    // target / draft log-sum-exp of the row
+  float shift;     // log p_tau (block verification), else 0
+  float temp;      // temperature of the request's state
+  uint32_t gseed;  // key of the row's Gumbel race, tl.randint(seed, pos)
+  int32_t rej;     // the rejected draft id (kResampleExclude)
+  int32_t mode;    // ResampleMode
+  // High word of the race's Philox key: always 0 (tl.randint's 32-bit seed).  Read at run
+  // time so that the key schedule stays in scalar registers, where the rounds' xors can
+  // take it as an operand, instead of folding into literals.
+  uint32_t key_hi;
+};
+static_assert(sizeof(ResampleDesc) == 48, "descriptor layout");
 
 struct V2Params {
   int64_t* sampled;
@@ -142,24 +201,24 @@ struct V2Params {
   int32_t* rarg;         // [num_logits] target argmax of a greedy verify row
   float* rmass;          // [num_logits, nchunks] block residual-mass partials
   int32_t* acc;  // accepted length per request, -1 for a malformed request
-  float *tlse, *dlse;    // [num_reqs] log-sum-exp of the rejected row
-  float* lpt;            // [num_reqs] log p_tau: the joint ratio of the accepted block
+  struct ResampleDesc* desc;  // [num_reqs] what the resampling pass scores, from the chain
   double* rval;
   int32_t* ridx;
 };
 
 __device__ inline int clamp_state(int s, int n) { return s < 0 ? 0 : (s >= n ? n - 1 : s); }
 
-// Load this thread's 16 columns of a chunk as fp32; columns at or past `limit` read -inf.
-template <int DT>
+// Load this thread's kV2Chunk / NT columns of a chunk as fp32 (NT threads per workgroup);
+// columns at or past `limit` read -inf.
+template <int DT, int NT = kThreads>
 __device__ inline void load_chunk(const void* base, int64_t row_off, int c0, int limit,
-                                  bool aligned, float (&x)[kV2PerThread]) {
+                                  bool aligned, float (&x)[kV2Chunk / NT]) {
   using S = typename Elem<DT>::storage;
   constexpr int VEC = Elem<DT>::kVec;
   const S* p = reinterpret_cast<const S*>(base) + row_off;
 #pragma unroll
-  for (int j = 0; j < kV2PerThread / VEC; ++j) {
-    const int col = c0 + (j * kThreads + (int)threadIdx.x) * VEC;
+  for (int j = 0; j < kV2Chunk / NT / VEC; ++j) {
+    const int col = c0 + (j * NT + (int)threadIdx.x) * VEC;
     float v[VEC];
     load_vec<DT>(p, col, limit, aligned, -INFINITY, v);
 #pragma unroll
@@ -167,9 +226,10 @@ __device__ inline void load_chunk(const void* base, int64_t row_off, int c0, int
   }
 }
 
+template <int NT = kThreads>
 __device__ inline int chunk_col(int c0, int k, int VEC) {
   const int j = k / VEC, e = k % VEC;
-  return c0 + (j * kThreads + (int)threadIdx.x) * VEC + e;
+  return c0 + (j * NT + (int)threadIdx.x) * VEC + e;
 }
 
 // (max, sum exp(x - max)) of the block's values; sum is 0 when the max is -inf.
@@ -191,6 +251,7 @@ __device__ inline void block_max_sumexp(float (&x)[kV2PerThread], float* s_max, 
 
 // Best (value, index) over the block: larger value, then lower index.  Doubles so the fp64
 // Gumbel scores reduce with the same code.
+template <int NW = kWaves>
 __device__ inline void block_best(double& v, int& i, double* s_v, int* s_i) {
 #pragma unroll
   for (int off = kWave / 2; off >= 1; off >>= 1) {
@@ -208,7 +269,7 @@ __device__ inline void block_best(double& v, int& i, double* s_v, int* s_i) {
   v = s_v[0];
   i = s_i[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) {
+  for (int w = 1; w < NW; ++w) {
     const bool take = (s_v[w] > v) | ((s_v[w] == v) & (s_i[w] < i));
     v = take ? s_v[w] : v;
     i = take ? s_i[w] : i;
@@ -396,7 +457,10 @@ __global__ __launch_bounds__(kThreads) void v2_chain_kernel(V2Params p) {
   if (r >= p.num_reqs) return;
   const int64_t start = p.cu_num_logits[r], end = p.cu_num_logits[r + 1];
   if (start < 0 || end > p.num_logits || end <= start || end - start - 1 > p.K) {
-    if (lane_id() == 0) p.acc[r] = -1;
+    if (lane_id() == 0) {
+      p.acc[r] = -1;
+      p.desc[r] = ResampleDesc{};
+    }
     return;
   }
   const int nd = (int)(end - start - 1);
@@ -489,11 +553,36 @@ __global__ __launch_bounds__(kThreads) void v2_chain_kernel(V2Params p) {
   }
   if (lane_id() == 0) {
     p.acc[r] = acc;
-    p.lpt[r] = lpt;
-    // statistics of the rejected row for its resampling (:683-700)
-    const bool rejected = !greedy && acc < nd;
-    p.tlse[r] = rejected ? p.rtl[start + acc] : 0.f;
-    p.dlse[r] = rejected ? p.rdl[start + acc] : 0.f;
+    // The resampling of row start + acc (:709-866): its state and temperature come from the
+    // expanded mapping of that row, as in the reference.
+    const int64_t ri = start + acc;
+    const bool is_bonus = acc == nd;
+    const int rst = clamp_state(p.exp_idx_mapping[ri], p.num_states);
+    const float rtemp = p.temperature[rst];
+    const int rej = is_bonus ? -1 : p.draft_sampled[ri + 1];
+    ResampleDesc d{};
+    d.row = ri;
+    d.draft = (int64_t)rst * p.draft_stride0 + (int64_t)acc * p.draft_stride1;
+    d.temp = rtemp;
+    d.rej = rej;
+    if (rtemp == 0.f) {
+      d.mode = is_bonus ? kResampleArgmax : kResampleNone;
+    } else {
+      d.gseed = randint4x64(p.seed[rst], p.pos[ri]).x;
+      if (is_bonus || !draft_valid(rej, p.vocab)) {
+        d.mode = kResampleTarget;
+      } else if (HAS_DRAFT) {
+        // statistics of the rejected row (:683-700)
+        d.mode = kResampleResidual;
+        d.tl = p.rtl[ri];
+        d.dl = p.rdl[ri];
+        // block verification scales the target by p_tau (:820-829); p_0 = 1
+        d.shift = block && acc > 0 ? lpt : 0.f;
+      } else {
+        d.mode = kResampleExclude;
+      }
+    }
+    p.desc[r] = d;
   }
 }
 
@@ -502,85 +591,89 @@ __global__ __launch_bounds__(kThreads) void v2_chain_kernel(V2Params p) {
 // Gumbel score of residual logit x at vocabulary index col: x + (-log(-log(u))) with u the
 // request's counter draw for col (gumbel.py:95-131): tl_rand32 and -log(-log1p(-u)) in fp32,
 // or tl_rand64 and -log(-log(u)) in fp64.
+// gseed and key_hi are uniform across the workgroup (one race per row).
 template <bool FP64>
-__device__ inline auto gumbel_score(float x, uint32_t gseed, int col) {
+__device__ inline auto gumbel_score(float x, uint32_t gseed, int col, uint32_t key_hi) {
+  const U32x4 rn = philox4x32_10_uniform_key((uint32_t)col, 0u, 0u, 0u, gseed, key_hi);
   if constexpr (FP64) {
-    const U32x4 rn = randint4x32(gseed, col);
     return (double)x + (-log(-log(uniform_f64(rn.x, rn.y))));
   } else {
-    const float u = uniform_f32(randint4x32(gseed, col).x);
-    return x + (-__logf(-fast_log1p(-u)));
+    const float u = uniform_f32(rn.x);
+    return x + (-hw_log(-fast_log1p(-u)));
   }
 }
 
+constexpr int kResThreads = 256;  // resampling workgroup: 16 columns per thread of a chunk
+constexpr int kResWaves = kResThreads / kWave;
+constexpr int kResPer = kV2Chunk / kResThreads;
+
 template <int TDT, int DDT, bool HAS_DRAFT, bool FP64>
-__global__ __launch_bounds__(kThreads) void v2_resample_kernel(V2Params p) {
-  __shared__ double s_v[kWaves];
-  __shared__ int s_i[kWaves];
-  // per wave: the live entries of its 1024 columns (residual logit, column offset)
-  __shared__ float s_x[kWaves][kWave * kV2PerThread];
-  __shared__ uint16_t s_c[kWaves][kWave * kV2PerThread];
+__global__ __launch_bounds__(kResThreads) void v2_resample_kernel(V2Params p) {
+  __shared__ double s_v[kResWaves];
+  __shared__ int s_i[kResWaves];
+  // per wave: the live entries of its 512 columns (residual logit, column offset)
+  __shared__ float s_x[kResWaves][kWave * kResPer];
+  __shared__ uint16_t s_c[kResWaves][kWave * kResPer];
   const int r = blockIdx.x;
   const int c = blockIdx.y;
-  const int acc = p.acc[r];
-  if (acc < 0) return;
-  const int64_t start = p.cu_num_logits[r], end = p.cu_num_logits[r + 1];
-  const int64_t ri = start + acc;
-  const bool is_bonus = ri == end - 1;
-  const int st = clamp_state(p.exp_idx_mapping[ri], p.num_states);
-  const float temp = p.temperature[st];
-  if (temp == 0.f && !is_bonus) return;
-  const int rej = is_bonus ? 0 : p.draft_sampled[ri + 1];
-  const bool rej_valid = rej >= 0 && rej < p.vocab;
+  const ResampleDesc d = p.desc[r];
+  if (d.mode == kResampleNone) return;
   const int c0 = c * kV2Chunk;
-  float x[kV2PerThread];
-  load_chunk<TDT>(p.target, ri * p.target_stride, c0, p.vocab, p.target_aligned, x);
+  float x[kResPer];
+  load_chunk<TDT, kResThreads>(p.target, d.row * p.target_stride, c0, p.vocab, p.target_aligned, x);
   constexpr int TV = Elem<TDT>::kVec;
-  if (!is_bonus && rej_valid) {
-    if constexpr (HAS_DRAFT) {
-      float q[kV2PerThread];
-      load_chunk<DDT>(p.draft, (int64_t)st * p.draft_stride0 + (int64_t)acc * p.draft_stride1, c0,
-                      p.vocab, p.draft_aligned, q);
-      const float tl = p.tlse[r], dlz = p.dlse[r];
-      // block verification scales the target by p_tau (:820-829); p_0 = 1
-      const float shift = p.use_block && acc > 0 ? p.lpt[r] : 0.f;
-      const Divider dv = make_divider(temp);
+  if constexpr (HAS_DRAFT) {
+    if (d.mode == kResampleResidual) {
+      float q[kResPer];
+      load_chunk<DDT, kResThreads>(p.draft, d.draft, c0, p.vocab, p.draft_aligned, q);
+      const Divider dv = make_divider(d.temp);
 #pragma unroll
-      for (int k = 0; k < kV2PerThread; ++k) {
-        const float tlp = (x[k] - tl) + shift;
-        const float dlp = divide(dv, q[k]) - dlz;
+      for (int k = 0; k < kResPer; ++k) {
+        const float tlp = (x[k] - d.tl) + d.shift;
+        const float dlp = divide(dv, q[k]) - d.dl;
         // log max(p - q, 0) = log p + log(1 - q / p) (:831-842)
         const float ratio = __expf(dlp - tlp);
         x[k] = ratio < 1.f ? tlp + fast_log1p(-ratio) : -INFINITY;
       }
-    } else {
-#pragma unroll
-      for (int k = 0; k < kV2PerThread; ++k)
-        x[k] = chunk_col(c0, k, TV) == rej ? -INFINITY : x[k];
     }
+  }
+  if (d.mode == kResampleExclude) {
+#pragma unroll
+    for (int k = 0; k < kResPer; ++k)
+      x[k] = chunk_col<kResThreads>(c0, k, TV) == d.rej ? -INFINITY : x[k];
   }
   using Score = typename std::conditional<FP64, double, float>::type;
   Score bv = -INFINITY;
   int bi = 0x7fffffff;
-  if (temp == 0.f) {
+  if (d.mode == kResampleArgmax) {
 #pragma unroll
-    for (int k = 0; k < kV2PerThread; ++k) {
-      const int col = chunk_col(c0, k, TV);
+    for (int k = 0; k < kResPer; ++k) {
+      const int col = chunk_col<kResThreads>(c0, k, TV);
       const bool take = col < p.vocab && ((x[k] > bv) | ((x[k] == bv) & (col < bi)));
       bv = take ? x[k] : bv;
+      bi = take ? col : bi;
+    }
+  } else if (d.mode != kResampleResidual) {
+    // the target row (less at most one id): every entry draws, straight from registers
+#pragma unroll
+    for (int k = 0; k < kResPer; ++k) {
+      const int col = chunk_col<kResThreads>(c0, k, TV);
+      if (col >= p.vocab) continue;
+      const Score sc = gumbel_score<FP64>(x[k], d.gseed, col, d.key_hi);
+      const bool take = (sc > bv) | ((sc == bv) & (col < bi));
+      bv = take ? sc : bv;
       bi = take ? col : bi;
     }
   } else {
     // Entries whose residual logit is -inf (or NaN) score -inf (or NaN) and cannot win: only
     // the live ones draw noise.  Each wave packs its live entries into LDS and then scores
-    // them one per lane, so a rejected row with half its vocabulary dead runs half the draws.
-    const uint32_t gseed = randint4x64(p.seed[st], p.pos[ri]).x;
+    // them four per lane at a time (independent draws for the lane to interleave).
     float* wx = s_x[wave_id()];
     uint16_t* wc = s_c[wave_id()];
     int n = 0;
 #pragma unroll
-    for (int k = 0; k < kV2PerThread; ++k) {
-      const int col = chunk_col(c0, k, TV);
+    for (int k = 0; k < kResPer; ++k) {
+      const int col = chunk_col<kResThreads>(c0, k, TV);
       const bool live = col < p.vocab && x[k] > -INFINITY;
       const uint64_t m = __ballot(live);
       if (live) {
@@ -592,16 +685,27 @@ __global__ __launch_bounds__(kThreads) void v2_resample_kernel(V2Params p) {
       n += __popcll(m);
     }
     __syncthreads();
-    for (int i = lane_id(); i < n; i += kWave) {
-      const int col = c0 + wc[i];
-      const Score sc = gumbel_score<FP64>(wx[i], gseed, col);
-      const bool take = (sc > bv) | ((sc == bv) & (col < bi));
-      bv = take ? sc : bv;
-      bi = take ? col : bi;
+    constexpr int kIlp = 4;
+    for (int i0 = 0; i0 < n; i0 += kIlp * kWave) {
+      Score sc[kIlp];
+      int col[kIlp];
+#pragma unroll
+      for (int j = 0; j < kIlp; ++j) {
+        const int i = i0 + j * kWave + lane_id();
+        const bool in = i < n;
+        col[j] = in ? c0 + wc[i] : 0x7fffffff;
+        sc[j] = gumbel_score<FP64>(in ? wx[i] : -INFINITY, d.gseed, col[j], d.key_hi);
+      }
+#pragma unroll
+      for (int j = 0; j < kIlp; ++j) {
+        const bool take = (sc[j] > bv) | ((sc[j] == bv) & (col[j] < bi));
+        bv = take ? sc[j] : bv;
+        bi = take ? col[j] : bi;
+      }
     }
   }
   double bvd = (double)bv;
-  block_best(bvd, bi, s_v, s_i);
+  block_best<kResWaves>(bvd, bi, s_v, s_i);
   if (threadIdx.x == 0) {
     const int64_t slot = (int64_t)r * p.nchunks + c;
     p.rval[slot] = bvd;
@@ -619,12 +723,8 @@ __global__ __launch_bounds__(kThreads) void v2_insert_kernel(V2Params p) {
     if (lane_id() == 0) p.num_sampled[r] = 0;
     return;
   }
-  const int64_t start = p.cu_num_logits[r], end = p.cu_num_logits[r + 1];
-  const int64_t ri = start + acc;
-  const bool is_bonus = ri == end - 1;
-  const int st = clamp_state(p.exp_idx_mapping[ri], p.num_states);
   if (lane_id() == 0) p.num_sampled[r] = acc + 1;
-  if (p.temperature[st] == 0.f && !is_bonus) return;
+  if (p.desc[r].mode == kResampleNone) return;
   const int64_t base = (int64_t)r * p.nchunks;
   double bv = -INFINITY;
   int bc = 0x7fffffff;
@@ -704,10 +804,10 @@ hipError_t launch_all(const V2Params& p, hipStream_t stream) {
   hipLaunchKernelGGL((v2_chain_kernel<TDT, HAS_DRAFT>), dim3(wg), dim3(kThreads), 0, stream, p);
   if (p.use_fp64)
     hipLaunchKernelGGL((v2_resample_kernel<TDT, DDT, HAS_DRAFT, true>),
-                       dim3((unsigned)p.num_reqs, p.nchunks), dim3(kThreads), 0, stream, p);
+                       dim3((unsigned)p.num_reqs, p.nchunks), dim3(kResThreads), 0, stream, p);
   else
     hipLaunchKernelGGL((v2_resample_kernel<TDT, DDT, HAS_DRAFT, false>),
-                       dim3((unsigned)p.num_reqs, p.nchunks), dim3(kThreads), 0, stream, p);
+                       dim3((unsigned)p.num_reqs, p.nchunks), dim3(kResThreads), 0, stream, p);
   hipLaunchKernelGGL(v2_insert_kernel, dim3(wg), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
@@ -735,7 +835,8 @@ int64_t mvsd_v2_workspace_bytes(int64_t num_logits, int64_t num_reqs, int64_t vo
   const int64_t nch = (vocab_size + mvsd::kV2Chunk - 1) / mvsd::kV2Chunk;
   const int64_t rows = num_logits * nch, reqs = num_reqs * nch;
   return 6 * mvsd::align256(rows * 4) + 5 * mvsd::align256(num_logits * 4) +
-         4 * mvsd::align256(num_reqs * 4) + mvsd::align256(reqs * 8) + mvsd::align256(reqs * 4);
+         mvsd::align256(num_reqs * 4) + mvsd::align256(num_reqs * 48) + mvsd::align256(reqs * 8) +
+         mvsd::align256(reqs * 4);
 }
 
 int mvsd_v2_rejection_sample(
@@ -824,9 +925,7 @@ int mvsd_v2_rejection_sample(
   p.rdlp = reinterpret_cast<float*>(take(num_logits * 4));
   p.rarg = reinterpret_cast<int32_t*>(take(num_logits * 4));
   p.acc = reinterpret_cast<int32_t*>(take(num_reqs * 4));
-  p.tlse = reinterpret_cast<float*>(take(num_reqs * 4));
-  p.dlse = reinterpret_cast<float*>(take(num_reqs * 4));
-  p.lpt = reinterpret_cast<float*>(take(num_reqs * 4));
+  p.desc = reinterpret_cast<ResampleDesc*>(take(num_reqs * (int64_t)sizeof(ResampleDesc)));
   p.rval = reinterpret_cast<double*>(take(reqs * 8));
   p.ridx = reinterpret_cast<int32_t*>(take(reqs * 4));
 
