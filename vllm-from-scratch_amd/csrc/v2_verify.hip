@@ -232,23 +232,6 @@ __device__ inline int chunk_col(int c0, int k, int VEC) {
   return c0 + (j * NT + (int)threadIdx.x) * VEC + e;
 }
 
-// (max, sum exp(x - max)) of the block's values; sum is 0 when the max is -inf.
-__device__ inline void block_max_sumexp(float (&x)[kV2PerThread], float* s_max, float* s_sum,
-                                        float& m, float& s) {
-  float mv[1] = {-INFINITY};
-#pragma unroll
-  for (int k = 0; k < kV2PerThread; ++k) mv[0] = fmaxf(mv[0], x[k]);
-  block_max<1>(mv, s_max);
-  m = mv[0];
-  float sv[1] = {0.f};
-  if (m > -INFINITY) {
-#pragma unroll
-    for (int k = 0; k < kV2PerThread; ++k) sv[0] += __expf(x[k] - m);
-  }
-  block_sum<1>(sv, s_sum);
-  s = m > -INFINITY ? sv[0] : 0.f;
-}
-
 // Best (value, index) over the block: larger value, then lower index.  Doubles so the fp64
 // Gumbel scores reduce with the same code.
 template <int NW = kWaves>
@@ -278,29 +261,64 @@ __device__ inline void block_best(double& v, int& i, double* s_v, int* s_i) {
 
 // ------------------------------------------------------------------ pass 1 ------------
 
+// (max, sum exp(x - max)) of G rows of the block's values at once; sum is 0 when the max
+// is -inf.
+template <int G>
+__device__ inline void block_max_sumexp_rows(float (&x)[G][kV2PerThread], float* s_red,
+                                             float (&m)[G], float (&sm)[G]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kV2PerThread; ++k) m[g] = fmaxf(m[g], x[g][k]);
+  }
+  block_max<G>(m, s_red);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    sm[g] = 0.f;
+    if (m[g] > -INFINITY) {
+#pragma unroll
+      for (int k = 0; k < kV2PerThread; ++k) sm[g] += __expf(x[g][k] - m[g]);
+    }
+  }
+  block_sum<G>(sm, s_red);
+#pragma unroll
+  for (int g = 0; g < G; ++g) sm[g] = m[g] > -INFINITY ? sm[g] : 0.f;
+}
+
 template <int TDT, int DDT, bool HAS_DRAFT>
 __global__ __launch_bounds__(kThreads) void v2_stats_kernel(V2Params p) {
-  __shared__ float s_a[kWaves], s_b[kWaves];
+  __shared__ float s_red[2 * kWaves];
   __shared__ double s_v[kWaves];
   __shared__ int s_i[kWaves];
   const int64_t row = blockIdx.x;
   const int c = blockIdx.y;
   const int step = p.exp_local_pos[row];
+  const int st_raw = p.exp_idx_mapping[row];
   if (step < 0 || step >= p.K) return;
-  const int st = clamp_state(p.exp_idx_mapping[row], p.num_states);
-  const float temp = p.temperature[st];
   const int c0 = c * kV2Chunk;
   const int64_t slot = row * p.nchunks + c;
-  float x[kV2PerThread];
-  load_chunk<TDT>(p.target, row * p.target_stride, c0, p.vocab, p.target_aligned, x);
+  constexpr int G = HAS_DRAFT ? 2 : 1;
+  float x[G][kV2PerThread];
+  // the target loads go out before the temperature is known; the draft loads (random rows
+  // only) right after, so both rows are in flight together
+  load_chunk<TDT>(p.target, row * p.target_stride, c0, p.vocab, p.target_aligned, x[0]);
+  const int st = clamp_state(st_raw, p.num_states);
+  const float temp = p.temperature[st];
+  if constexpr (HAS_DRAFT) {
+    if (temp != 0.f)
+      load_chunk<DDT>(p.draft, (int64_t)st * p.draft_stride0 + (int64_t)step * p.draft_stride1,
+                      c0, p.vocab, p.draft_aligned, x[1]);
+  }
   if (temp == 0.f) {
     double bv = -INFINITY;
     int bi = 0x7fffffff;
 #pragma unroll
     for (int k = 0; k < kV2PerThread; ++k) {
       const int col = chunk_col(c0, k, Elem<TDT>::kVec);
-      const bool take = col < p.vocab && (((double)x[k] > bv) | (((double)x[k] == bv) & (col < bi)));
-      bv = take ? (double)x[k] : bv;
+      const bool take =
+          col < p.vocab && (((double)x[0][k] > bv) | (((double)x[0][k] == bv) & (col < bi)));
+      bv = take ? (double)x[0][k] : bv;
       bi = take ? col : bi;
     }
     block_best(bv, bi, s_v, s_i);
@@ -310,23 +328,19 @@ __global__ __launch_bounds__(kThreads) void v2_stats_kernel(V2Params p) {
     }
     return;
   }
-  float m, s;
-  block_max_sumexp(x, s_a, s_b, m, s);
-  if (threadIdx.x == 0) {
-    p.tmax[slot] = m;
-    p.tsum[slot] = s;
-  }
   if constexpr (HAS_DRAFT) {
-    __syncthreads();
-    load_chunk<DDT>(p.draft, (int64_t)st * p.draft_stride0 + (int64_t)step * p.draft_stride1, c0,
-                    p.vocab, p.draft_aligned, x);
     const Divider dv = make_divider(temp);
 #pragma unroll
-    for (int k = 0; k < kV2PerThread; ++k) x[k] = divide(dv, x[k]);
-    block_max_sumexp(x, s_a, s_b, m, s);
-    if (threadIdx.x == 0) {
-      p.dmax[slot] = m;
-      p.dsum[slot] = s;
+    for (int k = 0; k < kV2PerThread; ++k) x[1][k] = divide(dv, x[1][k]);
+  }
+  float m[G], sm[G];
+  block_max_sumexp_rows<G>(x, s_red, m, sm);
+  if (threadIdx.x == 0) {
+    p.tmax[slot] = m[0];
+    p.tsum[slot] = sm[0];
+    if constexpr (HAS_DRAFT) {
+      p.dmax[slot] = m[1];
+      p.dsum[slot] = sm[1];
     }
   }
 }
