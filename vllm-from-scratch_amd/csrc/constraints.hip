@@ -356,6 +356,14 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
   const bool has_k = kk > 0 && kk < p.V;
   const bool has_p = t > 0.f;  // p >= 1 keeps every entry of non-zero probability
   if (!has_k && !has_p) return false;
+  // A greedy row only needs its argmax (the first maximum, or the first NaN).  Top-k keeps
+  // every entry at or above the k-th largest, so it never masks a maximum or a NaN; top-p
+  // masks an ascending prefix that never includes the last entry of the order (v, index), so
+  // it masks a maximum only when the maximum is tied (a NaN makes every mass NaN and masks
+  // nothing).  Such a row gets no mask unless it has top-p and a tied maximum.  (The in-place
+  // top-k / top-p of the sampler passes no temperatures: none of its rows is greedy.)
+  const bool greedy_row = p.temperature != nullptr && p.temperature[r] == 0.f;
+  if (greedy_row && !has_p) return false;
   const float T = req_temperature(p, r);
   const Divider dv = make_divider(T);
   const int V = p.V;
@@ -381,14 +389,24 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
       }
     });
   } else {
+    // t1 counts the entries at the thread maximum t0 (for the greedy tie test)
     for_each_group<DT>(x, V, aligned, [&](int, const float (&v)[VEC], int n) {
 #pragma unroll
-      for (int j = 0; j < VEC; ++j)
-        if (j < n) t0 = max(t0, ordered_bits(v[j]));
+      for (int j = 0; j < VEC; ++j) {
+        if (j < n) {
+          const uint32_t c = ordered_bits(v[j]);
+          t1 = c > t0 ? 1u : t1 + (c == t0);
+          t0 = max(t0, c);
+        }
+      }
     });
   }
   sm.tkey[tid] = t0;
   const uint32_t mkey = block_max_u32(t0, sm);
+  if (greedy_row) {
+    const unsigned long long ties = block_sum_u64(t0 == mkey ? t1 : 0u, sm);
+    if (mkey == kNanKey || ties < 2) return false;
+  }
 
   // ---- top-k: v_k, the k-th largest v, and the entries with v >= v_k in LDS if they fit ----
   bool cand_ok = false;
