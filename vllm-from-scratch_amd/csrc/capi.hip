@@ -93,7 +93,7 @@ int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 // Workspace layout of the verify kernel for launches of at most Bl requests over P verify
 // rows with at most nc chunks per row.  ctrl = {ticket, wait-failure flag, exit counter}.
 struct WorkspaceLayout {
-  int64_t ctrl, req_cnt, score_cnt, decision, masks, stat_slots, score_slots, total;
+  int64_t ctrl, req_cnt, score_cnt, decision, masks, order, stat_slots, score_slots, total;
 };
 
 WorkspaceLayout verify_layout(int64_t Bl, int64_t P, int64_t nc) {
@@ -110,6 +110,8 @@ WorkspaceLayout verify_layout(int64_t Bl, int64_t P, int64_t nc) {
   off = align_up(off + b * 4, 256);
   l.masks = off;  // row masks of the sampling constraints (zeroed again by the verify kernel)
   off = align_up(off + rows * 16, 256);
+  l.order = off;  // the constraints kernel's row plan (each entry cleared by its reader)
+  off = align_up(off + rows * 4, 256);
   l.stat_slots = off;
   off = align_up(off + rows * 2 * nc * 8, 256);  // two slots per chunk (tail halves)
   l.score_slots = off;
@@ -274,6 +276,7 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
   p.top_k = masked ? a->top_k : nullptr;
   p.top_p = masked ? a->top_p : nullptr;
   p.masks = masked ? reinterpret_cast<float4*>(ws + lay.masks) : nullptr;
+  p.order = masked ? reinterpret_cast<int*>(ws + lay.order) : nullptr;
   p.stat_slots = reinterpret_cast<uint64_t*>(ws + lay.stat_slots);
   p.score_slots = reinterpret_cast<uint64_t*>(ws + lay.score_slots);
   p.debug_row_stats = a->debug_row_stats;

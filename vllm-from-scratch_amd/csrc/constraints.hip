@@ -38,7 +38,7 @@ namespace mvsd {
 namespace {
 
 #ifndef MVSD_CONSTRAINT_BATCH
-#define MVSD_CONSTRAINT_BATCH 4   // 16-byte vectors per thread per batch of a row walk
+#define MVSD_CONSTRAINT_BATCH 6   // 16-byte vectors per thread per batch of a row walk
 #endif
 
 #ifndef MVSD_CONSTRAINT_THREADS
@@ -338,6 +338,59 @@ __device__ inline int request_of(const VerifyParams& p, int row) {
     else lo = mid + 1;
   }
   return lo;
+}
+
+// How much work the verify rows of request r take in the constraints kernel: 0 none (no
+// constraint, or a greedy request with top-k only: see row_thresholds), 1 random with top-p
+// (three passes per row), 2 random with top-k only (one pass), 3 greedy with top-p (one pass,
+// more when a row's maximum is tied).
+__device__ inline int request_class(const VerifyParams& p, int r) {
+  if (p.all_greedy) return 0;
+  const int64_t kk = p.top_k ? p.top_k[r] : (int64_t)p.V;
+  const bool has_k = kk > 0 && kk < p.V;
+  const bool has_p = p.top_p && 1.0f - p.top_p[r] > 0.f;
+  const bool greedy = p.temperature != nullptr && p.temperature[r] == 0.f;
+  if ((!has_k && !has_p) || (greedy && !has_p)) return 0;
+  return greedy ? 3 : (has_p ? 1 : 2);
+}
+
+// The plan of a masked call (one 1024-thread workgroup, one request per thread at a time):
+// the neutral mask for every row of class 0, and the other rows listed by class, as row + 1,
+// so that the rows with the most passes start first.  The order inside a class does not
+// matter: each row's mask depends on its own row only.
+__global__ __launch_bounds__(1024) void constraint_plan_kernel(VerifyParams p) {
+  __shared__ int cnt[4], base[4];
+  const int tid = threadIdx.x;
+  if (tid < 4) cnt[tid] = 0;
+  __syncthreads();
+  const float4 neutral = make_float4(-INFINITY, -INFINITY, __int_as_float(-1), 0.f);
+  // rows past the last request belong to none
+  for (int j = max(p.B > 0 ? p.cu[p.B - 1] : 0, 0) + tid; j < p.P; j += 1024) p.masks[j] = neutral;
+  for (int r = tid; r < p.B; r += 1024) {
+    const int begin = max(r == 0 ? 0 : p.cu[r - 1], 0), end = min(p.cu[r], p.P);
+    const int c = request_class(p, r);
+    if (c == 0) {
+      for (int j = begin; j < end; ++j) p.masks[j] = neutral;
+    } else if (end > begin) {
+      atomicAdd(&cnt[c], end - begin);
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    base[1] = 0;
+    base[2] = cnt[1];
+    base[3] = cnt[1] + cnt[2];
+    cnt[1] = cnt[2] = cnt[3] = 0;
+  }
+  __syncthreads();
+  for (int r = tid; r < p.B; r += 1024) {
+    const int begin = max(r == 0 ? 0 : p.cu[r - 1], 0), end = min(p.cu[r], p.P);
+    const int c = request_class(p, r);
+    if (c != 0 && end > begin) {
+      const int at = base[c] + atomicAdd(&cnt[c], end - begin);
+      for (int j = begin; j < end; ++j) p.order[at + (j - begin)] = j + 1;
+    }
+  }
 }
 
 // The row's mask (A, B, J) from its request's top-k / top-p; false when nothing is masked.
@@ -672,7 +725,18 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
 template <int DT, bool WRITE>
 __global__ __launch_bounds__(kCT) void constraints_kernel(VerifyParams p) {
   __shared__ ConstraintSmem sm;
-  const int row = blockIdx.x;
+  __shared__ int s_row;
+  int row = blockIdx.x;
+  if (p.order) {
+    // take this workgroup's entry of the plan, and clear it for the next call
+    if (threadIdx.x == 0) {
+      s_row = p.order[blockIdx.x] - 1;
+      p.order[blockIdx.x] = 0;
+    }
+    __syncthreads();
+    row = s_row;
+    if (row < 0) return;
+  }
   float A, Bv;
   int J;
   const bool any = row_thresholds<DT>(p, row, sm, A, Bv, J);
@@ -710,6 +774,8 @@ __global__ __launch_bounds__(kCT) void constraints_kernel(VerifyParams p) {
 
 hipError_t launch_constraints(const VerifyParams& params, int target_dtype, hipStream_t stream) {
   if (params.P == 0) return hipSuccess;
+  if (params.order)
+    hipLaunchKernelGGL(constraint_plan_kernel, dim3(1), dim3(1024), 0, stream, params);
   const dim3 grid((unsigned)params.P), block(kCT);
   switch (target_dtype) {
     case MVSD_F32: hipLaunchKernelGGL((constraints_kernel<MVSD_F32, false>), grid, block, 0, stream, params); break;

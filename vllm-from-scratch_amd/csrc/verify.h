@@ -72,6 +72,9 @@ struct VerifyParams {
   // Optional read-out [P, 3] of each random verify row as decided: raw max, sum of
   // exp2((x - max) log2(e) / T), and the fp32 probability of the draft token.
   float* debug_row_stats;
+  // Rows the constraints kernel works on, heaviest first, as row + 1 (0 = no entry), written
+  // by the plan kernel and cleared by the workgroup that takes each entry; null: every row.
+  int* order;
 };
 
 // Verify row j's row in the target tensor: target_rows[j] clamped to the tensor, or j.
@@ -118,6 +121,8 @@ hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream);
 hipError_t launch_verify(const VerifyParams& params, int target_dtype, int grid,
                          hipStream_t stream);
 // One workgroup per verify row: writes params.masks from top_k / top_p (constraints.hip).
+// With params.order set, a plan kernel first writes the masks of the rows that need no work
+// and lists the others heaviest first (random top-p, random top-k, greedy top-p).
 hipError_t launch_constraints(const VerifyParams& params, int target_dtype, hipStream_t stream);
 // Top-k / top-p masking in place on fp32 rows logits + r * stride, r < num_rows (one request
 // per row, no temperature): masked entries become -inf.  top_k [num_rows] int64 or null;
