@@ -273,6 +273,7 @@ def bench_ngram(args, device):
     t0 = time.perf_counter()
     ong.kmp_batch(tn, ln, 2, 5, 8192, 5)
     cpu_s = time.perf_counter() - t0
+    host_ms = bench_ngram_host_api(tn, ln, args.steps, args.warmup, device)
     line = {"metric": "ngram proposer drafts/s (C3)", "value": round(B / (ms / 1e3), 1),
             "unit": "requests/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "strong",
@@ -284,8 +285,36 @@ def bench_ngram(args, device):
                          "traffic": None},
             "cpu_baseline": {"value": round(B / cpu_s, 1), "unit": "requests/s", "cores": 1,
                              "kind": "port", "sample": "all 256 histories through oracle/ngram.c "
-                             "KMP (the reference CPU algorithm), one thread"}}
+                             "KMP (the reference CPU algorithm), one thread"},
+            "host_api": {"ms_per_call": round(host_ms, 5),
+                         "requests_per_s": round(B / (host_ms / 1e3), 1),
+                         "path": "NgramProposer.propose on pageable numpy histories [256, 4096] "
+                                 "int32: pinned staging, one upload, the kernel, drafts and "
+                                 "counts back, one synchronisation (wall clock)"}}
     print(json.dumps(line))
+
+
+def bench_ngram_host_api(tokens_np, lens_np, steps, warmup, device):
+    """Wall-clock ms per NgramProposer.propose call (the reference's host-buffer API) on the
+    C3 histories held in pageable host memory."""
+    from types import SimpleNamespace
+
+    from mvsd.spec_decode.ngram_proposer import NgramProposer
+
+    B = tokens_np.shape[0]
+    cfg = SimpleNamespace(
+        speculative_config=SimpleNamespace(num_speculative_tokens=5, prompt_lookup_min=2,
+                                           prompt_lookup_max=5),
+        model_config=SimpleNamespace(max_model_len=8192),
+        scheduler_config=SimpleNamespace(max_num_seqs=B))
+    prop = NgramProposer(cfg, device)
+    sampled = [[1]] * B
+    for _ in range(warmup):
+        prop.propose(5, sampled, lens_np, tokens_np)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        prop.propose(5, sampled, lens_np, tokens_np)
+    return (time.perf_counter() - t0) / steps * 1e3
 
 
 def bench_v2(args, device):

@@ -251,6 +251,25 @@ def test_c3_full_size_bit_exact(device):
         assert d2[r, :kc[r]].tolist() == kd[r, :kc[r]].tolist()
 
 
+def test_host_api_c3_twice_with_smaller_batch(device):
+    """NgramProposer.propose from pageable numpy histories at the C3 size (ragged lengths,
+    some requests inactive) equals the reference CPU KMP; a second, smaller call reuses the
+    pinned staging buffers and is exact too."""
+    tokens = configs.ngram_c3(device).cpu().numpy()
+    B, L = tokens.shape
+    rng = np.random.default_rng(5)
+    prop = NgramProposer(Cfg(k=5, min_n=2, max_n=5, max_model_len=8192, max_num_seqs=B),
+                         device)
+    for n, k in ((B, 5), (B // 3, 3)):
+        lens = rng.integers(1, L + 1, size=n).astype(np.int32)
+        sampled = [[1] if rng.random() < 0.8 else [] for _ in range(n)]
+        got = prop.propose(k, sampled, lens, tokens[:n])
+        kd, kc = ong.kmp_batch(tokens[:n], lens, 2, 5, 8192, k)
+        for r in range(n):
+            expect = kd[r, :kc[r]].tolist() if sampled[r] else []
+            assert got[r] == expect, (n, r)
+
+
 @pytest.mark.parametrize("lo,hi,vocab", [(1, 1, 3), (2, 5, 4), (3, 3, 2), (1, 8, 5), (4, 32, 2)])
 def test_random_histories_vs_brute_force(device, lo, hi, vocab):
     rng = np.random.default_rng(lo * 100 + hi)

@@ -6,8 +6,10 @@ Same constructor and methods as the reference (``propose``, ``batch_propose``,
 (:41-99): the longest n in [prompt_lookup_min, prompt_lookup_max] whose n-gram suffix
 occurred earlier, the earliest such occurrence, ``k = min(k, max_model_len - len)`` and
 ``min(k, tokens after the match)`` drafts.  The match itself runs on the GPU
-(``mvsd_ngram_propose`` with the max_model_len cap enabled): the valid rows' histories are
-uploaded once per call and the ``[B, k]`` drafts come back in one copy.
+(``mvsd_ngram_propose`` with the max_model_len cap enabled).  Per call the histories,
+lengths and active flags are written into one pinned host buffer and uploaded in one
+asynchronous copy; the drafts and counts come back through pinned buffers with one
+synchronisation.
 """
 
 from __future__ import annotations
@@ -34,6 +36,11 @@ class NgramProposer:
         self.valid_ngram_draft = np.zeros((max_num_seqs, self.k), dtype=np.int32)
         self.valid_ngram_num_drafts = np.zeros(max_num_seqs, dtype=np.int32)
         self.device = torch.device(device) if device is not None else None
+        # pinned staging (grown on demand): [tokens int32 | lengths int32 | active u8] up, and
+        # drafts / counts back; each call ends with a synchronisation, so reuse is safe
+        self._up_host: torch.Tensor | None = None
+        self._up_dev: torch.Tensor | None = None
+        self._down_host: torch.Tensor | None = None
 
     def _device(self) -> torch.device:
         if self.device is None:
@@ -62,18 +69,11 @@ class NgramProposer:
             lengths = np.asarray(num_tokens_no_spec[:num_requests], dtype=np.int64)
             width = max(1, int(lengths[valid].max()))
             width = min(width, token_ids_cpu.shape[1])
-            rows = np.ascontiguousarray(token_ids_cpu[:num_requests, :width], dtype=np.int32)
-            active = np.zeros(num_requests, dtype=np.uint8)
-            active[valid] = 1
-            device = self._device()
-            tokens = torch.from_numpy(rows).to(device)
-            lens = torch.from_numpy(np.minimum(lengths, width).astype(np.int32)).to(device)
-            act = torch.from_numpy(active).to(device)
+            tokens, lens, act = self._upload(token_ids_cpu, lengths, valid, num_requests, width)
             drafts, counts = ngram_propose_device(
                 tokens, lens, min_n=self.min_n, max_n=self.max_n, k=k, active=act,
                 cap_by_model_len=True, max_model_len=self.max_model_len)
-            drafts_np = drafts.cpu().numpy()
-            counts_np = counts.cpu().numpy()
+            drafts_np, counts_np = self._download(drafts, counts)
             for i in valid:
                 n = int(counts_np[i])
                 self.valid_ngram_num_drafts[i] = n
@@ -87,6 +87,43 @@ class NgramProposer:
             else:
                 out.append([])
         return out
+
+    def _upload(self, token_ids_cpu: np.ndarray, lengths: np.ndarray, valid: list[int],
+                num_requests: int, width: int):
+        """Stage rows [:num_requests, :width], their lengths and the active flags in the
+        pinned buffer and copy them to the device at once; returns device views."""
+        n_tok = num_requests * width * 4
+        n_len = num_requests * 4
+        need = n_tok + n_len + num_requests
+        device = self._device()
+        if self._up_host is None or self._up_host.numel() < need:
+            size = max(need, 2 * (0 if self._up_host is None else self._up_host.numel()))
+            self._up_host = torch.empty(size, dtype=torch.uint8, pin_memory=True)
+            self._up_dev = torch.empty(size, dtype=torch.uint8, device=device)
+        host = self._up_host.numpy()
+        host[:n_tok].view(np.int32).reshape(num_requests, width)[:] = \
+            token_ids_cpu[:num_requests, :width]
+        host[n_tok:n_tok + n_len].view(np.int32)[:] = np.minimum(lengths, width)
+        flags = host[n_tok + n_len:need]
+        flags[:] = 0
+        flags[valid] = 1
+        dev = self._up_dev
+        dev[:need].copy_(self._up_host[:need], non_blocking=True)
+        tokens = dev[:n_tok].view(torch.int32).view(num_requests, width)
+        return tokens, dev[n_tok:n_tok + n_len].view(torch.int32), dev[n_tok + n_len:need]
+
+    def _download(self, drafts: torch.Tensor, counts: torch.Tensor):
+        """Copy drafts [B, k] and counts [B] (int32) back through pinned memory; one sync."""
+        B, k = drafts.shape
+        need = B * (k + 1)
+        if self._down_host is None or self._down_host.numel() < need:
+            self._down_host = torch.empty(max(need, 1024), dtype=torch.int32, pin_memory=True)
+        host = self._down_host
+        host[:B * k].view(B, k).copy_(drafts, non_blocking=True)
+        host[B * k:need].copy_(counts, non_blocking=True)
+        torch.cuda.current_stream(drafts.device).synchronize()
+        out = host.numpy()
+        return out[:B * k].reshape(B, k).copy(), out[B * k:need].copy()
 
     def load_model(self, *args, **kwargs):
         pass
