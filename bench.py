@@ -487,10 +487,47 @@ def main():
         "cpu_baseline": None,
         "parity": None,
     }
+    if args.config == "h":
+        line["drop_in_forward"] = bench_forward(w, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         line["cpu_baseline"], ref = cpu_baseline(w, args.cpu_seconds)
         line["parity"] = parity_summary(w, out, ref)
     print(json.dumps(line), flush=True)
+
+
+def bench_forward(w, steps, warmup):
+    """ms per RejectionSampler.forward call (the drop-in's whole step) on the same rows in the
+    compact [P + B, V] layout: bonus rows through mvsd.sample.Sampler, the uniforms and the
+    [B, V] Exp(1) noise drawn by torch's generator, then the verification.  Reported beside
+    the headline, which times rejection_sample with the randomness supplied."""
+    from mvsd.sample import Sampler
+    from mvsd.sample.rejection_sampler import RejectionSampler
+    from mvsd.testing.spec_metadata import make_metadata, sampling_metadata
+
+    B, P, V = w.batch_size, w.num_tokens, w.vocab_size
+    ids = w.draft_token_ids.tolist()
+    drafts, start = [], 0
+    for k in w.num_draft_tokens:
+        drafts.append(ids[start:start + k])
+        start += k
+    device = w.target_logits.device
+    meta = make_metadata(drafts, device=device)
+    logits = torch.empty((P + B, V), dtype=torch.float32, device=device)
+    logits[meta.target_logits_indices.long()] = w.target_logits
+    logits[meta.bonus_logits_indices.long()] = w.target_logits[:B]
+    temps = w.temperature.tolist()
+    sm = sampling_metadata(temps, drafts, device=device)
+    rs = RejectionSampler(Sampler())
+
+    def step():
+        return rs(meta, w.draft_probs, logits, sm).sampled_token_ids
+
+    ms, _, wall_ms, _ = time_steps(step, steps, warmup)
+    del logits
+    return {"ms_per_step": round(ms, 5), "wall_ms_per_step": round(wall_ms, 5),
+            "path": "RejectionSampler(Sampler()).forward on compact [P + B, V] fp32 logits: "
+                    "bonus-row sampling, uniforms and Exp(1) noise from torch's generator, "
+                    "verification (no penalties, no logprobs)"}
 
 
 def accept_rates(outputs, num_draft_tokens, max_k):

@@ -342,13 +342,28 @@ int mvsd_spec_logprobs(int32_t* ids, float* lps, int32_t* ranks, const float* ta
 /* of row r, NaN first, lowest index on ties), apply_min_p (:280-293, op 1: with p the      */
 /* softmax of row r, entries with p < max(p) * aux[r] become -inf in place; aux[r] <= 0     */
 /* leaves the row), compute_logprobs (:313-315, op 3: out row r = (x - max) - log(sum      */
-/* exp(x - max))); and random_sample, minivllm/sample/ops/topk_topp_sampler.py:82-90        */
-/* (op 2: ids[r] = argmax of softmax(row r) / aux row r, the exponential race with the     */
-/* noise rows at aux + r * aux_stride).                                                     */
+/* exp(x - max))).  Op 2 is invalid: the exponential race is mvsd_sampler_race.            */
 /* ------------------------------------------------------------------------------------ */
 int mvsd_sampler_rows(int op, int32_t* ids, float* out, int64_t out_stride, float* x,
                       int64_t stride, const float* aux, int64_t aux_stride, int64_t num_rows,
                       int64_t vocab_size, mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* sampler_race — random_sample, minivllm/sample/ops/topk_topp_sampler.py:82-90, with the  */
+/* softmax before it (:73-80) and, when temperature is given, the temperature divide of    */
+/* Sampler.sample (minivllm/sample/sampler.py:263-268) folded in: ids[r] = argmax over i of */
+/* (exp(v_i - M) / S) / noise[r][i] with v = fl(x[r][i] / temperature[r]) (or x[r][i]      */
+/* when temperature is NULL), M the max and S the sum of exp(v - M) over row r; NaN first,  */
+/* lowest index on ties.  temperature [num_rows] fp32 holds positive divisors (the         */
+/* reference's safe temperatures: 1 for greedy rows).  Rows of 8192 columns are spread     */
+/* over workgroups; workspace: >= mvsd_sampler_race_workspace_bytes(num_rows, V) bytes of   */
+/* device memory, no initialisation needed.  V <= 8388608.                                  */
+/* ------------------------------------------------------------------------------------ */
+int64_t mvsd_sampler_race_workspace_bytes(int64_t num_rows, int64_t vocab_size);
+int mvsd_sampler_race(int32_t* ids, const float* x, int64_t stride, const float* noise,
+                      int64_t noise_stride, const float* temperature, int64_t num_rows,
+                      int64_t vocab_size, void* workspace, int64_t workspace_bytes,
+                      mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
 /* selftest — on-device check of an arithmetic assumption of the kernels.  No counterpart   */

@@ -87,6 +87,45 @@ def test_row_ops_match_torch(device):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("V,pad", [(1000, 0), (8192, 0), (8193, 3), (151936, 0), (151936, 1),
+                                   (20001, 0)])
+@pytest.mark.parametrize("with_t", [False, True])
+def test_race_matches_float64(device, V, pad, with_t):
+    """mvsd_sampler_race (through random_sample) against float64 softmax(fl(x / T)) / E: the
+    token is the oracle's argmax or within 1e-5 relative of its score.  Chunk edges (V = 8192,
+    8193), a scalar-load path (rows padded to an odd stride), a row with a NaN (every score
+    NaN: index 0), a row of -inf (index 0) and a row masked but for a few entries."""
+    rng = np.random.default_rng(V + pad + 7 * with_t)
+    n = 9
+    full = torch.from_numpy(rng.normal(0, 3, (n, V + pad)).astype(np.float32))
+    full[1, 5] = float("nan")
+    full[2, :] = -math.inf
+    full[3, :] = -math.inf
+    full[3, [V - 1, V // 2, 7]] = torch.tensor([1.0, 1.5, 0.5])
+    x = full[:, :V]
+    noise = torch.from_numpy(rng.exponential(1.0, (n, V)).astype(np.float32))
+    temps = torch.from_numpy(rng.uniform(0.3, 1.7, n).astype(np.float32))
+    temps[4] = 1.0
+    xd = full.to(device)[:, :V]
+    assert xd.stride(0) == V + pad
+    smp_noise = noise.to(device)
+    orig = smp.generate_sampler_noise
+    smp.generate_sampler_noise = lambda shape, gens, dev: smp_noise
+    try:
+        got = smp.random_sample(xd, {}, temperature=temps.to(device) if with_t else None)
+    finally:
+        smp.generate_sampler_noise = orig
+    got = got.cpu().tolist()
+    v = (x / temps[:, None]) if with_t else x          # fl(x / T), as the kernel divides
+    scores = torch.softmax(v.double(), dim=-1) / noise.double()
+    assert got[1] == 0 and got[2] == 0
+    for r in (0, 3, 4, 5, 6, 7, 8):
+        want = int(torch.argmax(scores[r]))
+        assert got[r] == want or float(scores[r, got[r]]) >= float(scores[r, want]) * (1 - 1e-5), \
+            (r, got[r], want)
+    assert got[3] in (V - 1, V // 2, 7)
+
+
 def _random_case(seed, V, n, mode, num_logprobs, *, greedy_rows=(), top_k=False, top_p=False,
                  min_p=False, penalties=False, min_tokens=False, device=None):
     rng = np.random.default_rng(seed)

@@ -493,16 +493,39 @@ int mvsd_topk_scores(int32_t* ids, float* scores, int32_t* ranks, const float* l
 int mvsd_sampler_rows(int op, int32_t* ids, float* out, int64_t out_stride, float* x,
                       int64_t stride, const float* aux, int64_t aux_stride, int64_t num_rows,
                       int64_t vocab_size, mvsd_stream_t stream) {
-  if (num_rows < 0 || vocab_size <= 0 || op < 0 || op > 3) return MVSD_E_INVALID;
+  // op 2 (the exponential race) is mvsd_sampler_race
+  if (num_rows < 0 || vocab_size <= 0 || op < 0 || op > 3 || op == 2) return MVSD_E_INVALID;
   if (num_rows == 0) return MVSD_OK;
   if (num_rows > 0x7fffffff || vocab_size > 0x7fffffff) return MVSD_E_RANGE;
   if (!x || stride < vocab_size) return MVSD_E_INVALID;
-  if ((op == mvsd::kSamplerArgmax || op == mvsd::kSamplerRace) && !ids) return MVSD_E_INVALID;
+  if (op == mvsd::kSamplerArgmax && !ids) return MVSD_E_INVALID;
   if (op == mvsd::kSamplerMinP && !aux) return MVSD_E_INVALID;
-  if (op == mvsd::kSamplerRace && (!aux || aux_stride < vocab_size)) return MVSD_E_INVALID;
   if (op == mvsd::kSamplerLogSoftmax && (!out || out_stride < vocab_size)) return MVSD_E_INVALID;
   return hip_status(mvsd::launch_sampler_rows(op, ids, out, out_stride, x, stride, aux,
                                               aux_stride, num_rows, vocab_size,
+                                              (hipStream_t)stream));
+}
+
+int64_t mvsd_sampler_race_workspace_bytes(int64_t num_rows, int64_t vocab_size) {
+  if (num_rows < 0 || vocab_size <= 0) return MVSD_E_INVALID;
+  return mvsd::sampler_race_workspace_bytes(num_rows, vocab_size);
+}
+
+int mvsd_sampler_race(int32_t* ids, const float* x, int64_t stride, const float* noise,
+                      int64_t noise_stride, const float* temperature, int64_t num_rows,
+                      int64_t vocab_size, void* workspace, int64_t workspace_bytes,
+                      mvsd_stream_t stream) {
+  if (num_rows < 0 || vocab_size <= 0) return MVSD_E_INVALID;
+  if (num_rows == 0) return MVSD_OK;
+  if (vocab_size > (int64_t)mvsd::kRaceChunk * mvsd::kRaceMaxChunks) return MVSD_E_RANGE;
+  const int64_t nch = (vocab_size + mvsd::kRaceChunk - 1) / mvsd::kRaceChunk;
+  if (num_rows * nch >= (1ll << 24)) return MVSD_E_RANGE;  // grid threads < 2^32
+  if (!ids || !x || !noise || stride < vocab_size || noise_stride < vocab_size)
+    return MVSD_E_INVALID;
+  if (!workspace || workspace_bytes < mvsd::sampler_race_workspace_bytes(num_rows, vocab_size))
+    return MVSD_E_WORKSPACE;
+  return hip_status(mvsd::launch_sampler_race(ids, x, stride, noise, noise_stride, temperature,
+                                              num_rows, vocab_size, workspace,
                                               (hipStream_t)stream));
 }
 

@@ -105,6 +105,9 @@ SIGNATURES = {
                                    c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
     "mvsd_sampler_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
                                   c_void_p, c_int64, c_int64, c_int64, c_void_p]),
+    "mvsd_sampler_race_workspace_bytes": (c_int64, [c_int64, c_int64]),
+    "mvsd_sampler_race": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                  c_int64, c_int64, c_void_p, c_int64, c_void_p]),
     "mvsd_ngram_propose": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
                                    c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int,
                                    c_int64, c_int32, c_int32, c_int32, c_int, c_int64,

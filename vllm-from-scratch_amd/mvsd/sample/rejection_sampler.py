@@ -107,10 +107,13 @@ class RejectionSampler:
                 "speculative decoding with logprobs=-1 (the whole vocabulary) is not supported; "
                 "request logprobs=k with k >= 1")
 
-        # 1) bonus tokens from the bonus rows with the regular sampler (:169-181)
+        # 1) bonus tokens from the bonus rows with the regular sampler (:169-181); their
+        # full-row logits are asked for only when logprobs are (the sampled tokens do not
+        # depend on it, and the copy is a [B, V] write)
         bonus_logits = logits[metadata.bonus_logits_indices]
         bonus_out = self.sampler.forward(
-            bonus_logits, replace(sampling_metadata, max_num_logprobs=-1),
+            bonus_logits, replace(sampling_metadata, max_num_logprobs=(
+                -1 if max_num_logprobs is not None else None)),
             predict_bonus_token=True,
             logprobs_mode_override=("processed_logits" if self.is_processed_logprobs_mode
                                     else "raw_logits"))

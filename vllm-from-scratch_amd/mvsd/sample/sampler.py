@@ -12,8 +12,11 @@ The rejection sampler takes its bonus tokens from a sampler object (rejection_sa
     -> logprobs of the raw (before any processing) or processed rows on request
 
 Every row operation is a HIP kernel (``mvsd_apply_logits_processors``,
-``mvsd_apply_top_k_top_p``, ``mvsd_sampler_rows``, ``mvsd_spec_logprobs``); the temperature
-divide is a tensor divide, as in the reference.  The exponential noise is drawn by
+``mvsd_apply_top_k_top_p``, ``mvsd_sampler_rows``, ``mvsd_sampler_race``,
+``mvsd_spec_logprobs``).  The temperature divide is a tensor divide, as in the reference,
+except where nothing reads the divided rows (no min_p, top-k or top-p, and no processed_*
+logprobs mode): there the race kernel divides each value as it reads it (the same IEEE fp32
+quotient), and the caller's logits are left undivided.  The exponential noise is drawn by
 ``generate_sampler_noise`` in the reference's order (the whole block from the global RNG when
 some row has no generator, then each seeded row from its generator), so a given RNG state
 gives the same noise; the function is a seam that tests may replace.
@@ -29,7 +32,7 @@ from ..outputs import LogprobsTensors, SamplerOutput
 from .metadata import SAMPLING_EPS, SamplingMetadata
 from .ops.topk_topp_sampler import apply_top_k_top_p
 
-_ARGMAX, _MIN_P, _RACE, _LOG_SOFTMAX = 0, 1, 2, 3
+_ARGMAX, _MIN_P, _LOG_SOFTMAX = 0, 1, 3
 
 
 def generate_sampler_noise(shape, generators: dict[int, torch.Generator],
@@ -53,14 +56,28 @@ def _rows(op, x: torch.Tensor, *, ids=None, out=None, aux=None):
         nat.stream_of(x.device)), "mvsd_sampler_rows")
 
 
-def random_sample(probs_logits: torch.Tensor, generators: dict[int, torch.Generator]):
+def random_sample(probs_logits: torch.Tensor, generators: dict[int, torch.Generator],
+                  temperature: torch.Tensor | None = None):
     """argmax of softmax(row) / E per row (the exponential race, ops/topk_topp_sampler.py:82-90,
-    with the softmax of the processed logits folded in)."""
+    with the softmax of the processed logits folded in); with ``temperature`` ([N] fp32,
+    positive) each row is first divided by its temperature inside the kernel.  One
+    ``mvsd_sampler_race`` call."""
     x = probs_logits.contiguous()
+    nat.require_device_tensor(x, "logits")
+    assert x.ndim == 2 and x.dtype == torch.float32
+    n, V = x.shape
     noise = generate_sampler_noise(tuple(x.shape), generators, x.device)
     noise = noise.to(device=x.device, dtype=torch.float32).contiguous()
-    ids = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)
-    _rows(_RACE, x, ids=ids, aux=noise)
+    ids = torch.empty(n, dtype=torch.int32, device=x.device)
+    if temperature is not None:
+        temperature = temperature.to(device=x.device, dtype=torch.float32).contiguous()
+    lib = nat.lib()
+    ws = torch.empty(max(1, lib.mvsd_sampler_race_workspace_bytes(n, V)), dtype=torch.uint8,
+                     device=x.device)
+    nat.check(lib.mvsd_sampler_race(
+        ids.data_ptr(), x.data_ptr(), x.stride(0), noise.data_ptr(), noise.stride(0),
+        nat.ptr(temperature), n, V, ws.data_ptr(), ws.numel(), nat.stream_of(x.device)),
+        "mvsd_sampler_race")
     return ids.to(torch.int64)
 
 
@@ -213,11 +230,20 @@ class Sampler:
         if temperature is None:
             raise ValueError("random rows in the batch but no temperature tensor")
         safe = torch.where(temperature < SAMPLING_EPS, torch.ones_like(temperature), temperature)
-        logits = logits.div_(safe.unsqueeze(dim=1))
-        logits = self.apply_min_p(logits, sampling_metadata.min_p)
-        random_sampled, processed = self.topk_topp_sampler(
-            logits, sampling_metadata.generators, sampling_metadata.top_k,
-            sampling_metadata.top_p)
+        if (sampling_metadata.min_p is None and sampling_metadata.top_k is None
+                and sampling_metadata.top_p is None
+                and self.topk_topp_sampler.logprobs_mode not in ("processed_logits",
+                                                                 "processed_logprobs")):
+            # nothing reads the divided rows: the race divides as it reads
+            random_sampled = random_sample(logits, sampling_metadata.generators,
+                                           temperature=safe)
+            processed = None
+        else:
+            logits = logits.div_(safe.unsqueeze(dim=1))
+            logits = self.apply_min_p(logits, sampling_metadata.min_p)
+            random_sampled, processed = self.topk_topp_sampler(
+                logits, sampling_metadata.generators, sampling_metadata.top_k,
+                sampling_metadata.top_p)
         if greedy_sampled is None:
             return random_sampled, processed
         return torch.where(temperature < SAMPLING_EPS, greedy_sampled, random_sampled), processed
