@@ -46,6 +46,11 @@ def _args(w, out, workspace=None):
     a.num_tokens = w.num_tokens
     a.vocab_size = w.vocab_size
     a.max_spec_len = w.max_spec_len
+    if w.top_k is not None or w.top_p is not None:
+        # sampling constraints in the kernels, after the temperature divide
+        a.top_k = None if w.top_k is None else w.top_k.data_ptr()
+        a.top_p = None if w.top_p is None else w.top_p.data_ptr()
+        a.apply_temperature = 1
     if workspace is not None:
         a.workspace = workspace.data_ptr()
         a.workspace_bytes = workspace.numel()
@@ -95,6 +100,16 @@ def test_static_scratch_repeated_calls(device):
     for w in (a, b, a):
         ref, got = _run_both(w, device)
         assert np.array_equal(ref, got), f"{w.name}: static-scratch entry differs"
+
+
+@pytest.mark.gpu
+def test_static_scratch_masked_batch(device):
+    """A batch with top-k / top-p (C4-shaped, smaller): the plan, the constraints kernel and
+    the masked verify kernel use the static scratch's mask and plan arrays; the tokens are the
+    workspace entry's."""
+    w = configs.ragged_c4(device, B=96, seed=9103)
+    ref, got = _run_both(w, device)
+    assert np.array_equal(ref, got), "masked batch: static-scratch entry differs"
 
 
 def test_static_scratch_refuses_oversized_batches():
