@@ -158,6 +158,19 @@ def test_chains_longer_than_a_wavefront(block):
     assert n[0] == 101 and n[3] == 66
 
 
+@pytest.mark.parametrize("block", [False, True])
+def test_batch_many_rows(block):
+    """About 1000 logits rows in 240 requests at V = 4096: some greedy, some without drafts,
+    some with an invalid draft."""
+    g = np.random.default_rng(61 + block)
+    R, K = 240, 4
+    nd = [int(x) for x in g.integers(0, K + 1, R)]
+    temps = [0.0 if x < 0.3 else float(x) for x in g.uniform(0.0, 1.5, R)]
+    invalid = {(r, int(g.integers(0, K))) for r in range(0, R, 11)}
+    case = make_case(nd, temps, K, 4096, seed=61, states=R + 5, invalid=invalid)
+    _compare(case, f"R={R} block={block}", use_block_verification=block)
+
+
 def test_block_and_standard_differ():
     temps = [0.9] * 16
     case = make_case([4] * 16, temps, 4, 4096, seed=43)
