@@ -190,6 +190,30 @@ def test_fallback_paths(device, case):
     _check_against_oracle(x, got, ks_np, ps_np, case)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_greedy_rows_with_tied_maxima(device, dtype):
+    """Greedy rows whose maximum is tied, under top-p values on both sides of the point where
+    the masked prefix reaches the maximum: each mask is neutral (the prefix stops below the
+    maximum, so the argmax is unchanged) or the processed path's mask exactly, and the first
+    unmasked maximum is the processed path's argmax."""
+    V, n = 4096, 24
+    g = np.random.default_rng(8)
+    x = g.normal(0, 1, size=(n, V)).astype(np.float32)
+    for r in range(n):
+        ties = int(g.integers(2, 7))
+        x[r, g.choice(V, ties, replace=False)] = 9.0 if r % 2 else 4.0
+    x = torch.from_numpy(x).to(dtype).float().numpy()  # values the rows hold
+    ps = [0.1, 0.3, 0.5, 0.6, 0.9, 1e-7] * 4
+    target, cu, sm = _single_request_rows(device, x, [0.0] * n, [V] * n, ps, dtype=dtype)
+    masks = sampling_masks(target, cu, sm)
+    got = _expand(masks, x)
+    processed = apply_sampling_constraints(target.float().clone(), cu, sm)
+    want = ~torch.isfinite(processed).cpu().numpy()
+    _greedy_rows_unmasked_or_exact(masks, got, want, x, np.ones(n, dtype=bool))
+    reach = [r for r in range(n) if want[r][x[r] == x[r].max()].any()]
+    assert 0 < len(reach) < n, reach  # both cases occur
+
+
 def test_greedy_row_argmax_respects_top_p_tie_order(device):
     """A greedy request in a mixed batch is masked too (the reference divides by 1 and masks
     every row): with a tiny top_p only the last of the tied maxima survives, so the greedy

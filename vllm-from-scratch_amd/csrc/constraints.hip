@@ -393,6 +393,63 @@ __global__ __launch_bounds__(1024) void constraint_plan_kernel(VerifyParams p) {
   }
 }
 
+// Top-p of a greedy row whose maximum is tied (ties >= 2 entries at raw key mkey), without
+// top-k.  Only the row's argmax matters, and the temperature is 1, so v = x and the tied
+// entries are exactly the entries at the maximum, each of mass mass_of(0) = 2^40.  The masked
+// prefix of the order (v, index) reaches them only when the mass below the maximum is at most
+// the limit; then it takes every entry below the maximum and the first m tied entries in index
+// order, m = floor((limit - below) / 2^40) (at most ties - 1: the last entry is always kept).
+// One pass sums the masses; a second gathers the tied entries' indices only when the prefix
+// reaches them.  Returns 0 (no mask changes the argmax: the neutral mask), 1 (A, B, J set), or
+// -1 (more tied entries than LDS holds: the general path).
+template <int DT>
+__device__ inline int greedy_tied_top_p(const typename Elem<DT>::storage* __restrict__ x, int V,
+                                        bool aligned, const Divider& dv, float T, float t,
+                                        uint32_t mkey, unsigned long long ties,
+                                        ConstraintSmem& sm, float& A, float& Bv, int& J) {
+  constexpr int VEC = Elem<DT>::kVec;
+  const float vmax = divide(dv, key_float(mkey));
+  if (vmax != vmax || fabsf(vmax) == INFINITY) return 0;
+  unsigned long long s = 0;
+  for_each_group<DT>(x, V, aligned, [&](int, const float (&v)[VEC], int n) {
+    float q[VEC];
+    divide_group(dv, v, q);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j)
+      if (j < n) s += mass_of(vmax - q[j]);
+  });
+  const unsigned long long total = block_sum_u64(s, sm);
+  const unsigned long long limit = scaled_floor(fminf(t, 1.f), total);
+  constexpr unsigned long long kUnit = 1ull << 40;  // mass_of(0)
+  const unsigned long long below = total - ties * kUnit;
+  if (limit < below + kUnit) return 0;  // the first maximum is kept
+  if (ties > (unsigned long long)kCap) return -1;
+  unsigned long long m = (limit - below) / kUnit;
+  if (m > ties - 1) m = ties - 1;
+  if (threadIdx.x == 0) sm.count = 0;
+  __syncthreads();
+  for_each_group<DT>(x, V, aligned, [&](int i0, const float (&v)[VEC], int n) {
+    bool c[VEC], any = false;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      c[j] = (j < n) && ordered_bits(v[j]) == mkey;
+      any |= c[j];
+    }
+    if (__ballot(any) == 0) return;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j)
+      append(c[j], c[j] ? (((unsigned long long)mkey << 32) | (uint32_t)(i0 + j)) : 0ull, sm);
+  });
+  __syncthreads();
+  const int n = sm.count;  // == ties
+  sort_candidates(n, sm);
+  const int i_f = (int)(uint32_t)sm.u.cand[min((int)m, n - 1)];
+  A = min_x_reaching(vmax, T);
+  Bv = min_x_reaching(next_up(vmax), T);
+  J = i_f - 1;
+  return 1;
+}
+
 // The row's mask (A, B, J) from its request's top-k / top-p; false when nothing is masked.
 template <int DT>
 __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, ConstraintSmem& sm, float& A,
@@ -459,6 +516,10 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
   if (greedy_row) {
     const unsigned long long ties = block_sum_u64(t0 == mkey ? t1 : 0u, sm);
     if (mkey == kNanKey || ties < 2) return false;
+    if (!has_k) {
+      const int g = greedy_tied_top_p<DT>(x, V, aligned, dv, T, t, mkey, ties, sm, A, Bv, J);
+      if (g >= 0) return g == 1;
+    }
   }
 
   // ---- top-k: v_k, the k-th largest v, and the entries with v >= v_k in LDS if they fit ----

@@ -81,7 +81,8 @@ constexpr int kFull = 2;  // random request whose recovered id comes from in-ker
 // row, rows (clamped as by req_range) with the flags above bit 16, log2(e) / T, and the
 // score units (position in the unit order << 12 | request) of the kFull requests.
 struct Tables {
-  int* goff;   // [B + 1]
+  int* gpos;    // [B + 1] by position: first group << 12 | request; gpos[B] = groups << 12
+  int* gstart;  // [B] first group of request r
   int* begin;  // [B]
   int* kflags;  // [B]
   float* c1;   // [B]
@@ -689,7 +690,7 @@ __device__ inline void decide_position(const VerifyParams& p, int r, bool greedy
 
 // Stats slots of row k of request r: nc, or 2 nc when its group is in the tail.
 __device__ inline int row_slot_count(const VerifyParams& p, const Tables& tb, int r, int k) {
-  return tb.goff[r] + k / p.G >= tb.gt ? 2 * p.nc : p.nc;
+  return tb.gstart[r] + k / p.G >= tb.gt ? 2 * p.nc : p.nc;
 }
 
 struct DecideSmem {
@@ -873,38 +874,56 @@ __device__ inline int block_exclusive_scan(int v, int& total, int* s_wave) {
 }
 
 // Every workgroup builds the tables: each thread reads the metadata of a run of consecutive
-// requests once, then two block scans give the group offsets and the kFull ordinals.
-// Requests without drafts get their output row here (bonus, then -1), from workgroup
-// r mod grid.
+// requests once, then block scans give the group offsets and the kFull ordinals.  Stats
+// groups run random requests first, then greedy requests (each in request order): greedy
+// requests have no score units, so the launch ends on stats tasks that nothing waits for,
+// rather than on score tasks waiting for the last decisions.  Requests without drafts get
+// their output row here (bonus, then -1), from workgroup r mod grid.
 __device__ inline void build_tables(const VerifyParams& p, Tables& tb, int* s_wave) {
   const int tid = threadIdx.x;
   const int per = (p.B + kVThreads - 1) / kVThreads;
   const int r0 = tid * per, r1 = min(p.B, r0 + per);
-  int run_g = 0, run_f = 0;
+  // per class (random, greedy): requests << 18 | groups, which a launch keeps below 2^31
+  int run_r = 0, run_g = 0, run_f = 0;
   for (int r = r0; r < r1; ++r) {
     int b, k;
     req_range(p, r, b, k);
     const int ng = (k + p.G - 1) / p.G;
     const bool greedy = req_is_greedy(p, r);
     const bool full = !greedy && !p.recovered && k > 0;
-    tb.goff[r] = ng;
-    run_g += ng;
+    tb.gstart[r] = ng;
+    if (greedy) run_g += (1 << 18) + ng;
+    else run_r += (1 << 18) + ng;
     run_f += full ? 1 : 0;
     tb.begin[r] = b;
     tb.kflags[r] = k | ((greedy ? kGreedy : 0) | (full ? kFull : 0)) << 16;
     tb.c1[r] = exp2_scale(req_temperature(p, r));
   }
-  int groups, nfull;
-  int acc_g = block_exclusive_scan(run_g, groups, s_wave);
-  __syncthreads();  // s_wave is reused by the second scan
+  int tot_r, tot_g, nfull;
+  int acc_r = block_exclusive_scan(run_r, tot_r, s_wave);
+  __syncthreads();  // s_wave is reused by each scan
+  int acc_g = block_exclusive_scan(run_g, tot_g, s_wave);
+  __syncthreads();
   int acc_f = block_exclusive_scan(run_f, nfull, s_wave);
+  const int groups_r = tot_r & 0x3ffff, nreq_r = tot_r >> 18;
+  const int groups = groups_r + (tot_g & 0x3ffff);
   for (int r = r0; r < r1; ++r) {
-    const int ng = tb.goff[r];
-    tb.goff[r] = acc_g;
-    acc_g += ng;
+    const int ng = tb.gstart[r];
     const int kf = tb.kflags[r];
+    int g0, pos;
+    if ((kf >> 16) & kGreedy) {
+      g0 = groups_r + (acc_g & 0x3ffff);
+      pos = nreq_r + (acc_g >> 18);
+      acc_g += (1 << 18) + ng;
+    } else {
+      g0 = acc_r & 0x3ffff;
+      pos = acc_r >> 18;
+      acc_r += (1 << 18) + ng;
+    }
+    tb.gstart[r] = g0;
+    tb.gpos[pos] = g0 << 12 | r;
     if ((kf >> 16) & kFull) {
-      tb.fpos[acc_f] = (acc_f + min(groups, acc_g + p.lag)) << 12 | r;
+      tb.fpos[acc_f] = (acc_f + min(groups, g0 + ng + p.lag)) << 12 | r;
       ++acc_f;
     }
     if (ng == 0 && (r % (int)gridDim.x) == (int)blockIdx.x) {
@@ -912,7 +931,7 @@ __device__ inline void build_tables(const VerifyParams& p, Tables& tb, int* s_wa
       for (int c = 0; c <= p.max_spec_len; ++c) out[c] = c == 0 ? p.bonus[r] : -1;
     }
   }
-  if (tid == 0) tb.goff[p.B] = groups;
+  if (tid == 0) tb.gpos[p.B] = groups << 12;
   __syncthreads();
   tb.groups = groups;
   tb.nfull = nfull;
@@ -968,17 +987,17 @@ __device__ inline void fetch_task(const VerifyParams& p, const Tables& tb, int t
     } else {
       kind = kStatsTask;
       const int li = u - lo;
-      int a = 0, b = p.B - 1;  // the last request whose first group is <= li owns it
+      int a = 0, b = p.B - 1;  // the last position whose first group is <= li owns it
       while (a < b) {
         const int mid = (a + b + 1) / 2;
-        if (tb.goff[mid] <= li) a = mid;
+        if ((tb.gpos[mid] >> 12) <= li) a = mid;
         else b = mid - 1;
       }
-      r = a;
+      r = tb.gpos[a] & 0xfff;
       const int kf = tb.kflags[r];
       const int k = kf & 0xffff;
-      const int g = li - tb.goff[r];
-      const int ng = tb.goff[r + 1] - tb.goff[r];
+      const int g = li - (tb.gpos[a] >> 12);
+      const int ng = (tb.gpos[a + 1] >> 12) - (tb.gpos[a] >> 12);
       row0 = tb.begin[r] + g * p.G;
       info = min(p.G, k - g * p.G) | ng << 8 | (kf >> 16) << 16;
     }
@@ -1028,7 +1047,7 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
   __shared__ int s_dec;
   __shared__ int s_wave[kVWaves];
   __shared__ DecideSmem dsm;
-  __shared__ int s_goff[kMaxLaunchRequests + 1];
+  __shared__ int s_gpos[kMaxLaunchRequests + 1], s_gstart[kMaxLaunchRequests];
   __shared__ int s_begin[kMaxLaunchRequests], s_kf[kMaxLaunchRequests], s_fpos[kMaxLaunchRequests];
   __shared__ float s_c1[kMaxLaunchRequests];
 
@@ -1037,7 +1056,7 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
   // the first ticket is claimed before the tables are built, so its round trip overlaps them
   int tfirst = 0;
   if (tid == 0) tfirst = atomic_add_relaxed(ticket, 1);
-  Tables tb{s_goff, s_begin, s_kf, s_c1, s_fpos, 0, 0};
+  Tables tb{s_gpos, s_gstart, s_begin, s_kf, s_c1, s_fpos, 0, 0};
   build_tables(p, tb, s_wave);
   const int total = tb.u0 * p.nc + (tb.groups + tb.nfull - tb.u0) * 2 * p.nc;
 
@@ -1078,7 +1097,7 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
       else
         task_stats<DT, EPT, G, MASKED>(p, c, c1, row0, nrows, v0, vend, s_red, s_M, prefetch);
       // the request's stats tasks: nc per group, 2 nc per tail group
-      const int g0 = tb.goff[r], g1 = tb.goff[r + 1];
+      const int g0 = tb.gstart[r], g1 = g0 + ngr;
       const int ntasks = p.nc * (ngr + max(0, g1 - max(g0, tb.gt)));
       if (tid == 0) s_last = started == ntasks - 1;
       __syncthreads();
@@ -1108,7 +1127,7 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
         const int row = row0 + d - 1;
         const int draft = DD >= 0 ? -1 : p.draft_ids[row];
         bool ok;
-        const int nslots = tb.goff[r] + (d - 1) / p.G >= tb.gt ? 2 * p.nc : p.nc;
+        const int nslots = tb.gstart[r] + (d - 1) / p.G >= tb.gt ? 2 * p.nc : p.nc;
         key = task_score<DT, 2 * EPT, DD, MASKED>(p, r, c1, row, nslots, draft, v0, vend,
                                                          s_key, s_ml, ok, prefetch);
         if (!ok) key = kFailKey;
