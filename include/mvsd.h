@@ -197,7 +197,8 @@ int mvsd_rejection_sample_static(const mvsd_rejection_args* args, mvsd_stream_t 
 /* (A, B, J as int bits, 0): entry i of verify row j, raw value x (before the temperature  */
 /* divide), is masked iff x < A || (x < B && i <= J).  Rows without constraints get        */
 /* (-inf, -inf, -1), and so do the rows of greedy requests whose argmax no mask can change */
-/* (top-k never masks a maximum; top-p masks one only when the maximum is tied).            */
+/* (top-k never masks a maximum; top-p masks one only when the maximum is tied and the     */
+/* entries below it hold at most 1 - p of the mass).                                        */
 /* ------------------------------------------------------------------------------------ */
 int mvsd_sampling_masks(const mvsd_rejection_args* args, float* masks, mvsd_stream_t stream);
 

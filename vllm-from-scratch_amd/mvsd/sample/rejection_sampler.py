@@ -607,7 +607,8 @@ def sampling_masks(target_logits: torch.Tensor, cu_num_draft_tokens: torch.Tenso
     ``x < A or (x < B and i <= J)`` -- the entries ``apply_sampling_constraints`` (:537-571)
     would set to -inf.  Rows without constraints get (-inf, -inf, -1), and so do the rows of
     greedy requests whose argmax no mask can change: top-k never masks a row's maximum, and
-    top-p masks one only when the maximum is tied (such a row gets its full mask)."""
+    top-p masks one only when the maximum is tied and the entries below it hold at most 1 - p
+    of the mass (such a row gets its full mask)."""
     device = target_logits.device
     nat.require_device_tensor(target_logits, "target_logits")
     if target_logits.stride(1) != 1:
