@@ -419,7 +419,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
-                          "(multi-GPU sharding is described in DESIGN.md, not launched)"}))
+                          "(request or vocabulary sharding across GPUs is not launched)"}))
         sys.exit(2)
     device = torch.device("cuda", 0)
     if args.config == "c3":
