@@ -26,7 +26,7 @@ Randomness is drawn by the same seams as the reference, and both stay monkeypatc
 ``sample_recovered_tokens`` (one Exp(1) row per request, drawn by
 ``generate_exponential_noise``).  Callers may also pass them explicitly
 (``uniform_probs=``, ``exp_noise=``).  When a test replaces ``sample_recovered_tokens``
-the fused kernel takes its result as the recovered ids, as the reference's random kernel
+the verify kernel takes its result as the recovered ids, as the reference's random kernel
 does.
 
 Differences from the reference, all on inputs the reference does not define:
