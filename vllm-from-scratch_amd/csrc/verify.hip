@@ -525,9 +525,55 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
 }
 
 // ------------------------------------------------------------------ score tasks ------
+// Score tasks read three rows per column (target, draft, noise) and lay all three out in
+// quads: 4 consecutive columns per lane and load, consecutive lanes on consecutive quads (the
+// fp32 layout, elem_index<MVSD_F32>, whatever the target type).  Every load instruction of a
+// wave then covers one contiguous span of each row: 512 bytes of a 2-byte target, 1 KB of fp32
+// noise.  In the 16-byte-vector layout of a 2-byte target a lane owns 8 columns, and its two
+// fp32 noise (and draft) loads of one sub-chunk lie 16 bytes apart with the next lane's 32 bytes
+// on: each instruction would cover every other 16 bytes of a 2 KB span.
+template <int DT>
+using TargetQuad = std::conditional_t<Elem<DT>::kVec == 4, u32x4, u32x2>;
+
+// Target row sub-chunk in quads; FAST: full and aligned, else bounds-checked with `fill`.
+template <int DT, int EPT, bool FAST>
+__device__ inline void load_target_quads(const typename Elem<DT>::storage* __restrict__ base,
+                                         int64_t s0, int64_t vend, bool aligned,
+                                         typename Elem<DT>::storage fill,
+                                         TargetQuad<DT> (&out)[EPT / 4]) {
+  if constexpr (Elem<DT>::kVec == 4) {
+    if constexpr (FAST) load_raw<DT, EPT, true>(base, s0, out);
+    else load_raw_checked<DT, EPT, true>(base, s0, vend, aligned, fill, out);
+  } else {
+#pragma unroll
+    for (int m = 0; m < EPT / 4; ++m) {
+      const int64_t col = vec_col<MVSD_F32>(s0, m);
+      if (FAST || (aligned && col + 4 <= vend)) {
+        out[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(base + col));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t lo = bits16(col + 2 * j < vend ? base[col + 2 * j] : fill);
+          const uint32_t hi = bits16(col + 2 * j + 1 < vend ? base[col + 2 * j + 1] : fill);
+          out[m][j] = lo | hi << 16;
+        }
+      }
+    }
+  }
+}
+
+// Element k (0 <= k < EPT) of a target buffer in quads, as fp32.
+template <int DT>
+__device__ inline float quad_elem(const TargetQuad<DT>* x, int k) {
+  using S = typename Elem<DT>::storage;
+  const S* s = reinterpret_cast<const S*>(&x[k / 4]);
+  return Elem<DT>::cvt(s[k % 4]);
+}
+
 template <int DT, int DD, int EPT>
 struct ScoreBuf {
-  u32x4 x[EPT / Elem<DT>::kVec];
+  static_assert(EPT % 4 == 0, "score tasks load whole quads");
+  TargetQuad<DT> x[EPT / 4];
   DraftBuf<DD < 0 ? MVSD_F32 : DD, DD < 0 ? 4 : EPT> q;  // unused without draft probs
   u32x4 e[EPT / 4];
 };
@@ -554,10 +600,9 @@ __device__ inline uint64_t task_score(const VerifyParams& p, int r, float c1, in
 
   auto load = [&](Buf& buf, int64_t s0, auto fast) {
     constexpr bool F = decltype(fast)::value;
-    if constexpr (F) load_raw<DT, EPT, true>(tb, s0, buf.x);
-    else load_raw_checked<DT, EPT, true>(tb, s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x);
-    if constexpr (HAS_DRAFT) load_draft<DT, DD, EPT, F>(qb, s0, vend, p.draft_aligned, buf.q);
-    load_raw_f32<DT, EPT, F>(eb, s0, vend, p.noise_aligned, 1.f, buf.e);
+    load_target_quads<DT, EPT, F>(tb, s0, vend, p.target_aligned, Elem<DT>::ninf(), buf.x);
+    if constexpr (HAS_DRAFT) load_draft<MVSD_F32, DD, EPT, F>(qb, s0, vend, p.draft_aligned, buf.q);
+    load_raw_f32<MVSD_F32, EPT, F>(eb, s0, vend, p.noise_aligned, 1.f, buf.e);
   };
 
   float MX = 0.f, NL = 0.f;
@@ -591,8 +636,8 @@ __device__ inline uint64_t task_score(const VerifyParams& p, int r, float c1, in
     for (int k = 0; k < EPT; ++k) inv[k] = recip_rn(raw_f32(buf.e, k));
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
-      const int idx = elem_index<DT, EPT>(s0, k);
-      const float x = raw_elem<DT>(buf.x, k);
+      const int idx = elem_index<MVSD_F32, EPT>(s0, k);
+      const float x = quad_elem<DT>(buf.x, k);
       float prob = __builtin_amdgcn_exp2f(fmaf(x - MX, c1, NL));  // softmax
       if constexpr (MASKED) prob = row_masked(mk, x, idx) ? 0.f : prob;
       float w;
