@@ -298,20 +298,32 @@ __device__ inline void pipeline(int64_t v0, int64_t vend, bool aligned, Load&& l
 // kKeep * 64 of them in registers (v[j] holds slot lane + 64 j).  Gives up after
 // p.spin_limit polls, or sooner once the failure flag ctrl[1] is set (so one wait that cannot
 // complete ends every other wait quickly); giving up sets the flag and returns false.
+// first_read: v already holds a first read of those slots (wave_read_slots), issued ahead of
+// other loads so that the in-order load counter does not hold the poll behind them.
 constexpr int kKeep = 2;
 
-__device__ inline bool wave_poll(const VerifyParams& p, const uint64_t* slots, int n,
-                                 uint64_t (&v)[kKeep]) {
-  const int lane = lane_id();
+__device__ inline void wave_read_slots(const uint64_t* slots, int n, uint64_t (&v)[kKeep]) {
 #pragma unroll
-  for (int j = 0; j < kKeep; ++j) v[j] = 0;
+  for (int j = 0; j < kKeep; ++j) {
+    const int c = lane_id() + j * kWave;
+    v[j] = c < n ? slot_load(slots + c) : 0;
+  }
+}
+
+__device__ inline bool wave_poll(const VerifyParams& p, const uint64_t* slots, int n,
+                                 uint64_t (&v)[kKeep], bool first_read = false) {
+  const int lane = lane_id();
+  if (!first_read) {
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j) v[j] = 0;
+  }
   for (int spins = 0;; ++spins) {
     if (spins >= p.spin_limit) break;
     int ready = 1;
 #pragma unroll
     for (int j = 0; j < kKeep; ++j) {
       const int c = lane + j * kWave;
-      v[j] = c < n ? slot_load(slots + c) : 0;
+      if (!first_read || spins > 0) v[j] = c < n ? slot_load(slots + c) : 0;
       ready &= (c >= n) | (v[j] != 0);
     }
     for (int c = lane + kKeep * kWave; c < n; c += kWave) ready &= slot_load(slots + c) != 0;
@@ -580,7 +592,7 @@ struct ScoreBuf {
 
 // The rejected row `row` of random request r: the chunk-local argmax of max(p - q, 0) * (1 / E)
 // over [v0, vend) (point-mass drafts: p with the draft id d removed, :891-897).  The row's
-// statistics come from its nslots stats slots, polled by wave 0 while the first sub-chunk
+// statistics come from its nslots stats slots, polled by wave 1 while the first sub-chunk
 // loads.
 // Returns the chunk's argmax key in thread 0; ok = false if the statistics wait gave up.
 template <int DT, int EPT, int DD, bool MASKED, typename Hook>
@@ -606,12 +618,18 @@ __device__ inline uint64_t task_score(const VerifyParams& p, int r, float c1, in
   };
 
   float MX = 0.f, NL = 0.f;
+  // Wave 1 polls, so that the poll overlaps the next ticket's decode in thread 0 (after_loads),
+  // and its first read of the slots is issued before the first sub-chunk's loads, so that the
+  // wave's in-order load counter does not hold the poll behind them (wave 0 polling after its
+  // loads measured 1.0 % slower at the headline, 2.2 % at an EAGLE-sized bf16 batch).
+  static_assert(kVWaves >= 2, "the statistics poll runs on wave 1");
+  const uint64_t* slots = p.stat_slots + row * slot_stride(p);
+  uint64_t v[kKeep];
+  if (wave_id() == 1) wave_read_slots(slots, nslots, v);
   auto wait_stats = [&]() {
     after_loads();
-    if (wave_id() == 0) {
-      uint64_t v[kKeep];
-      const uint64_t* slots = p.stat_slots + row * slot_stride(p);
-      const bool polled = wave_poll(p, slots, nslots, v);
+    if (wave_id() == 1) {
+      const bool polled = wave_poll(p, slots, nslots, v, true);
       float mx, sum;
       combine_stats(slots, nslots, v, c1, mx, sum);
       if (lane_id() == 0) {
