@@ -343,6 +343,24 @@ def test_odd_vocab_sizes(device, V):
     assert np.array_equal(run_workload(g).cpu().numpy(), oracle_for(g).output_token_ids)
 
 
+@pytest.mark.parametrize("ddtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("V", [4097, 8200, 151936])
+def test_bf16_target_score_loads(device, V, ddtype):
+    """Random requests on a bf16 target, so that score tasks run on 2-byte targets: 4 columns
+    per lane and load for the target, draft and noise rows.  V = 4097 leaves the rows unaligned
+    (every load bounds-checked, element by element), V = 8200 ends each row in a partial
+    sub-chunk (8-byte loads where a quad fits, checked loads past it)."""
+    w = configs.random_c2(device, B=32, k=4, V=V, seed=V + 17)
+    w = replace(w, target_logits=w.target_logits.to(torch.bfloat16),
+                draft_probs=w.draft_probs.to(ddtype))
+    out = run_workload(w)
+    ref = oracle_for(w)
+    rejected = sum(len([t for t in row if t != -1]) <= k
+                   for row, k in zip(ref.output_token_ids.tolist(), w.num_draft_tokens))
+    assert rejected > 0, "no request rejected a draft: no score task ran"
+    check_parity(w, out, ref, f"bf16 target V={V} draft {ddtype}")
+
+
 def test_repeated_calls_are_identical(device):
     w = configs.random_c2(device, B=32, k=4, seed=5)
     a = run_workload(w)
@@ -482,8 +500,8 @@ def test_corrected_reciprocal_equals_ieee_division(device):
 def test_16bit_draft_probs(device, ddtype, case):
     """draft_probs in bf16 / fp16, upcast in the kernel (the reference's kernels load them in
     their own dtype and compute in fp32, rejection_sampler.py:797-806, :882-890): against the
-    oracle on the same 16-bit values upcast.  fp32 targets take 8-byte draft loads, 16-bit
-    targets 16-byte loads; odd V takes the bounds-checked loads."""
+    oracle on the same 16-bit values upcast.  Score tasks load 16-bit drafts 4 columns (8 bytes)
+    per lane for every target type; odd V takes the bounds-checked loads."""
     w = {"c2": lambda: configs.random_c2(device, B=48, k=4, seed=301),
          "odd_v": lambda: configs.random_c2(device, B=24, k=3, V=4097, seed=302),
          "c4_bf16_target": lambda: configs.ragged_c4(device, B=96, seed=303)}[case]()
