@@ -319,9 +319,8 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
     // The last groups' stats tasks and every score task after them cover half chunks, so
     // that the dependent decisions and scores at the end of the launch are short.  Half
     // tasks cost more per byte, so the tail groups hold about one half-chunk stats ticket per
-    // four workgroups (one or two per workgroup measured about 1 % slower, none 0.7 % slower
-    // on a mixed bf16 batch).
-    q.tail_groups = (int)((grid + 8 * plan.nc - 1) / (8 * plan.nc));
+    // two workgroups (a quarter of that, or none, measured 0.3-1.2 % slower on bf16 batches).
+    q.tail_groups = (int)((grid + 4 * plan.nc - 1) / (4 * plan.nc));
     // every workgroup may claim two tickets past the last task
     if (units * 2 * plan.nc > 0x7fffffff - 4 * grid) return MVSD_E_RANGE;
     err = mvsd::launch_verify(q, a->target_dtype, (int)grid, (hipStream_t)stream);
