@@ -1267,11 +1267,11 @@ hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream) {
 constexpr int kGroup = 4;          // rows per stats group
 constexpr int kMinSubs = 8;        // sub-chunks per task at least
 // Every task has fixed costs (its first loads' latency, block reductions, publication), so
-// tasks are as long as the tail allows: 7 per workgroup and up to 768 KiB per stats task measured
-// 1.5 % faster at the headline, 3.7 % on an EAGLE-sized bf16 batch and 1.8 % on a ragged one than
-// 10 and 512 KiB; 1.5 MiB tasks lengthened the ragged batch's tail (3 % slower).
+// tasks are as long as the tail allows: about 7 per resident workgroup measured 1.5 % faster at
+// the headline and 1.8 % on a ragged bf16 batch than 10 (with tasks capped at 512 KiB).  On large
+// batches the 7 tasks are long (whole 1.2 MB bf16 row groups on an EAGLE-sized batch, 6 %
+// faster than 512 KiB tasks); the tail is then a small share of the launch.
 constexpr int kTasksPerWg = 7;     // tasks per resident workgroup aimed for
-constexpr int64_t kTaskBytes = 768 * 1024;  // target bytes of a stats task at most (about 22 us)
 template <int DT>
 constexpr int ept_of() {
   return DT == MVSD_F32 ? 4 : 8;  // 16 bytes of target per thread and row per sub-chunk
@@ -1287,16 +1287,12 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int 
   // long as possible (fewer ticket claims, longer load pipelines), and at least kMinSubs
   // sub-chunks per task so that small batches do not shred the rows into tasks too short to
   // amortise their start and end.
-  // Long tasks also lengthen the launch's tail, so a stats task reads at most about kTaskBytes.
   // Score tasks walk sub-chunks of twice the columns, so chunks hold an even number of
   // sub-chunks.
   const int64_t nc_max = nsub / kMinSubs > 1 ? nsub / kMinSubs : 1;
   int64_t nc = nc_max;
   if (units > 0 && cap > 0) {
-    const int64_t esize = target_dtype == MVSD_F32 ? 4 : 2;
-    const int64_t by_bytes = (vocab_size * kGroup * esize + kTaskBytes - 1) / kTaskBytes;
     nc = ((int64_t)kTasksPerWg * cap + units - 1) / units;
-    nc = nc < by_bytes ? by_bytes : nc;
     nc = nc < 1 ? 1 : (nc > nc_max ? nc_max : nc);
   }
   int64_t subs_per_chunk = (nsub + nc - 1) / nc;
