@@ -417,8 +417,9 @@ int mvsd_v2_rejection_sample(
 /* v2_flatten_sampled — the V2 sampled tokens, one per logits row.                         */
 /* Replaces: flatten_sampled / _flatten_sampled_kernel (minivllm/worker/gpu/spec_decode/   */
 /*           rejection_sampler.py:73-108).  Row cu_num_logits[r] + j of flat_sampled       */
-/* [num_logits] int64 gets sampled[r * sampled_stride + j] for j < num_sampled[r], 0 for   */
-/* the other rows of the request.                                                          */
+/* [num_logits] int64 gets sampled[r * sampled_stride + j] for j < num_sampled[r]; every  */
+/* other row (the rest of each request's rows, rows no request covers) gets 0, as after   */
+/* the reference's zero fill.                                                              */
 /* ------------------------------------------------------------------------------------ */
 int mvsd_v2_flatten_sampled(int64_t* flat_sampled, const int64_t* sampled, int64_t sampled_stride,
                             const int32_t* num_sampled, const int32_t* cu_num_logits,

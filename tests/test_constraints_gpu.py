@@ -98,10 +98,14 @@ def test_c4_masks_match_processed_path_and_oracle(device, B):
                           w.top_p.cpu().numpy()[req][rnd], "c4 in-kernel masks")
 
 
-def test_c4_in_kernel_constraints_then_verify(device):
+@pytest.mark.parametrize("B,V,seed", [(128, configs.VOCAB, 2024), (4500, 1024, 2027)],
+                         ids=["B128", "B4500_several_launches"])
+def test_c4_in_kernel_constraints_then_verify(device, B, V, seed):
     """rejection_sample on the raw bf16 rows with the divide and the constraints in the
-    kernels, against the oracle sampler on the same rows masked by the processed path."""
-    w = configs.ragged_c4(device, B=128, seed=2024)
+    kernels, against the oracle sampler on the same rows masked by the processed path.  Beyond
+    4096 requests the constraints kernel masks the whole batch once and several verify launches
+    share its masks, plan order and slot arrays."""
+    w = configs.ragged_c4(device, B=B, V=V, seed=seed)
     sm = _metadata(w)
     out = rejection_sample(w.draft_token_ids, w.num_draft_tokens, w.max_spec_len,
                            w.cu_num_draft_tokens, w.draft_probs, w.target_logits,
@@ -289,3 +293,44 @@ def test_masked_call_leaves_workspace_zero(device):
     print(f"[after masked call] mismatched={rep.mismatched} "
           f"accept_flips={rep.accept_flips} recovered_flips={rep.recovered_flips}", flush=True)
     assert not rep.unexplained, rep.unexplained[:5]
+
+
+@pytest.mark.parametrize("B,k,V", [(16, 3, 32768), (64, 4, 151936)])
+def test_masked_chunks_with_zero_maximum(device, B, k, V):
+    """Random rows whose only positive entries lie in the first 64 columns; every other entry is
+    negative or exactly +0.0, and top-k = 50 masks all of them.  Every chunk of a row past the
+    first then has the raw maximum +0.0 and nothing kept, so it publishes the statistics pair
+    (+0.0, sum 0).  The call must finish without poisoned rows and give the oracle's tokens on
+    the rows masked by the processed path."""
+    g = torch.Generator().manual_seed(4400 + B)
+    P = B * k
+    x = -torch.randn(P, V, generator=g).abs() * 2.0
+    x[:, ::3] = 0.0
+    x[:, :64] = 1.0 + 2.0 * torch.rand(P, 64, generator=g)
+    temps = torch.full((B,), 0.8)
+    q = torch.softmax((x / 0.8 + 0.5 * torch.randn(P, V, generator=g)).double(), -1).float()
+    head = q[:, :64] / q[:, :64].sum(-1, keepdim=True)
+    ids = torch.multinomial(head, 1, generator=g).flatten().to(torch.int32)
+    u = torch.rand(P, generator=g, dtype=torch.float64)
+    noise = torch.empty(B, V).exponential_(1.0, generator=g)
+    bonus = torch.randint(0, V, (B,), generator=g, dtype=torch.int32)
+    ks = [k] * B
+    cu = torch.tensor(np.cumsum(ks), dtype=torch.int32)
+    dev = dict(device=device)
+    sm = SamplingMetadata(temperature=temps.to(**dev), all_greedy=False, all_random=True,
+                          top_k=torch.full((B,), 50, dtype=torch.int64, **dev), top_p=None)
+    out = rejection_sample(ids.to(**dev), ks, k, cu.to(**dev), q.to(**dev), x.to(**dev),
+                           bonus.to(**dev), sm, uniform_probs=u.to(**dev),
+                           exp_noise=noise.to(**dev), apply_temperature=True,
+                           apply_top_k_top_p=True)
+    got = out.cpu().numpy()
+    assert not (got == nat.POISON).any(), np.flatnonzero((got == nat.POISON).any(axis=1))
+    processed = apply_sampling_constraints(x.to(**dev), cu.to(**dev), sm)
+    ref = orc.rejection_sample(ids, ks, k, q, processed.cpu(), bonus, temperature=temps,
+                               all_greedy=False, uniforms=u, exp_noise=noise,
+                               apply_temperature=False)
+    rep = orc.compare(got, ref, ids, ks)
+    print(f"[zero-max masked chunks B={B} V={V}] mismatched={rep.mismatched} "
+          f"accept_flips={rep.accept_flips} recovered_flips={rep.recovered_flips}", flush=True)
+    assert not rep.unexplained, rep.unexplained[:5]
+    assert (got[:, 0] >= 0).all()

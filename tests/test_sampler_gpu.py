@@ -261,3 +261,26 @@ def test_rejection_sampler_with_device_sampler(device, monkeypatch):
     assert accepted, "no request accepted all its drafts"
     for i in accepted:
         assert int(got[i, k]) == int(want[i]), f"request {i}"
+
+
+def test_caller_rows_after_forward(device):
+    """Which rows the caller holds after Sampler.forward on fp32 logits.  Where something reads
+    the divided rows (top-k here), they are divided in place, as in the reference
+    (sampler.py:260 ``logits.div_``).  Where nothing does (no min_p, top-k or top-p, raw
+    logprobs), the race kernel divides each value as it reads it and the caller's rows stay as
+    they were: this build's documented difference, which saves a [B, V] read and write."""
+    rng = np.random.default_rng(61)
+    temps = [0.7, 1.3, 0.0, 2.0]
+    x = torch.from_numpy(rng.normal(0, 2, (4, 3000)).astype(np.float32)).to(device)
+
+    rows = x.clone()
+    Sampler().forward(rows, sampling_metadata(temps, [[]] * 4, device=device))
+    assert torch.equal(rows, x)
+
+    rows = x.clone()
+    Sampler().forward(rows, sampling_metadata(temps, [[]] * 4, device=device, top_k=[50] * 4))
+    divisor = torch.tensor([t if t >= 1e-5 else 1.0 for t in temps], device=device)
+    divided = x / divisor.unsqueeze(1)
+    kept = torch.isfinite(rows)
+    assert torch.equal(rows[kept], divided[kept])
+    assert kept.sum(1).tolist() == [50] * 4

@@ -274,3 +274,23 @@ def test_flatten_sampled_against_the_oracle():
     got = flatten_sampled(torch.from_numpy(sampled).cuda(), torch.from_numpy(ns).int().cuda(),
                           torch.from_numpy(cu).int().cuda(), int(cu[-1]))
     assert got.cpu().numpy().tolist() == o.flatten_sampled(sampled, ns, cu, cu[-1]).tolist()
+
+
+def test_flatten_sampled_writes_rows_past_the_last_request():
+    """Rows after cu[-1] (padded or compacted logits) hold 0, as after the reference's zero
+    fill, even when the output's memory held other values before."""
+    from mvsd.worker.gpu.spec_decode import flatten_sampled
+    g = np.random.default_rng(59)
+    R, K, pad = 12, 4, 9
+    rows = g.integers(1, K + 2, R)
+    cu = np.concatenate(([0], np.cumsum(rows)))
+    n = int(cu[-1]) + pad
+    sampled = g.integers(1, 1000, (R, K + 1))
+    ns = np.array([g.integers(0, r + 1) for r in rows])
+    dirty = torch.full((n,), -5, dtype=torch.int64, device="cuda")
+    del dirty  # the caching allocator hands this block to the next allocation of its size
+    got = flatten_sampled(torch.from_numpy(sampled).cuda(), torch.from_numpy(ns).int().cuda(),
+                          torch.from_numpy(cu).int().cuda(), n)
+    want = o.flatten_sampled(sampled, ns, cu, n)
+    assert got.cpu().numpy().tolist() == want.tolist()
+    assert (want[int(cu[-1]):] == 0).all()

@@ -389,11 +389,16 @@ __device__ inline uint64_t slot_load(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// (chunk max, chunk sumexp): s >= 1 whenever m is finite and m = -inf has a non-zero bit
-// pattern, so a written stats slot is never 0.  NaN maxima are stored canonically.
+// (chunk max, chunk sumexp).  Unmasked, s >= 1 whenever m is finite and m = -inf has a
+// non-zero bit pattern.  Masked, the max covers every entry but the sum only the kept ones, so
+// a chunk whose entries are all masked and whose max is +0.0 has the pair (+0, +0): its sum is
+// then stored as -0.0, which adds nothing where the sums are combined, so that a written stats
+// slot is never 0.  NaN maxima are stored canonically.
 __device__ inline uint64_t pack_stats(float m, float s) {
   const uint32_t mb = (m != m) ? 0x7fc00000u : __float_as_uint(m);
-  return (uint64_t)mb | ((uint64_t)__float_as_uint(s) << 32);
+  uint32_t sb = __float_as_uint(s);
+  if ((mb | sb) == 0) sb = 0x80000000u;
+  return (uint64_t)mb | ((uint64_t)sb << 32);
 }
 __device__ inline float2 unpack_stats(uint64_t v) {
   return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));

@@ -762,23 +762,30 @@ __global__ __launch_bounds__(kThreads) void v2_insert_kernel(V2Params p) {
 
 // ------------------------------------------------------------------ after the call ----
 
-// flatten_sampled (minivllm/worker/gpu/spec_decode/rejection_sampler.py:73-108): one
-// wavefront per request writes its logits rows [start, end) of flat: the first num_sampled
-// from sampled[r], 0 after them (the reference zero-fills flat first).
+// flatten_sampled (minivllm/worker/gpu/spec_decode/rejection_sampler.py:73-108): one thread
+// per logits row i writes flat[i]: sampled[r, i - cu[r]] when request r's rows [cu[r], cu[r+1])
+// hold i and i - cu[r] < num_sampled[r], else 0 (the reference zero-fills flat first, so rows
+// outside every request's range, such as padding after cu[num_reqs], hold 0 too).
 __global__ __launch_bounds__(kThreads) void v2_flatten_kernel(int64_t* flat, const int64_t* sampled,
                                                                int64_t stride, const int32_t* num_sampled,
                                                                const int32_t* cu, int32_t num_reqs,
                                                                int64_t num_logits) {
-  const int r = blockIdx.x * kWaves + wave_id();
-  if (r >= num_reqs) return;
-  int64_t start = cu[r], end = cu[r + 1];
-  start = start < 0 ? 0 : start;
-  end = end > num_logits ? num_logits : end;
-  const int64_t ns = num_sampled[r];
-  for (int64_t i = start + lane_id(); i < end; i += kWave) {
-    const int64_t j = i - start;
-    flat[i] = j < ns && j < stride ? sampled[(int64_t)r * stride + j] : 0;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= num_logits) return;
+  // last request r with cu[r] <= i (cu is non-decreasing); -1 if none
+  int lo = 0, hi = num_reqs;  // answer in [lo - 1, hi)
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if ((int64_t)cu[mid] <= i) lo = mid + 1;
+    else hi = mid;
   }
+  const int r = lo - 1;
+  int64_t v = 0;
+  if (r >= 0 && i < (int64_t)cu[r + 1]) {
+    const int64_t j = i - cu[r];
+    if (j < num_sampled[r] && j < stride) v = sampled[(int64_t)r * stride + j];
+  }
+  flat[i] = v;
 }
 
 // get_num_sampled_and_rejected (minivllm/worker/gpu/input_batch.py:507-553): a request
@@ -957,10 +964,12 @@ int mvsd_v2_flatten_sampled(int64_t* flat_sampled, const int64_t* sampled, int64
                             int64_t num_reqs, int64_t num_logits, mvsd_stream_t stream) {
   using namespace mvsd;
   if (num_reqs < 0 || num_logits < 0 || sampled_stride < 0) return MVSD_E_INVALID;
-  if (num_reqs == 0 || num_logits == 0) return MVSD_OK;
-  if (!flat_sampled || !sampled || !num_sampled || !cu_num_logits) return MVSD_E_INVALID;
+  if (num_logits == 0) return MVSD_OK;
+  if (!flat_sampled || (num_reqs > 0 && (!sampled || !num_sampled || !cu_num_logits)))
+    return MVSD_E_INVALID;
   if (num_reqs > 0x7fffffff) return MVSD_E_RANGE;
-  const unsigned wg = (unsigned)((num_reqs + kWaves - 1) / kWaves);
+  if (num_logits > 0x7fffffffLL * kThreads) return MVSD_E_RANGE;
+  const unsigned wg = (unsigned)((num_logits + kThreads - 1) / kThreads);
   hipLaunchKernelGGL(v2_flatten_kernel, dim3(wg), dim3(kThreads), 0, (hipStream_t)stream,
                      flat_sampled, sampled, sampled_stride, num_sampled, cu_num_logits,
                      (int32_t)num_reqs, num_logits);

@@ -1,7 +1,7 @@
 """Build recipe for libmvsd.so (the HIP kernels + C ABI declared in include/mvsd.h).
 
-Compiles every ``csrc/*.hip`` for gfx950 with hipcc into one shared library next to this
-file.  Flags:
+Compiles every ``csrc/*.hip`` for gfx950 with hipcc (one object per source, in parallel) and
+links them into one shared library next to this file.  Flags:
   * ``-fhip-fp32-correctly-rounded-divide-sqrt``: IEEE fp32 division, so the temperature
     divide and ``p / q`` round like the reference's fp32 arithmetic;
   * ``-Xclang -target-feature -Xclang -packed-fp32-ops``: no packed-FP32 VALU instructions;
@@ -54,23 +54,45 @@ def sources() -> list[Path]:
     return sorted(CSRC_DIR.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile libmvsd.so in place (always rebuilds) and return its path."""
-    srcs = sources()
-    if not srcs:
-        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-o", str(tmp), *map(str, srcs)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def _run(cmd: list[str]) -> str:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature; that is expected.
     noise = "packed-fp32-ops"
     stderr = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{stderr}")
-    if verbose and stderr.strip():
-        print(stderr, file=sys.stderr)
+        raise RuntimeError(f"hipcc failed ({proc.returncode}): {' '.join(cmd)}\n{stderr}")
+    return stderr
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile libmvsd.so in place (always rebuilds) and return its path.  Each source is
+    compiled to an object of its own, in parallel, and the objects are linked into the
+    library (every translation unit carries its own device code; none calls device code of
+    another)."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1)), 16))
+    with tempfile.TemporaryDirectory(prefix="mvsd_build_") as tmpdir:
+        objs = [Path(tmpdir) / (src.stem + ".o") for src in srcs]
+        cmds = [[hipcc(), *compile_flags, f"-I{INCLUDE_DIR}", "-c", "-o", str(obj), str(src)]
+                for src, obj in zip(srcs, objs)]
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            logs = list(pool.map(_run, cmds))
+        tmp = LIB_PATH.with_suffix(".so.tmp")
+        link = [hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+                *map(str, objs)]
+        logs.append(_run(link))
+    if verbose:
+        for cmd in cmds + [link]:
+            print(" ".join(cmd), flush=True)
+        for log in logs:
+            if log.strip():
+                print(log, file=sys.stderr)
     tmp.replace(LIB_PATH)
     return LIB_PATH
 

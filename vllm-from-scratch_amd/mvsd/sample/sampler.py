@@ -33,6 +33,7 @@ from .metadata import SAMPLING_EPS, SamplingMetadata
 from .ops.topk_topp_sampler import apply_top_k_top_p
 
 _ARGMAX, _MIN_P, _LOG_SOFTMAX = 0, 1, 3
+_PROCESSED_MODES = ("processed_logits", "processed_logprobs")
 
 
 def generate_sampler_noise(shape, generators: dict[int, torch.Generator],
@@ -213,40 +214,35 @@ class Sampler:
     def sample(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata,
                logprobs_mode: str | None = None):
         """(tokens, processed logits / logprobs of the processed_* modes) (sampler.py:243-278)."""
-        mode = logprobs_mode or self.logprobs_mode
-        if sampling_metadata.all_random:
-            greedy_sampled = None
-        else:
-            greedy_sampled = self.greedy_sample(logits)
-            if sampling_metadata.all_greedy:
-                processed = None
-                if sampling_metadata.max_num_logprobs is not None:
-                    if mode == "processed_logits":
-                        processed = logits
-                    elif mode == "processed_logprobs":
-                        processed = self.compute_logprobs(logits)
-                return greedy_sampled, processed
-        temperature = sampling_metadata.temperature
-        if temperature is None:
+        md = sampling_metadata
+        # The argmax is taken on the rows as they arrive (penalties applied, no temperature),
+        # before anything below divides them in place.
+        argmax_ids = None if md.all_random else self.greedy_sample(logits)
+        if md.all_greedy:
+            # nothing scales or masks an all-greedy batch: the "processed" rows are the rows
+            wanted = None
+            if md.max_num_logprobs is not None:
+                wanted = {"processed_logits": lambda: logits,
+                          "processed_logprobs": lambda: self.compute_logprobs(logits)
+                          }.get(logprobs_mode or self.logprobs_mode)
+            return argmax_ids, (wanted() if wanted else None)
+        if md.temperature is None:
             raise ValueError("random rows in the batch but no temperature tensor")
-        safe = torch.where(temperature < SAMPLING_EPS, torch.ones_like(temperature), temperature)
-        if (sampling_metadata.min_p is None and sampling_metadata.top_k is None
-                and sampling_metadata.top_p is None
-                and self.topk_topp_sampler.logprobs_mode not in ("processed_logits",
-                                                                 "processed_logprobs")):
-            # nothing reads the divided rows: the race divides as it reads
-            random_sampled = random_sample(logits, sampling_metadata.generators,
-                                           temperature=safe)
-            processed = None
+        # rows under SAMPLING_EPS are greedy: their divisor is 1 and their draw is discarded
+        greedy_rows = md.temperature < SAMPLING_EPS
+        divisor = md.temperature.masked_fill(greedy_rows, 1.0)
+        reads_divided_rows = (md.min_p is not None or md.top_k is not None
+                              or md.top_p is not None
+                              or self.topk_topp_sampler.logprobs_mode in _PROCESSED_MODES)
+        if reads_divided_rows:
+            scaled = self.apply_min_p(logits.div_(divisor.unsqueeze(1)), md.min_p)
+            drawn, processed = self.topk_topp_sampler(scaled, md.generators, md.top_k, md.top_p)
         else:
-            logits = logits.div_(safe.unsqueeze(dim=1))
-            logits = self.apply_min_p(logits, sampling_metadata.min_p)
-            random_sampled, processed = self.topk_topp_sampler(
-                logits, sampling_metadata.generators, sampling_metadata.top_k,
-                sampling_metadata.top_p)
-        if greedy_sampled is None:
-            return random_sampled, processed
-        return torch.where(temperature < SAMPLING_EPS, greedy_sampled, random_sampled), processed
+            # the race kernel divides each value as it reads it; the rows stay undivided
+            drawn, processed = random_sample(logits, md.generators, temperature=divisor), None
+        if argmax_ids is not None:
+            drawn = torch.where(greedy_rows, argmax_ids, drawn)
+        return drawn, processed
 
     @staticmethod
     def apply_min_p(logits: torch.Tensor, min_p: torch.Tensor | None) -> torch.Tensor:

@@ -140,16 +140,24 @@ class NgramProposer:
             token_ids = input_batch.token_ids_cpu.numpy()
             num_tokens_no_spec = input_batch.num_tokens_no_spec.numpy()
         else:
-            token_ids = np.zeros((len(rows), self.max_model_len), dtype=np.int32)
-            num_tokens_no_spec = np.zeros(len(rows), dtype=np.int32)
-            for index, target in enumerate(rows):
-                tokens = all_token_ids[target.req_id][:target.history_end]
-                length = min(len(tokens), self.max_model_len)
-                token_ids[index, :length] = tokens[:length]
-                num_tokens_no_spec[index] = length
+            token_ids, num_tokens_no_spec = self._history_table(rows, all_token_ids)
         sampled = [[0] if target.ready else [] for target in rows]
         drafts = self.propose(num_speculative_tokens, sampled, num_tokens_no_spec, token_ids)
         return DraftTokenIds(req_ids=[t.req_id for t in rows], draft_token_ids=drafts)
+
+    def _history_table(self, rows: list[TargetRows], all_token_ids: dict[str, list[int]]):
+        """The batch buffers built from token lists: an int32 table [len(rows), max_model_len]
+        whose row i starts with request rows[i]'s committed tokens (at most history_end of
+        them, cut at max_model_len) and is zero after them, and those lengths."""
+        width = self.max_model_len
+        kept = [all_token_ids[t.req_id][:t.history_end][:width] for t in rows]
+        lengths = np.array([len(h) for h in kept], dtype=np.int32)
+        table = np.zeros((len(rows), width), dtype=np.int32)
+        if lengths.sum():
+            # a boolean mask fills row-major order, which is the order of the concatenation
+            table[np.arange(width)[None, :] < lengths[:, None]] = np.concatenate(
+                [np.asarray(h, dtype=np.int32) for h in kept if len(h)])
+        return table, lengths
 
     def remove_requests(self, req_ids) -> None:
         pass
