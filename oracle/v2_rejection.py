@@ -272,11 +272,26 @@ def residual_logits(row, rej, t_lse=0.0, d_row=None, d_lse=0.0, log_p_tau=0.0):
         return np.where(ratio < 1.0, tlp + np.log1p(-ratio), -np.inf).astype(np.float32)
 
 
+# fp32 evaluation error allowed between this restatement (numpy libm, float64 where it helps)
+# and a device build that computes the same quantities in fp32 with the hardware exp2 / log2
+# (each within 3 ulp) and reduced sums: DEVICE_ULPS fp32 ulps of every magnitude that enters a
+# decision.
+DEVICE_ULPS = 8
+EPS32 = 2.0 ** -23
+
+
+def flip_window(magnitude: float) -> float:
+    """Width below which a decision margin (or a resampling gap) whose terms sum to
+    ``magnitude`` in absolute value may be flipped by fp32 evaluation differences."""
+    return DEVICE_ULPS * EPS32 * float(magnitude)
+
+
 def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, pos, idx_mapping,
                      expanded_idx_mapping, expanded_local_pos, temperature, seed,
                      num_speculative_steps: int, synthetic_conditional_rates=None,
                      use_fp64: bool = False, use_block_verification: bool = False,
-                     return_margins: bool = False, return_details: bool = False):
+                     return_margins: bool = False, return_details: bool = False,
+                     return_windows: bool = False):
     """V2 ``rejection_sample`` on numpy arrays, standard or block verification.
 
     Returns ``(sampled [R, K+1] int64, num_sampled [R] int32)`` where entries at or past
@@ -284,6 +299,9 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
     also returns, per request, the list of decision margins of the random steps that were
     decided (|log p - log u - log q| for the standard test, |u - h| for the block test), and
     the gap between the best and second-best resampled scores (a near-tie measure).  With
+    ``return_windows`` (and ``return_margins``) also returns, in the same shapes, the width
+    below which a margin or gap may be flipped by fp32 evaluation differences between this
+    restatement and a device build (``flip_window``).  With
     ``return_details`` (block verification) the last element returned is a dict with the
     per-request thresholds ``h``, the ``cumulative_log_p`` and ``residual_mass`` arrays and
     the ``stats``."""
@@ -316,8 +334,14 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
     sampled = np.full((R, K + 1), -1, np.int64)
     num_sampled = np.zeros(R, np.int32)
     margins = [[] for _ in range(R)]
+    windows = [[] for _ in range(R)]
     thresholds = [[] for _ in range(R)]
     gaps = np.full(R, np.inf)
+    gap_windows = np.zeros(R)
+
+    def lse_mag(row):
+        m = abs(float(stats.target_lse(row)))
+        return m + (abs(float(stats.draft_lse(row))) if dl is not None else 0.0)
     for r in range(R):
         st = int(idx_mapping[r])
         start, end = int(cu[r]), int(cu[r + 1])
@@ -361,6 +385,11 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
                     h = prefix
                 thresholds[r].append(float(h))
                 margins[r].append(abs(float(u) - float(h)))
+                if return_windows:
+                    # h is a function of exp(cum) and the next row's residual: its relative
+                    # error follows the log-space error of every row up to the next one
+                    mag = abs(float(cum[li])) + sum(lse_mag(j) for j in range(start, min(li + 2, end - 1)))
+                    windows[r].append(flip_window(mag + 1.0))
                 if u <= h:
                     acc = i + 1
                 sampled[r, i] = d
@@ -378,6 +407,10 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
                 else:
                     ok = bool(tlp > rhs)
                     margins[r].append(abs(float(tlp) - float(rhs)))
+                    if return_windows:
+                        windows[r].append(flip_window(
+                            abs(float(tlp)) + abs(float(t_lse)) + abs(float(np.log(u)))
+                            + abs(float(dlp)) + abs(float(d_lse)) + 1.0))
                 verifying = ok
                 acc += ok
                 sampled[r, i] = d
@@ -408,14 +441,22 @@ def rejection_sample(target_logits, draft_logits, draft_sampled, cu_num_logits, 
                     sc = x - np.log(-np.log(tl_rand64(gseed, keys)))
                 else:
                     sc = x - np.log(-np.log1p(-tl_rand32(gseed, keys).astype(np.float64)))
-            top2 = np.sort(sc[np.isfinite(sc)])[-2:]
-            if top2.size == 2:
-                gaps[r] = float(top2[1] - top2[0])
+            finite = np.flatnonzero(np.isfinite(sc))
+            best = finite[np.argsort(sc[finite], kind="stable")[-2:]]
+            if best.size == 2:
+                gaps[r] = float(sc[best[1]] - sc[best[0]])
+                if return_windows:
+                    noise = np.abs(x[best] - sc[best]).sum()
+                    gap_windows[r] = flip_window(
+                        np.abs(sc[best]).sum() + noise + 2.0 * (abs(float(t_lse)) + abs(float(d_lse))
+                                                                + abs(float(log_p_tau))) + 1.0)
         sampled[r, acc] = tok
         num_sampled[r] = acc + 1
     out = (sampled, num_sampled)
     if return_margins:
         out = out + (margins, gaps)
+        if return_windows:
+            out = out + (windows, gap_windows)
     if return_details:
         out = out + (dict(h=thresholds, cumulative_log_p=cum, residual_mass=mass, stats=stats),)
     return out

@@ -33,7 +33,8 @@ def test_more_than_one_gpu_is_refused():
 @pytest.mark.gpu
 def test_json_line_fields():
     """A short headline-config run prints one line with the contract's fields."""
-    r = _run("--steps", "3", "--warmup", "1", "--cpu-seconds", "0.5")
+    r = _run("--steps", "3", "--warmup", "1", "--cpu-seconds", "0.5", "--configs", "c1,c3,v2",
+             "--sub-steps", "3", "--sub-cpu-seconds", "0.2")
     assert r.returncode == 0, r.stderr[-3000:]
     line = _json_line(r.stdout)
     for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
@@ -50,3 +51,14 @@ def test_json_line_fields():
     assert isinstance(cpu["sample"], str) and cpu["sample"]
     assert "workload" in line["config"]
     assert line["parity"]["unexplained"] == 0
+    # the roofline is taken on the timed region's clock
+    assert roof["kernel_ms"] <= line["ms_per_step"]
+    subs = line["configs"]
+    assert set(subs) == {"c1", "c3", "v2"}
+    for name, entry in subs.items():
+        assert entry["ms_per_step"] > 0 and entry["cpu_baseline"]["value"] > 0, name
+        assert [f["cores"] for f in entry["cpu_baseline"]["by_cores"]][-1] == 1, name
+        assert entry["parity"]["mismatched"] == 0 or name == "v2", name
+    assert subs["c1"]["frac_on_kernel_bytes"] > 0
+    assert subs["c1"]["reference_algorithm_bytes"] > 0 and subs["c1"]["kernel_bytes"] > 0
+    assert subs["v2"]["parity"]["unexplained"] == 0

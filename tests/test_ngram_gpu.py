@@ -233,15 +233,23 @@ def test_propose_drafts_protocol(device):
     assert prop.propose_drafts(rows, all_ids, num_speculative_tokens=0).draft_token_ids == [[], []]
 
 
-def test_c3_full_size_bit_exact(device):
-    tokens = configs.ngram_c3(device)
+@pytest.mark.parametrize("suffix_copies", [False, True], ids=["c3", "c3_suffix_copies"])
+def test_c3_full_size_bit_exact(device, suffix_copies):
+    """C3 as generated: its copied spans never cover a history's last token, so no suffix
+    repeats and every request scans its whole history without a match.  With suffix_copies,
+    every other history ends with a copy of an earlier span of 8-64 tokens, so those requests
+    find a match of max_n and stop early."""
+    tokens = configs.ngram_c3(device, suffix_copies=suffix_copies)
     B, L = tokens.shape
     lens = torch.full((B,), L, dtype=torch.int32, device=device)
     drafts, valid = ngram_propose_device(tokens, lens, min_n=2, max_n=5, k=5)
     exp_d, exp_v = ong.brute_device_batch(tokens.cpu().numpy(), lens.cpu().numpy(), 2, 5, 5)
     assert np.array_equal(drafts.cpu().numpy(), exp_d)
     assert np.array_equal(valid.cpu().numpy(), exp_v)
-    print(f"[c3] rows with drafts: {(exp_v > 0).sum()}/{B}", flush=True)
+    print(f"[c3 suffix_copies={suffix_copies}] rows with drafts: {(exp_v > 0).sum()}/{B}",
+          flush=True)
+    if suffix_copies:
+        assert (exp_v[0::2] == 5).all()
     # host API with the max_model_len cap = the reference's CPU KMP, bit-exact
     d2, c2 = ngram_propose_device(tokens, lens, min_n=2, max_n=5, k=5, cap_by_model_len=True,
                                   max_model_len=8192)

@@ -172,3 +172,17 @@ def test_flatten_sampled_by_hand():
     sampled = np.array([[5, 6, 7], [8, -1, -1], [9, 10, -1]])
     flat = o.flatten_sampled(sampled, [3, 1, 2], [0, 3, 5, 8], 8)
     assert flat.tolist() == [5, 6, 7, 8, 0, 9, 10, 0]
+
+
+def test_flip_windows_cover_fp32_evaluation_only():
+    """The flip windows the GPU parity tests allow are a few fp32 ulps of each decision's
+    magnitudes: one per decided random step, every one far below the 1e-4 a libm-agnostic
+    comparison would need, and zero for greedy requests' gaps."""
+    case = make_case([4, 4, 0, 3], [0.8, 0.0, 1.0, 1.2], 4, 4096, seed=31)
+    es, en, margins, gaps, wins, gap_wins = o.rejection_sample(
+        **oracle_args(case), return_margins=True, return_windows=True)
+    for r in range(len(en)):
+        assert len(wins[r]) == len(margins[r])
+        assert all(o.DEVICE_ULPS * o.EPS32 <= w < 1e-4 for w in wins[r])
+    assert gap_wins[1] == 0.0 and 0.0 < gap_wins[0] < 1e-4
+    assert o.flip_window(1.0) == 8 * 2.0 ** -23

@@ -27,11 +27,11 @@ from oracle import topk_topp as otp
 
 pytestmark = pytest.mark.gpu
 
-REL = 1e-5          # north_star: probabilities within 1e-5 relative (fp32) ...
-P_MEANINGFUL = 1e-12  # ... for probabilities >= 1e-12.  Below, the fp32 exponent of a deep-tail
-REL_TAIL = 4e-5     # entry (|x - M| / T up to ~100) rounds to a few 1e-6 absolute, so two exact
-P_FLOOR = 1e-30     # fp32 evaluations differ by up to ~1.4e-5 relative there (T = 0.3); and
-ABS_FLOOR = 1e-35   # below 1e-30 the check is absolute.
+REL = 1e-5          # north_star: probabilities within 1e-5 relative (fp32), for p >= 1e-12
+P_MEANINGFUL = 1e-12  # and for the deep tail 1e-30 <= p < 1e-12 alike (there the fp32 exponent
+REL_TAIL = 1e-5     # (x - M) / T, up to ~70 in magnitude, carries the largest rounding: the
+P_FLOOR = 1e-30     # runs measure at most ~4e-6 relative); below 1e-30 the check is
+ABS_FLOOR = 1e-35   # absolute.
 
 
 def _report(label, rep, extra=""):
@@ -201,3 +201,56 @@ def test_verify_kernel_row_statistics(device, case):
     valid = (dr >= 0) & (dr < x.shape[1])
     want = p64[np.nonzero(valid)[0], dr[valid]]
     _rel_check(st[valid, 2], want, f"{case} p[d] as compared")
+
+
+def test_c5_drop_in_forward_with_bonus_rows(device, monkeypatch):
+    """RejectionSampler(Sampler()).forward on C5's compact [8192, V] bf16 logits (B=1024, k=7):
+    the bonus rows sampled on the device by the exponential race, the verification with the
+    gather and temperature in the kernel.  Every seam is fed known randomness (the bonus rows'
+    noise, the uniforms, the recovered-token noise); the bonus tokens must equal the oracle
+    sampler's on the bonus rows (a race near-tie within 1e-5 relative allowed and counted),
+    and the whole output the oracle verification given those bonus tokens."""
+    from mvsd.sample import Sampler
+    from mvsd.sample import sampler as smp
+    from mvsd.testing.spec_metadata import make_metadata, sampling_metadata
+    from oracle import sampler as osm
+
+    w = configs.eagle_c5(device)
+    B, k, V = w.batch_size, w.max_spec_len, w.vocab_size
+    drafts = w.draft_token_ids.view(B, k).tolist()
+    meta = make_metadata(drafts, device=device)
+    assert torch.equal(meta.target_logits_indices.long(), w.target_rows.long())
+    g = torch.Generator(device=device).manual_seed(5005)
+    bonus_noise = torch.empty((B, V), device=device).exponential_(generator=g)
+    monkeypatch.setattr(smp, "generate_sampler_noise", lambda *a, **kw: bonus_noise)
+    monkeypatch.setattr(rs, "generate_uniform_probs", lambda *a, **kw: w.uniforms)
+    monkeypatch.setattr(rs, "generate_exponential_noise", lambda *a, **kw: w.exp_noise)
+    sm = sampling_metadata([1.0] * B, drafts, device=device)
+    out = rs.RejectionSampler(Sampler())(meta, w.draft_probs, w.target_logits, sm)
+    got = out.sampled_token_ids.cpu().numpy()
+
+    bonus_rows = w.target_logits[meta.bonus_logits_indices.long()].float().cpu()
+    want_bonus, _, scores = osm.forward(bonus_rows, sampling_metadata([1.0] * B, drafts),
+                                        bonus_noise.cpu(), "raw_logprobs",
+                                        predict_bonus_token=True)
+    want_bonus = want_bonus.numpy()
+    all_accepted = got[:, k] >= 0
+    bonus = want_bonus.copy()
+    ties = 0
+    for r in np.nonzero(all_accepted)[0]:
+        gb, wb = int(got[r, k]), int(want_bonus[r])
+        if gb != wb:
+            assert float(scores[r, gb]) >= float(scores[r, wb]) * (1 - 1e-5), (r, gb, wb)
+            ties += 1
+            bonus[r] = gb
+    logits = w.target_logits[w.target_rows.long()].cpu()
+    ref = orc.rejection_sample(w.draft_token_ids.cpu(), w.num_draft_tokens, k,
+                               w.draft_probs.cpu(), logits, torch.from_numpy(bonus).view(B, 1),
+                               temperature=w.temperature.cpu(), all_greedy=False,
+                               uniforms=w.uniforms.cpu(), exp_noise=w.exp_noise.cpu(),
+                               apply_temperature=True)
+    rep = orc.compare(got, ref, w.draft_token_ids.cpu(), w.num_draft_tokens)
+    _report("c5 drop-in forward B=1024 k=7", rep,
+            f" all_accepted={int(all_accepted.sum())} bonus_near_ties={ties}")
+    assert all_accepted.any()
+    assert not rep.unexplained, rep.unexplained[:5]

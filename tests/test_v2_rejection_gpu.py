@@ -3,9 +3,12 @@
 (mvsd.worker.gpu.spec_decode.rejection_sample -> mvsd_v2_rejection_sample).
 
 Bar: ``num_sampled`` and every defined entry ``sampled[r, :num_sampled[r]]`` equal the oracle's.
-A difference is tolerated only where the oracle's decision is a near-tie that fp32 libm
-rounding (device vs numpy) can flip: an acceptance margin |log p - log u - log q| < 1e-4, or a
-resampling gap between the two best Gumbel scores < 1e-4.  Such cases are counted and printed.
+A difference is tolerated only where the oracle's decision is a near-tie that fp32 evaluation
+differences (device exp2 / log2 within 3 ulp, other summation orders; numpy on the host) can
+flip: an acceptance margin |log p - log u - log q| (standard) or |u - h| (block), or the gap
+between the two best Gumbel scores, below 8 fp32 ulps of the magnitudes of the terms that enter
+it (oracle.v2_rejection.flip_window).  Such cases are counted and printed; every run so far has
+had none.
 """
 
 import numpy as np
@@ -13,7 +16,7 @@ import pytest
 import torch
 
 from oracle import v2_rejection as o
-from v2_cases import make_case, oracle_args, repeat_case
+from v2_cases import make_case, near_tie, oracle_args, repeat_case
 
 pytestmark = pytest.mark.gpu
 
@@ -36,17 +39,20 @@ def _compare(case, name, **kw):
     okw = dict(kw)
     if okw.get("synthetic_conditional_rates") is not None:
         okw["synthetic_conditional_rates"] = okw["synthetic_conditional_rates"].numpy()
-    es, en, margins, gaps = o.rejection_sample(**oracle_args(case), **okw, return_margins=True)
+    es, en, margins, gaps, wins, gap_wins = o.rejection_sample(
+        **oracle_args(case), **okw, return_margins=True, return_windows=True)
     flips = 0
     for r in range(len(en)):
         same = n[r] == en[r] and (s[r, :en[r]] == es[r, :en[r]]).all()
         if same:
             continue
-        near = (margins[r] and min(margins[r]) < 1e-4) or gaps[r] < 1e-4
+        near = near_tie(margins[r], wins[r], gaps[r], gap_wins[r])
         assert near, f"{name}: request {r}: got {n[r]} {s[r, :n[r]]}, want {en[r]} {es[r, :en[r]]}"
         flips += 1
-    print(f"[v2 parity] {name}: {len(en)} requests, {flips} near-tie differences", flush=True)
-    assert flips <= max(1, len(en) // 20)
+    in_window = sum(any(m < w for m, w in zip(margins[r], wins[r])) or gaps[r] < gap_wins[r]
+                    for r in range(len(en)))
+    print(f"[v2 parity] {name}: {len(en)} requests, {flips} near-tie differences "
+          f"({in_window} requests with a decision inside its flip window)", flush=True)
     return s, n, es, en
 
 

@@ -18,7 +18,7 @@ import torch
 
 from oracle import logprobs as olp
 from oracle import v2_rejection as o
-from v2_cases import make_case, oracle_args
+from v2_cases import make_case, near_tie, oracle_args
 
 pytestmark = pytest.mark.gpu
 
@@ -104,14 +104,14 @@ def test_call_matches_the_verification_and_the_oracle(method):
     okw = {}
     if rates is not None:
         okw["synthetic_conditional_rates"] = rs.synthetic_conditional_rates.cpu().numpy()
-    es, en, margins, gaps = o.rejection_sample(
+    es, en, margins, gaps, wins, gap_wins = o.rejection_sample(
         **oracle_args(case), use_block_verification=method == "block", return_margins=True,
-        **okw)
+        return_windows=True, **okw)
     s, n = out.sampled_token_ids.cpu().numpy(), out.num_sampled.cpu().numpy()
     for r in range(len(en)):
         if n[r] == en[r] and (s[r, :en[r]] == es[r, :en[r]]).all():
             continue
-        assert (margins[r] and min(margins[r]) < 1e-4) or gaps[r] < 1e-4, r
+        assert near_tie(margins[r], wins[r], gaps[r], gap_wins[r]), r
 
 
 def test_requests_still_prefilling_sample_nothing():

@@ -91,3 +91,11 @@ def repeat_case(target, draft, tokens, temp, n, *, seed=0):
         temperature=torch.full((n,), float(temp)),
         seed=torch.randint(0, 2**62, (n,), generator=g, dtype=torch.int64),
         num_speculative_steps=K)
+
+
+def near_tie(margins, windows, gap, gap_window) -> bool:
+    """A request's output may differ from the oracle's only when one of its decisions was
+    within its fp32 flip window (oracle.v2_rejection.flip_window: 8 fp32 ulps of the terms'
+    magnitudes, from the hardware exp2 / log2 error of at most 3 ulp and the sums' roundings),
+    or when the best two resampling scores were."""
+    return any(m < w for m, w in zip(margins, windows)) or gap < gap_window

@@ -176,9 +176,12 @@ def eagle_c5(device, B=1024, k=7, V=VOCAB, seed=1005) -> Workload:
                     _exp_noise(B, V, g, device))
 
 
-def ngram_c3(device, B=256, L=4096, V=VOCAB, seed=1003, copy_frac=0.3):
+def ngram_c3(device, B=256, L=4096, V=VOCAB, seed=1003, copy_frac=0.3, suffix_copies=False):
     """Histories [B, L] int32 uniform in [0, V) with ~copy_frac of each overwritten by copies
-    of earlier spans of length 8..64 at random offsets (generated on the host)."""
+    of earlier spans of length 8..64 at random offsets (generated on the host).  A copy never
+    covers a history's last token, so no suffix repeats and no request finds a match.  With
+    ``suffix_copies`` every other history (even rows) then ends with a copy of an earlier span
+    of 8..64 tokens, so those requests match at max_n (prompt lookup's useful case)."""
     rng = np.random.default_rng(seed)
     tokens = rng.integers(0, V, size=(B, L), dtype=np.int64).astype(np.int32)
     for b in range(B):
@@ -189,6 +192,12 @@ def ngram_c3(device, B=256, L=4096, V=VOCAB, seed=1003, copy_frac=0.3):
             src = int(rng.integers(0, dst - n + 1))
             tokens[b, dst:dst + n] = tokens[b, src:src + n]
             written += n
+    if suffix_copies:
+        tail = np.random.default_rng(seed + 1)
+        for b in range(0, B, 2):
+            n = int(tail.integers(8, 65))
+            src = int(tail.integers(0, L - 2 * n))
+            tokens[b, L - n:] = tokens[b, src:src + n]
     return torch.from_numpy(tokens).to(device)
 
 
