@@ -353,9 +353,13 @@ int mvsd_sampler_rows(int op, int32_t* ids, float* out, int64_t out_stride, floa
 /* sampler_race — random_sample, minivllm/sample/ops/topk_topp_sampler.py:82-90, with the  */
 /* softmax before it (:73-80) and, when temperature is given, the temperature divide of    */
 /* Sampler.sample (minivllm/sample/sampler.py:263-268) folded in: ids[r] = argmax over i of */
-/* (exp(v_i - M) / S) / noise[r][i] with v = fl(x[r][i] / temperature[r]) (or x[r][i]      */
-/* when temperature is NULL), M the max and S the sum of exp(v - M) over row r; NaN first,  */
-/* lowest index on ties.  temperature [num_rows] fp32 holds positive divisors (the         */
+/* softmax(v)_i / noise[r][i] with v = fl(x[r][i] / temperature[r]) (or x[r][i] when       */
+/* temperature is NULL).  The row's max and sum are common to its entries, so the argmax   */
+/* is evaluated as that of v log2(e) - log2(noise[r][i]) in one pass; the keys differ from */
+/* the reference's fp32 roundings of exp(v - M) / S / noise by a few ulps of |v| log2(e) + */
+/* |log2 noise|, so only closer near-ties can pick another index.  A row the reference     */
+/* maps to all-NaN probabilities (a NaN or +inf value, or every value -inf) gives 0; NaN   */
+/* first, lowest index on ties.  temperature [num_rows] fp32 holds positive divisors (the  */
 /* reference's safe temperatures: 1 for greedy rows).  Rows of 8192 columns are spread     */
 /* over workgroups; workspace: >= mvsd_sampler_race_workspace_bytes(num_rows, V) bytes of   */
 /* device memory, no initialisation needed.  V <= 8388608.                                  */
@@ -365,6 +369,25 @@ int mvsd_sampler_race(int32_t* ids, const float* x, int64_t stride, const float*
                       int64_t noise_stride, const float* temperature, int64_t num_rows,
                       int64_t vocab_size, void* workspace, int64_t workspace_bytes,
                       mvsd_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* sampler_race_rows — the bonus-row sampling of RejectionSampler.forward                  */
+/* (minivllm/sample/rejection_sampler.py:169-181: logits[bonus_logits_indices] through      */
+/* Sampler.forward, minivllm/sample/sampler.py:73-120, :243-278) when no logits processor, */
+/* min_p, top-k or top-p applies: the race of mvsd_sampler_race on rows picked in place,   */
+/* without the gather and the fp32 upcast.  Row r is x + row_index[r] * stride (row_index  */
+/* clamped to [0, num_x_rows); NULL: x + r * stride, num_x_rows >= num_rows), x_dtype       */
+/* MVSD_F32 / MVSD_BF16 / MVSD_F16, upcast exactly.  With temperature, a row whose          */
+/* temperature is below greedy_eps (the reference's SAMPLING_EPS, 1e-5) is greedy: its id  */
+/* is the argmax of the raw row (greedy_sample, sampler.py:295-298) and its noise row is    */
+/* not read; the other rows race on fl(x / T).  noise NULL makes every row greedy.          */
+/* Same workspace as mvsd_sampler_race.                                                     */
+/* ------------------------------------------------------------------------------------ */
+int mvsd_sampler_race_rows(int32_t* ids, const void* x, int x_dtype, int64_t stride,
+                           const int32_t* row_index, int64_t num_x_rows, const float* noise,
+                           int64_t noise_stride, const float* temperature, float greedy_eps,
+                           int64_t num_rows, int64_t vocab_size, void* workspace,
+                           int64_t workspace_bytes, mvsd_stream_t stream);
 
 /* ------------------------------------------------------------------------------------ */
 /* selftest — on-device check of an arithmetic assumption of the kernels.  No counterpart   */

@@ -284,3 +284,75 @@ def test_caller_rows_after_forward(device):
     kept = torch.isfinite(rows)
     assert torch.equal(rows[kept], divided[kept])
     assert kept.sum(1).tolist() == [50] * 4
+
+
+class _GenericPathSampler(Sampler):
+    """The device sampler under another type: RejectionSampler then takes its generic path
+    (gathered bonus rows through Sampler.forward)."""
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("temps_kind", ["random", "mixed", "greedy"])
+def test_forward_race_only_path_equals_generic_path(device, dtype, temps_kind):
+    """RejectionSampler(Sampler()).forward without processors or constraints reads the bonus
+    rows in place in one race launch; from the same RNG state (global and per-request
+    generators) it must give exactly the generic path's tokens: the same draws in the same
+    order, the same keys."""
+    rng = np.random.default_rng(62)
+    B, V = 48, 5000
+    ks = [int(k) for k in rng.integers(0, 5, B)]
+    drafts = [list(map(int, rng.integers(0, V, k))) for k in ks]
+    meta = make_metadata(drafts, device=device)
+    rows = sum(ks) + B
+    logits = torch.from_numpy(rng.normal(0, 2, (rows, V)).astype(np.float32)).to(device, dtype)
+    for i, d in enumerate(drafts):  # make acceptance likely: drafts near the top of their rows
+        for j, tok in enumerate(d):
+            logits[int(meta.target_logits_indices[sum(ks[:i]) + j]), tok] += 6.0
+    temps = {"random": [float(t) for t in rng.uniform(0.3, 1.5, B)],
+             "mixed": [0.0 if i % 3 == 0 else float(rng.uniform(0.3, 1.5)) for i in range(B)],
+             "greedy": [0.0] * B}[temps_kind]
+    P = sum(ks)
+    probs = torch.softmax(torch.from_numpy(rng.normal(0, 2, (P, V)).astype(np.float32)), -1)
+    probs = probs.to(device)
+
+    def run(sampler):
+        gens = {i: torch.Generator(device=device).manual_seed(500 + i) for i in range(0, B, 5)}
+        sm = sampling_metadata(temps, drafts, device=device, generators=gens)
+        torch.manual_seed(77)
+        return rs.RejectionSampler(sampler)(meta, probs, logits, sm).sampled_token_ids
+
+    fast = run(Sampler())
+    generic = run(_GenericPathSampler())
+    assert torch.equal(fast, generic)
+    got = fast.cpu().numpy()
+    assert (got[:, 0] >= 0).all()
+    if temps_kind != "greedy":
+        assert (got[np.array(ks) > 0, 1] >= 0).any()  # some request accepted a draft
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_race_rows_in_place(device, dtype):
+    """mvsd_sampler_race_rows on rows picked by index in a larger 16/32-bit tensor, greedy rows
+    (temperature below 1e-5) among random ones, against float64 softmax(fl(x / T)) / E on the
+    upcast rows (within 1e-5 relative of the winner's score) and the exact argmax for greedy
+    rows; without noise every row is greedy."""
+    rng = np.random.default_rng(63)
+    V, n = 20001, 12
+    table = torch.from_numpy(rng.normal(0, 3, (40, V)).astype(np.float32)).to(dtype)
+    idx = torch.from_numpy(rng.choice(40, n, replace=False).astype(np.int32))
+    x = table[idx.long()].float()
+    noise = torch.from_numpy(rng.exponential(1.0, (n, V)).astype(np.float32))
+    temps = torch.from_numpy(rng.uniform(0.3, 1.7, n).astype(np.float32))
+    temps[[2, 7]] = 0.0
+    temps[5] = 1e-6
+    got = smp.race_rows(table.to(device), idx.to(device), noise.to(device),
+                        temps.to(device)).cpu().tolist()
+    for r in range(n):
+        if temps[r] < 1e-5:
+            assert got[r] == int(torch.argmax(x[r])), r
+            continue
+        scores = torch.softmax((x[r] / temps[r]).double(), -1) / noise[r].double()
+        want = int(torch.argmax(scores))
+        assert got[r] == want or float(scores[got[r]]) >= float(scores[want]) * (1 - 1e-5), r
+    greedy = smp.race_rows(table.to(device), idx.to(device), None, temps.to(device))
+    assert greedy.cpu().tolist() == [int(torch.argmax(x[r])) for r in range(n)]

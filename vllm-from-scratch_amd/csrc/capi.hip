@@ -517,16 +517,32 @@ int mvsd_sampler_race(int32_t* ids, const float* x, int64_t stride, const float*
                       int64_t noise_stride, const float* temperature, int64_t num_rows,
                       int64_t vocab_size, void* workspace, int64_t workspace_bytes,
                       mvsd_stream_t stream) {
+  // positive divisors only: no row is greedy (greedy_eps 0)
+  if (!noise) return MVSD_E_INVALID;
+  return mvsd_sampler_race_rows(ids, x, MVSD_F32, stride, nullptr, num_rows, noise,
+                                noise_stride, temperature, 0.0f, num_rows, vocab_size,
+                                workspace, workspace_bytes, stream);
+}
+
+int mvsd_sampler_race_rows(int32_t* ids, const void* x, int x_dtype, int64_t stride,
+                           const int32_t* row_index, int64_t num_x_rows, const float* noise,
+                           int64_t noise_stride, const float* temperature, float greedy_eps,
+                           int64_t num_rows, int64_t vocab_size, void* workspace,
+                           int64_t workspace_bytes, mvsd_stream_t stream) {
   if (num_rows < 0 || vocab_size <= 0) return MVSD_E_INVALID;
   if (num_rows == 0) return MVSD_OK;
+  if (x_dtype != MVSD_F32 && x_dtype != MVSD_BF16 && x_dtype != MVSD_F16) return MVSD_E_INVALID;
   if (vocab_size > (int64_t)mvsd::kRaceChunk * mvsd::kRaceMaxChunks) return MVSD_E_RANGE;
   const int64_t nch = (vocab_size + mvsd::kRaceChunk - 1) / mvsd::kRaceChunk;
   if (num_rows * nch >= (1ll << 24)) return MVSD_E_RANGE;  // grid threads < 2^32
-  if (!ids || !x || !noise || stride < vocab_size || noise_stride < vocab_size)
+  if (!ids || !x || stride < vocab_size || (noise && noise_stride < vocab_size))
     return MVSD_E_INVALID;
+  if (row_index ? num_x_rows <= 0 : num_x_rows < num_rows) return MVSD_E_INVALID;
+  if (!(greedy_eps >= 0.0f)) return MVSD_E_INVALID;
   if (!workspace || workspace_bytes < mvsd::sampler_race_workspace_bytes(num_rows, vocab_size))
     return MVSD_E_WORKSPACE;
-  return hip_status(mvsd::launch_sampler_race(ids, x, stride, noise, noise_stride, temperature,
+  return hip_status(mvsd::launch_sampler_race(ids, x, x_dtype, stride, row_index, num_x_rows,
+                                              noise, noise_stride, temperature, greedy_eps,
                                               num_rows, vocab_size, workspace,
                                               (hipStream_t)stream));
 }

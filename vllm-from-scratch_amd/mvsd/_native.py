@@ -34,7 +34,8 @@ _TORCH_CODES = {
 }
 
 c_int, c_int32, c_int64, c_double, c_void_p = (ctypes.c_int, ctypes.c_int32, ctypes.c_int64,
-                                               ctypes.c_double, ctypes.c_void_p)
+                                              ctypes.c_double, ctypes.c_void_p)
+c_float = ctypes.c_float
 
 
 class RejectionArgs(ctypes.Structure):
@@ -108,6 +109,9 @@ SIGNATURES = {
     "mvsd_sampler_race_workspace_bytes": (c_int64, [c_int64, c_int64]),
     "mvsd_sampler_race": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                                   c_int64, c_int64, c_void_p, c_int64, c_void_p]),
+    "mvsd_sampler_race_rows": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64,
+                                       c_void_p, c_int64, c_void_p, c_float, c_int64, c_int64,
+                                       c_void_p, c_int64, c_void_p]),
     "mvsd_ngram_propose": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
                                    c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int,
                                    c_int64, c_int32, c_int32, c_int32, c_int, c_int64,

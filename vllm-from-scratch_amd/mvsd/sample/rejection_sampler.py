@@ -107,6 +107,9 @@ class RejectionSampler:
                 "speculative decoding with logprobs=-1 (the whole vocabulary) is not supported; "
                 "request logprobs=k with k >= 1")
 
+        if self._bonus_rows_race_only(sampling_metadata, logits):
+            return self._forward_race_only(metadata, draft_probs, logits, sampling_metadata)
+
         # 1) bonus tokens from the bonus rows with the regular sampler (:169-181); their
         # full-row logits are asked for only when logprobs are (the sampled tokens do not
         # depend on it, and the copy is a [B, V] write)
@@ -166,6 +169,60 @@ class RejectionSampler:
                     max_num_logprobs, metadata, logits, None, bonus_rows, output_token_ids)
         return SamplerOutput(sampled_token_ids=output_token_ids,
                              logprobs_tensors=logprobs_tensors)
+
+    def _bonus_rows_race_only(self, sm: SamplingMetadata, logits: torch.Tensor) -> bool:
+        """True when the caller's sampler is mvsd.sample.Sampler itself and, for this batch,
+        it would only take each bonus row's argmax or exponential race: no logprobs, no
+        penalty or active min_tokens, no min_p, top-k or top-p; and the recovered-token seam
+        is the module's own."""
+        from .sampler import Sampler as DeviceSampler
+
+        return (type(self.sampler) is DeviceSampler and sm.max_num_logprobs is None
+                and sm.no_penalties and not _has_active_min_tokens(sm)
+                and sm.min_p is None and sm.top_k is None and sm.top_p is None
+                and sample_recovered_tokens is _SAMPLE_RECOVERED_TOKENS
+                and logits.dtype in (torch.float32, torch.bfloat16, torch.float16)
+                and logits.stride(1) == 1)
+
+    def _forward_race_only(self, metadata: "SpecDecodeMetadata",
+                           draft_probs: torch.Tensor | None, logits: torch.Tensor,
+                           sm: SamplingMetadata):
+        """forward when the bonus rows only need the race (``_bonus_rows_race_only``).
+
+        The randomness is drawn exactly as the reference draws it, in its order: the bonus
+        rows' Exp(1) noise (Sampler.sample's random_sample, for every row unless the batch is
+        all greedy), the uniforms (generate_uniform_probs), the recovered tokens' noise
+        (generate_exponential_noise).  Then one race launch reads the bonus rows in place
+        (greedy rows: their argmax) and the verify kernel reads the verify rows in place, so
+        neither the [B, V] gather of the bonus rows nor its fp32 upcast is written, and the
+        race runs between the noise writes and the verification."""
+        from ..outputs import SamplerOutput
+        from . import sampler as smp
+
+        device = logits.device
+        B = len(metadata.num_draft_tokens)
+        V = logits.shape[-1]
+        num_tokens = int(metadata.draft_token_ids.shape[0])
+        all_greedy = bool(sm.all_greedy)
+        bonus_noise = uniforms = exp_noise = None
+        if not all_greedy:
+            bonus_noise = smp.generate_sampler_noise((B, V), sm.generators, device)
+        if self.synthetic_mode or not all_greedy:
+            uniforms = generate_uniform_probs(num_tokens, metadata.num_draft_tokens,
+                                              sm.generators, device)
+        if not all_greedy and num_tokens > 0:
+            exp_noise = generate_exponential_noise(B, V, metadata.num_draft_tokens,
+                                                   sm.generators, device)
+        bonus = smp.race_rows(logits, metadata.bonus_logits_indices, bonus_noise,
+                              None if all_greedy else sm.temperature)
+        output_token_ids = rejection_sample(
+            metadata.draft_token_ids, metadata.num_draft_tokens, metadata.max_spec_len,
+            metadata.cu_num_draft_tokens, draft_probs, logits, bonus.view(B, 1), sm,
+            synthetic_mode=self.synthetic_mode,
+            synthetic_conditional_rates=self.synthetic_conditional_rates,
+            uniform_probs=uniforms, exp_noise=exp_noise,
+            target_rows=metadata.target_logits_indices, apply_temperature=True)
+        return SamplerOutput(sampled_token_ids=output_token_ids, logprobs_tensors=None)
 
     def _get_logprobs_tensors(self, max_num_logprobs: int, metadata: "SpecDecodeMetadata",
                               logits: torch.Tensor, target_logits: torch.Tensor | None,

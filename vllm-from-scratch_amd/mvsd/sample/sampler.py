@@ -12,11 +12,15 @@ The rejection sampler takes its bonus tokens from a sampler object (rejection_sa
     -> logprobs of the raw (before any processing) or processed rows on request
 
 Every row operation is a HIP kernel (``mvsd_apply_logits_processors``,
-``mvsd_apply_top_k_top_p``, ``mvsd_sampler_rows``, ``mvsd_sampler_race``,
+``mvsd_apply_top_k_top_p``, ``mvsd_sampler_rows``, ``mvsd_sampler_race(_rows)``,
 ``mvsd_spec_logprobs``).  The temperature divide is a tensor divide, as in the reference,
 except where nothing reads the divided rows (no min_p, top-k or top-p, and no processed_*
-logprobs mode): there the race kernel divides each value as it reads it (the same IEEE fp32
-quotient), and the caller's logits are left undivided.  The exponential noise is drawn by
+logprobs mode): there one race launch divides each value as it reads it (the same IEEE fp32
+quotient) and gives the rows under SAMPLING_EPS their argmax, and the caller's logits are
+left undivided.  The race's token is the argmax of softmax(v) / E, evaluated as that of
+v log2(e) - log2(E) (the row's max and sum are common to its entries), so only near-ties
+within a few fp32 ulps of the keys' magnitudes can differ from the reference's fp32
+arithmetic.  The exponential noise is drawn by
 ``generate_sampler_noise`` in the reference's order (the whole block from the global RNG when
 some row has no generator, then each seeded row from its generator), so a given RNG state
 gives the same noise; the function is a seam that tests may replace.
@@ -80,6 +84,39 @@ def random_sample(probs_logits: torch.Tensor, generators: dict[int, torch.Genera
         nat.ptr(temperature), n, V, ws.data_ptr(), ws.numel(), nat.stream_of(x.device)),
         "mvsd_sampler_race")
     return ids.to(torch.int64)
+
+
+def race_rows(logits: torch.Tensor, row_index: torch.Tensor | None,
+              noise: torch.Tensor | None, temperature: torch.Tensor | None,
+              greedy_eps: float = SAMPLING_EPS) -> torch.Tensor:
+    """Sampled ids (int32 [n]) of the rows ``logits[row_index]`` (fp32, bf16 or fp16, read in
+    place) in one ``mvsd_sampler_race_rows`` call: rows whose temperature is below
+    ``greedy_eps`` take the argmax of the raw row (greedy_sample), the others the exponential
+    race of softmax(row / T) with ``noise`` [n, V]; without noise every row is greedy."""
+    nat.require_device_tensor(logits, "logits")
+    assert logits.ndim == 2 and logits.stride(1) == 1
+    device = logits.device
+    rows = None
+    n = logits.shape[0]
+    if row_index is not None:
+        rows = row_index.to(device=device, dtype=torch.int32).contiguous()
+        n = rows.shape[0]
+    V = logits.shape[1]
+    if noise is not None:
+        noise = noise.to(device=device, dtype=torch.float32)
+        assert noise.shape == (n, V) and noise.stride(1) == 1
+    if temperature is not None:
+        temperature = temperature.to(device=device, dtype=torch.float32).contiguous()
+    ids = torch.empty(n, dtype=torch.int32, device=device)
+    lib = nat.lib()
+    ws = torch.empty(max(1, lib.mvsd_sampler_race_workspace_bytes(n, V)), dtype=torch.uint8,
+                     device=device)
+    nat.check(lib.mvsd_sampler_race_rows(
+        ids.data_ptr(), logits.data_ptr(), nat.dtype_code(logits.dtype), logits.stride(0),
+        nat.ptr(rows), logits.shape[0], nat.ptr(noise), 0 if noise is None else noise.stride(0),
+        nat.ptr(temperature), float(greedy_eps), n, V, ws.data_ptr(), ws.numel(),
+        nat.stream_of(device)), "mvsd_sampler_race_rows")
+    return ids
 
 
 class TopKTopPSampler:
@@ -215,9 +252,6 @@ class Sampler:
                logprobs_mode: str | None = None):
         """(tokens, processed logits / logprobs of the processed_* modes) (sampler.py:243-278)."""
         md = sampling_metadata
-        # The argmax is taken on the rows as they arrive (penalties applied, no temperature),
-        # before anything below divides them in place.
-        argmax_ids = None if md.all_random else self.greedy_sample(logits)
         if md.all_greedy:
             # nothing scales or masks an all-greedy batch: the "processed" rows are the rows
             wanted = None
@@ -225,21 +259,25 @@ class Sampler:
                 wanted = {"processed_logits": lambda: logits,
                           "processed_logprobs": lambda: self.compute_logprobs(logits)
                           }.get(logprobs_mode or self.logprobs_mode)
-            return argmax_ids, (wanted() if wanted else None)
+            return self.greedy_sample(logits), (wanted() if wanted else None)
         if md.temperature is None:
             raise ValueError("random rows in the batch but no temperature tensor")
-        # rows under SAMPLING_EPS are greedy: their divisor is 1 and their draw is discarded
-        greedy_rows = md.temperature < SAMPLING_EPS
-        divisor = md.temperature.masked_fill(greedy_rows, 1.0)
         reads_divided_rows = (md.min_p is not None or md.top_k is not None
                               or md.top_p is not None
                               or self.topk_topp_sampler.logprobs_mode in _PROCESSED_MODES)
-        if reads_divided_rows:
-            scaled = self.apply_min_p(logits.div_(divisor.unsqueeze(1)), md.min_p)
-            drawn, processed = self.topk_topp_sampler(scaled, md.generators, md.top_k, md.top_p)
-        else:
-            # the race kernel divides each value as it reads it; the rows stay undivided
-            drawn, processed = random_sample(logits, md.generators, temperature=divisor), None
+        if not reads_divided_rows:
+            # one race launch: rows under SAMPLING_EPS take their argmax, the others race on
+            # fl(x / T) divided as the kernel reads; the caller's rows stay undivided
+            noise = generate_sampler_noise(tuple(logits.shape), md.generators, logits.device)
+            return race_rows(logits, None, noise, md.temperature).to(torch.int64), None
+        # The argmax is taken on the rows as they arrive (penalties applied, no temperature),
+        # before the divide below changes them in place.
+        argmax_ids = None if md.all_random else self.greedy_sample(logits)
+        # rows under SAMPLING_EPS are greedy: their divisor is 1 and their draw is discarded
+        greedy_rows = md.temperature < SAMPLING_EPS
+        divisor = md.temperature.masked_fill(greedy_rows, 1.0)
+        scaled = self.apply_min_p(logits.div_(divisor.unsqueeze(1)), md.min_p)
+        drawn, processed = self.topk_topp_sampler(scaled, md.generators, md.top_k, md.top_p)
         if argmax_ids is not None:
             drawn = torch.where(greedy_rows, argmax_ids, drawn)
         return drawn, processed
