@@ -24,7 +24,7 @@
 //            over the value keys counts entries per pass;
 //   top-p    masses floor(2^40 * exp(v - v_max)) in 64-bit fixed point, so sums are exact and
 //            independent of order.  With a top-k candidate set the prefix is found in LDS;
-//            otherwise a histogram over 2048 logarithmic mass bins (48 per factor of two)
+//            otherwise a histogram over 4096 logarithmic mass bins (96 per factor of two)
 //            locates the bin of the first kept entry, whose entries are gathered, sorted and
 //            scanned; an overfull bin falls back to bisection over (v, index).
 // The limit floor((1 - p) * S) is computed exactly in integers.
@@ -38,7 +38,7 @@ namespace mvsd {
 namespace {
 
 #ifndef MVSD_CONSTRAINT_BATCH
-#define MVSD_CONSTRAINT_BATCH 6   // 16-byte vectors per thread per batch of a row walk
+#define MVSD_CONSTRAINT_BATCH 3   // 16-byte vectors per thread per batch of a row walk
 #endif
 
 #ifndef MVSD_CONSTRAINT_THREADS
@@ -51,9 +51,9 @@ namespace {
 constexpr int kCT = MVSD_CONSTRAINT_THREADS;  // threads per row
 constexpr int kCW = kCT / kWave;
 constexpr int kCap = MVSD_CONSTRAINT_CAP;     // candidates gathered in LDS
-constexpr int kBins = 2048;              // top-p histogram bins
+constexpr int kBins = 4096;              // top-p histogram bins
+constexpr float kBinScale = 96.f * 1.44269504088896340736f;  // bins per unit of v_max - v
 constexpr float kLog2e = 1.44269504088896340736f;
-constexpr float kBinScale = 48.f * kLog2e;   // bins per unit of v_max - v
 constexpr uint32_t kNanKey = 0xffffffffu;
 
 struct ConstraintSmem {
@@ -61,7 +61,6 @@ struct ConstraintSmem {
     unsigned long long hist[kBins];
     unsigned long long cand[kCap];     // ordered_bits(v) << 32 | index, sorted ascending
   } u;
-  alignas(16) uint32_t tkey[kCT];      // per-thread maximum keys
   unsigned long long part[kCT];        // scan partials
   unsigned long long red[kCW];
   unsigned long long bcast[4];
@@ -90,32 +89,42 @@ __device__ inline float vec_elem<MVSD_F16>(const u32x4& r, int j) {
   return static_cast<float>(__builtin_bit_cast(_Float16, (uint16_t)((j & 1) ? (w >> 16) : w)));
 }
 
-// Calls g(vector index, 16-byte vector) for every vector of a row of nvec vectors, in batches
-// of U vectors per thread.  Two batches are in flight: the loop alternates between two
-// register buffers, issuing one buffer's next loads before consuming the other, so each wait
-// covers exactly one batch and no register copy waits for loads.  Addresses are clamped into
-// the row, so every thread issues the same loads.
+// Calls g(vector index, 16-byte vector) for every vector of a row of nvec vectors: full
+// batches of U vectors per thread, two batches in flight (each iteration issues one buffer's
+// next loads before consuming the other, and the loads of a full batch are unconditional, the
+// last one clamped to the last full batch, so each wait covers exactly one batch), then the
+// remaining vectors one per thread and step.
 template <typename G>
 __device__ inline void for_each_vector(const u32x4* xv, int nvec, G&& g) {
   constexpr int U = MVSD_CONSTRAINT_BATCH;
   constexpr int step = U * kCT;
   const int tid = threadIdx.x;
-  u32x4 a[U], b[U];
+  const int nfull = nvec / step;
+  auto load = [&](u32x4 (&buf)[U], int j) {
+    const int base = min(j, nfull - 1) * step + tid;
 #pragma unroll
-  for (int u = 0; u < U; ++u) a[u] = xv[min(tid + u * kCT, nvec - 1)];
-  for (int v0 = tid; v0 < nvec; v0 += 2 * step) {
+    for (int u = 0; u < U; ++u) buf[u] = xv[base + u * kCT];
+  };
+  auto consume = [&](const u32x4 (&buf)[U], int j) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) b[u] = xv[min(v0 + step + u * kCT, nvec - 1)];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (v0 + u * kCT < nvec) g(v0 + u * kCT, a[u]);
-    if (v0 + step >= nvec) break;
-#pragma unroll
-    for (int u = 0; u < U; ++u) a[u] = xv[min(v0 + 2 * step + u * kCT, nvec - 1)];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (v0 + step + u * kCT < nvec) g(v0 + step + u * kCT, b[u]);
+    for (int u = 0; u < U; ++u) g(j * step + tid + u * kCT, buf[u]);
+  };
+  if (nfull > 0) {
+    u32x4 a[U], b[U];
+    load(a, 0);
+    for (int j = 0;;) {
+      load(b, j + 1);
+      // a compiler barrier: the loads above stay issued ahead of the consumption below
+      asm volatile("" ::: "memory");
+      consume(a, j);
+      if (++j == nfull) break;
+      load(a, j + 1);
+      asm volatile("" ::: "memory");
+      consume(b, j);
+      if (++j == nfull) break;
+    }
   }
+  for (int v = nfull * step + tid; v < nvec; v += kCT) g(v, xv[v]);
 }
 
 // Calls f(index, value) for every entry of the row: vector walk for rows that are 16-byte
@@ -220,19 +229,27 @@ __device__ inline unsigned long long block_scan_u64(unsigned long long v, Constr
   return r;
 }
 
-// floor(2^40 * exp(-d)) for d = v_max - v >= 0 (or +inf): the 64-bit fixed-point mass.
-__device__ inline unsigned long long mass_of(float d) {
-  const float e = __builtin_amdgcn_exp2f(-d * kLog2e);  // in [0, 1]
-  const float h = e * 256.f;                            // e * 2^8, exact
+// exp(-d) for d = v_max - v >= 0 (or +inf), in [0, 1].
+__device__ inline float mass_exp(float d) { return __builtin_amdgcn_exp2f(-d * kLog2e); }
+
+// floor(2^40 * e): the 64-bit fixed-point mass.
+__device__ inline unsigned long long mass_from_e(float e) {
+  const float h = e * 256.f;  // e * 2^8, exact
   const float hi = floorf(h);
   const uint32_t lo = (uint32_t)((h - hi) * 4294967296.f);  // exact fraction * 2^32 < 2^32
   return ((unsigned long long)(uint32_t)hi << 32) | lo;
 }
 
+// Histogram bin of d = v_max - v: 96 bins per factor of two of mass, bin 0 at the maximum,
+// clamped to the last bin past d = 29.6 (masses there are below 2^-40 of the maximum's, 0 in
+// fixed point).  A non-decreasing function of d, computed with correctly rounded operations,
+// so the entries of one bin are an interval of v, and of x.
 __device__ inline int mass_bin(float d) {
   const float y = d * kBinScale;
   return y < (float)(kBins - 1) ? (y > 0.f ? (int)y : 0) : kBins - 1;
 }
+
+__device__ inline unsigned long long mass_of(float d) { return mass_from_e(mass_exp(d)); }
 
 // floor(t * S) for fp32 t in (0, 1] and S < 2^64, exactly (t = mant * 2^(e - 24)).
 __device__ inline unsigned long long scaled_floor(float t, unsigned long long S) {
@@ -276,6 +293,99 @@ __device__ inline void append(bool pred, unsigned long long key, ConstraintSmem&
   }
 }
 
+// Appends the keys of this lane's flagged entries (c[j]: key(j)) to the LDS candidate list:
+// per-lane positions from the wave's ballots, one LDS atomic per wave.  Safe with inactive
+// lanes (ballots count active lanes only).
+__device__ inline int lanes_below(unsigned long long mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+template <int N, typename K>
+__device__ inline void append_group(const bool (&c)[N], K&& key, ConstraintSmem& sm) {
+  int total = 0, pos = 0;
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const unsigned long long m = __ballot(c[j]);
+    total += __popcll(m);
+    pos += lanes_below(m);
+  }
+  if (total == 0) return;
+  const int leader = __ffsll((long long)__ballot(true)) - 1;
+  int base = 0;
+  if (lane_id() == leader) base = atomicAdd(&sm.count, total);
+  pos += __shfl(base, leader);
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    if (c[j]) {
+      if (pos < kCap) sm.u.cand[pos] = key(j);
+      ++pos;
+    }
+  }
+}
+
+// Smallest non-NaN x whose bin mass_bin(vmax - fl(x / T)) is at most b: the bin of x falls as x
+// grows, so the entries of bin b are exactly those with min_x_in_bins(b) <= x <
+// min_x_in_bins(b - 1).  Bisection over the ordered keys with the histogram's own arithmetic.
+__device__ inline float min_x_in_bins(float vmax, const Divider& dv, int b) {
+  if (b < 0) return INFINITY;  // no x has a negative bin; +inf bounds every finite entry
+  auto in = [&](uint32_t key) { return mass_bin(vmax - divide(dv, key_float(key))) <= b; };
+  uint32_t lo = ordered_bits(-INFINITY), hi = ordered_bits(INFINITY);  // in(hi) holds
+  if (in(lo)) return -INFINITY;
+  while (hi - lo > 1) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    if (in(mid)) hi = mid;
+    else lo = mid;
+  }
+  return key_float(hi);
+}
+
+// The k-th largest (1 <= k <= kCT) of the block's keys, one per thread (`mine`), by radix
+// selection: four rounds of an 8-bit digit, each counting the keys that share the digits found
+// so far per next digit (LDS atomics on 256 counters), after which one wave picks the digit
+// holding the k-th largest.  Every thread receives the key.  Uses sm.part and sm.bcast.
+__device__ inline uint32_t kth_largest_key(uint32_t mine, int k, ConstraintSmem& sm) {
+  int* cnt = reinterpret_cast<int*>(sm.part);  // 256 counters
+  const int tid = threadIdx.x;
+  uint32_t prefix = 0, pmask = 0;
+  int need = k;  // rank of the wanted key among the keys matching the prefix
+#pragma unroll 1
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int b = tid; b < 256; b += kCT) cnt[b] = 0;
+    __syncthreads();
+    if ((mine & pmask) == prefix) atomicAdd(&cnt[(mine >> shift) & 255u], 1);
+    __syncthreads();
+    if (tid < kWave) {
+      // lane l holds digits 255 - 4l .. 252 - 4l, the largest first
+      int c[4], own = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = cnt[255 - 4 * tid - j];
+        own += c[j];
+      }
+      int incl = own;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const int t = __shfl_up(incl, off);
+        if (tid >= off) incl += t;
+      }
+      const int above = incl - own;  // keys with a larger digit than this lane's
+      if (above < need && need <= incl) {
+        int run = above, j = 0;
+        while (run + c[j] < need) run += c[j++];
+        sm.bcast[0] = (unsigned long long)(255 - 4 * tid - j);
+        sm.bcast[1] = (unsigned long long)(need - run);
+      }
+    }
+    __syncthreads();
+    prefix |= (uint32_t)sm.bcast[0] << shift;
+    pmask |= 0xffu << shift;
+    need = (int)sm.bcast[1];
+    __syncthreads();
+  }
+  return prefix;
+}
+
 // Bitonic sort of cand[0, n), ascending; n <= kCap.
 __device__ inline void sort_candidates(int n, ConstraintSmem& sm) {
   int N = 1;
@@ -300,20 +410,21 @@ __device__ inline void sort_candidates(int n, ConstraintSmem& sm) {
 }
 
 // First position f in the sorted cand[s, e) where base + (mass of cand[s..f]) > limit, or
-// e - 1 when there is none (the last entry is always kept).
-__device__ inline int first_over(int s, int e, float vmax, unsigned long long base,
-                                 unsigned long long limit, ConstraintSmem& sm) {
+// e - 1 when there is none (the last entry is always kept).  mass(key) is a candidate's mass.
+template <typename M>
+__device__ inline int first_over(int s, int e, unsigned long long base, unsigned long long limit,
+                                 ConstraintSmem& sm, M&& mass) {
   const int len = e - s;
   const int per = (len + kCT - 1) / kCT;
   const int b0 = s + (int)threadIdx.x * per, b1 = min(e, b0 + per);
   unsigned long long seg = 0;
-  for (int i = b0; i < b1; ++i) seg += mass_of(vmax - key_float((uint32_t)(sm.u.cand[i] >> 32)));
+  for (int i = b0; i < b1; ++i) seg += mass(sm.u.cand[i]);
   if (threadIdx.x == 0) sm.bcast[0] = (unsigned long long)(e - 1);
   const unsigned long long incl = block_scan_u64(seg, sm);
   unsigned long long run = base + (incl - seg);
   if (run <= limit && limit < base + incl) {
     for (int i = b0; i < b1; ++i) {
-      run += mass_of(vmax - key_float((uint32_t)(sm.u.cand[i] >> 32)));
+      run += mass(sm.u.cand[i]);
       if (run > limit) {
         sm.bcast[0] = (unsigned long long)i;
         break;
@@ -486,32 +597,65 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
   uint32_t t0 = 0, t1 = 0, t2 = 0, t3 = 0;
   constexpr int VEC = Elem<DT>::kVec;
   if (k_only) {
+    // The four largest values in floats (NaN read as -inf and flagged): max / min pairs.  A
+    // row with a NaN, which ranks above every number, takes the key-based walk below.
+    float f0 = -INFINITY, f1 = -INFINITY, f2 = -INFINITY, f3 = -INFINITY;
+    int seen = 0;
+    bool nan = false;
     for_each_group<DT>(x, V, aligned, [&](int, const float (&v)[VEC], int n) {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         if (j < n) {
-          uint32_t c = ordered_bits(v[j]), m;
-          m = max(t0, c); c = min(t0, c); t0 = m;
-          m = max(t1, c); c = min(t1, c); t1 = m;
-          m = max(t2, c); c = min(t2, c); t2 = m;
-          t3 = max(t3, c);
+          nan |= v[j] != v[j];
+          float c = v[j] == v[j] ? v[j] : -INFINITY, m;
+          m = fmaxf(f0, c); c = fminf(f0, c); f0 = m;
+          m = fmaxf(f1, c); c = fminf(f1, c); f1 = m;
+          m = fmaxf(f2, c); c = fminf(f2, c); f2 = m;
+          f3 = fmaxf(f3, c);
         }
       }
+      seen += n;
     });
+    // a slot no entry filled keeps key 0, below every entry's key
+    t0 = seen > 0 ? ordered_bits(f0) : 0u;
+    t1 = seen > 1 ? ordered_bits(f1) : 0u;
+    t2 = seen > 2 ? ordered_bits(f2) : 0u;
+    t3 = seen > 3 ? ordered_bits(f3) : 0u;
+    if (__syncthreads_or(nan)) {
+      t0 = t1 = t2 = t3 = 0;
+      for_each_group<DT>(x, V, aligned, [&](int, const float (&v)[VEC], int n) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          if (j < n) {
+            uint32_t c = ordered_bits(v[j]), m;
+            m = max(t0, c); c = min(t0, c); t0 = m;
+            m = max(t1, c); c = min(t1, c); t1 = m;
+            m = max(t2, c); c = min(t2, c); t2 = m;
+            t3 = max(t3, c);
+          }
+        }
+      });
+    }
   } else {
-    // t1 counts the entries at the thread maximum t0 (for the greedy tie test)
+    // The thread maximum in floats, the number of entries equal to it (for the greedy tie
+    // test; -0 and +0 compare equal, as their keys do) and a NaN flag (NaN ranks above every
+    // number, so the thread's key is then the NaN key).
+    float fm = -INFINITY;
+    uint32_t ties = 0;
+    bool nan = false;
     for_each_group<DT>(x, V, aligned, [&](int, const float (&v)[VEC], int n) {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         if (j < n) {
-          const uint32_t c = ordered_bits(v[j]);
-          t1 = c > t0 ? 1u : t1 + (c == t0);
-          t0 = max(t0, c);
+          nan |= v[j] != v[j];
+          ties = v[j] > fm ? 1u : ties + (v[j] == fm);
+          fm = fmaxf(fm, v[j]);
         }
       }
     });
+    t0 = nan ? kNanKey : (ties > 0 ? ordered_bits(fm) : 0u);
+    t1 = ties;
   }
-  sm.tkey[tid] = t0;
   const uint32_t mkey = block_max_u32(t0, sm);
   if (greedy_row) {
     const unsigned long long ties = block_sum_u64(t0 == mkey ? t1 : 0u, sm);
@@ -530,21 +674,9 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
     uint32_t theta = 0;
     if (k <= kCT) {
       // theta: the k-th largest thread maximum; at least k entries are >= theta
-      const uint32_t mine = sm.tkey[tid];
-      const uint4* tk4 = reinterpret_cast<const uint4*>(sm.tkey);
-      int rank = 0;
-#pragma unroll 8
-      for (int u = 0; u < kCT / 4; ++u) {
-        const uint4 o = tk4[u];
-        rank += (o.x > mine) | ((o.x == mine) & (4 * u < tid));
-        rank += (o.y > mine) | ((o.y == mine) & (4 * u + 1 < tid));
-        rank += (o.z > mine) | ((o.z == mine) & (4 * u + 2 < tid));
-        rank += (o.w > mine) | ((o.w == mine) & (4 * u + 3 < tid));
-      }
-      if (rank == k - 1) sm.bcast[1] = mine;
+      theta = kth_largest_key(t0, k, sm);
       if (tid == 0) sm.count = 0;
       __syncthreads();
-      theta = (uint32_t)sm.bcast[1];
     }
     bool k_done = false;
     uint32_t vk_key = 0;
@@ -645,7 +777,10 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
     for (int i = lo_k + tid; i < n; i += kCT)
       seg += mass_of(vmax - key_float((uint32_t)(sm.u.cand[i] >> 32)));
     const unsigned long long total = block_sum_u64(seg, sm);
-    fkey = sm.u.cand[max(first_over(lo_k, n, vmax, 0, scaled_floor(tl, total), sm), 0)];
+    fkey = sm.u.cand[max(first_over(lo_k, n, 0, scaled_floor(tl, total), sm,
+                                    [&](unsigned long long key) {
+                                      return mass_of(vmax - key_float((uint32_t)(key >> 32)));
+                                    }), 0)];
   } else {
     for (int b = tid; b < kBins; b += kCT) sm.u.hist[b] = 0;
     __syncthreads();
@@ -663,7 +798,7 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
     });
     __syncthreads();
     // Bins run from large v (bin 0) to small v, so the mass below a bin is a suffix sum.
-    // Thread t owns bins [4t, 4t + 4); the scan runs over reversed thread order.
+    // Thread t owns bins [per t, per (t + 1)); the scan runs over reversed thread order.
     constexpr int per = kBins / kCT;
     unsigned long long s4 = 0;
     for (int j = 0; j < per; ++j) s4 += sm.u.hist[tid * per + j];
@@ -676,7 +811,7 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
       sm.part[rt] += add;
       __syncthreads();
     }
-    const unsigned long long incl = sm.part[rt];  // mass of bins >= 4t
+    const unsigned long long incl = sm.part[rt];  // mass of bins >= per t
     const unsigned long long total = sm.part[kCT - 1];
     if (tid == 0) {
       sm.bcast[2] = 0;
@@ -701,7 +836,7 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
       fkey = best;
     } else {
       if (tid == 0) sm.count = 0;
-      unsigned long long run = incl - s4;  // mass of bins >= 4t + 4
+      unsigned long long run = incl - s4;  // mass of bins >= per (t + 1)
       if (run <= limit && limit < incl) {
         for (int j = per - 1; j >= 0; --j) {
           const unsigned long long h = sm.u.hist[tid * per + j];
@@ -716,25 +851,25 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
       __syncthreads();
       const int bin = (int)sm.bcast[2];
       const unsigned long long base = sm.bcast[3];  // mass below the bin
+      // the bin's entries as an interval of raw values (no divide or exp per entry), kept by
+      // top-k too (x >= A)
+      const float blo = fmaxf(min_x_in_bins(vmax, dv, bin), A);
+      const float bhi = min_x_in_bins(vmax, dv, bin - 1);
       for_each_group<DT>(x, V, aligned, [&](int i0, const float (&v)[VEC], int n) {
-        float q[VEC];
-        divide_group(dv, v, q);
-        bool c[VEC], any = false;
+        bool c[VEC];
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-          c[j] = (j < n) && !(v[j] < A) && mass_bin(vmax - q[j]) == bin;
-          any |= c[j];
-        }
-        if (__ballot(any) == 0) return;
-#pragma unroll
-        for (int j = 0; j < VEC; ++j)
-          append(c[j], c[j] ? (((unsigned long long)ordered_bits(q[j]) << 32) | (uint32_t)(i0 + j)) : 0ull, sm);
+        for (int j = 0; j < VEC; ++j) c[j] = (j < n) && v[j] >= blo && v[j] < bhi;
+        append_group(c, [&](int j) {
+          return ((unsigned long long)ordered_bits(divide(dv, v[j])) << 32) | (uint32_t)(i0 + j);
+        }, sm);
       });
       __syncthreads();
       const int nb = sm.count;
       if (nb <= kCap) {
         sort_candidates(nb, sm);
-        fkey = sm.u.cand[max(first_over(0, nb, vmax, base, limit, sm), 0)];
+        fkey = sm.u.cand[max(first_over(0, nb, base, limit, sm, [&](unsigned long long key) {
+                               return mass_of(vmax - key_float((uint32_t)(key >> 32)));
+                             }), 0)];
       } else {
         // Too many entries in one bin (long runs of equal values): bisection over the value
         // keys, then over the indices within the value, with exact sums per pass.
