@@ -169,7 +169,8 @@ int64_t mvsd_rejection_workspace_bytes(int64_t batch_size, int64_t num_tokens, i
                                        int target_dtype, int64_t max_spec_len) {
   (void)max_spec_len;
   if (batch_size < 0 || num_tokens < 0 || vocab_size <= 0) return -1;
-  const mvsd::VerifyPlan plan = mvsd::verify_plan(target_dtype, vocab_size, 0, 0);
+  const mvsd::VerifyPlan plan = mvsd::verify_plan(target_dtype, vocab_size, 0, 0,
+                                                  num_tokens + launch_requests(batch_size));
   return verify_layout(launch_requests(batch_size), num_tokens, plan.nc_max).total;
 }
 
@@ -218,7 +219,8 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
 
   // Slot arrays are sized for the most chunks any plan can use, so the layout does not depend
   // on the device.
-  const mvsd::VerifyPlan size_plan = mvsd::verify_plan(a->target_dtype, V, 0, 0);
+  const int64_t batch_rows = P + launch_requests(B);
+  const mvsd::VerifyPlan size_plan = mvsd::verify_plan(a->target_dtype, V, 0, 0, batch_rows);
   const WorkspaceLayout lay = verify_layout(launch_requests(B), P, size_plan.nc_max);
   if (!ws_ptr || ws_bytes < lay.total) return MVSD_E_WORKSPACE;
   if ((uintptr_t)ws_ptr % 256 != 0) return MVSD_E_ALIGN;
@@ -304,7 +306,7 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
     int64_t groups = Bl * groups_per_req;
     if (groups > P) groups = P;
     const int64_t units = groups + (scores ? Bl : 0);
-    const mvsd::VerifyPlan plan = mvsd::verify_plan(a->target_dtype, V, units, cap);
+    const mvsd::VerifyPlan plan = mvsd::verify_plan(a->target_dtype, V, units, cap, batch_rows);
     q.chunk = plan.chunk;
     q.nc = plan.nc;
     int64_t grid = units * plan.nc;

@@ -105,14 +105,16 @@ struct VerifyPlan {
   int ept;     // elements per thread per row in one sub-chunk
   int g;       // rows per stats group
   int sub;     // columns per sub-chunk (threads * ept)
-  int nc_max;  // largest nc any plan for this vocabulary uses (sizes the workspace)
+  int nc_max;  // largest nc any plan for this vocabulary and batch size uses (sizes the workspace)
   int chunk;   // columns per task, a multiple of sub
   int nc;      // chunks per row
 };
 
 // units = stats groups + score units of the launch (0 gives the workspace-sizing plan);
-// cap = resident workgroups.
-VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int cap);
+// cap = resident workgroups; batch_rows = verify rows + requests of the call (the same value
+// when sizing the workspace and when planning its launches: nc never exceeds nc_max).
+VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int cap,
+                       int64_t batch_rows);
 
 // The verify kernel variant for a target dtype, draft dtype (-1: point-mass drafts) and
 // sampling constraints.

@@ -1266,6 +1266,8 @@ hipError_t launch_zero_fill(void* p, int64_t bytes, hipStream_t stream) {
 // ------------------------------------------------------------------ dispatch ---------
 constexpr int kGroup = 4;          // rows per stats group
 constexpr int kMinSubs = 8;        // sub-chunks per task at least
+constexpr int kMinSubsSmall = 2;   // ... on batches too small to fill the device otherwise
+constexpr int64_t kSmallBatchRows = 64;  // verify rows + requests of such a batch at most
 // Every task has fixed costs (its first loads' latency, block reductions, publication), so
 // tasks are as long as the tail allows: about 7 per resident workgroup measured 1.5 % faster at
 // the headline and 1.8 % on a ragged bf16 batch than 10 (with tasks capped at 512 KiB).  On large
@@ -1277,7 +1279,8 @@ constexpr int ept_of() {
   return DT == MVSD_F32 ? 4 : 8;  // 16 bytes of target per thread and row per sub-chunk
 }
 
-VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int cap) {
+VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int cap,
+                       int64_t batch_rows) {
   VerifyPlan plan;
   plan.ept = target_dtype == MVSD_F32 ? ept_of<MVSD_F32>() : ept_of<MVSD_BF16>();
   plan.g = kGroup;
@@ -1285,15 +1288,27 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int 
   const int64_t nsub = (vocab_size + plan.sub - 1) / plan.sub;
   // Chunks per row: enough tasks for about kTasksPerWg per resident workgroup, each task as
   // long as possible (fewer ticket claims, longer load pipelines), and at least kMinSubs
-  // sub-chunks per task so that small batches do not shred the rows into tasks too short to
-  // amortise their start and end.
+  // sub-chunks per task so that batches do not shred the rows into tasks too short to
+  // amortise their start and end.  A batch of at most kSmallBatchRows verify rows and requests
+  // that cannot give every resident workgroup a task of kMinSubs sub-chunks (a few requests)
+  // takes shorter tasks instead, down to kMinSubsSmall sub-chunks, so that its few megabytes
+  // are spread over the device.
   // Score tasks walk sub-chunks of twice the columns, so chunks hold an even number of
   // sub-chunks.
-  const int64_t nc_max = nsub / kMinSubs > 1 ? nsub / kMinSubs : 1;
-  int64_t nc = nc_max;
+  const int64_t nc_regular = nsub / kMinSubs > 1 ? nsub / kMinSubs : 1;
+  const int64_t nc_small = nsub / kMinSubsSmall > 1 ? nsub / kMinSubsSmall : 1;
+  // the workspace holds slots for nc_max chunks per row
+  const int64_t nc_max = batch_rows <= kSmallBatchRows ? nc_small : nc_regular;
+  int64_t nc_hi = nc_regular;
+  if (units > 0 && cap > 0 && units * nc_regular < cap) {
+    const int64_t want = (cap + units - 1) / units;
+    nc_hi = want < nc_max ? want : nc_max;
+    if (nc_hi < nc_regular) nc_hi = nc_regular;
+  }
+  int64_t nc = nc_hi;
   if (units > 0 && cap > 0) {
     nc = ((int64_t)kTasksPerWg * cap + units - 1) / units;
-    nc = nc < 1 ? 1 : (nc > nc_max ? nc_max : nc);
+    nc = nc < 1 ? 1 : (nc > nc_hi ? nc_hi : nc);
   }
   int64_t subs_per_chunk = (nsub + nc - 1) / nc;
   if (subs_per_chunk > 1) subs_per_chunk += subs_per_chunk & 1;
