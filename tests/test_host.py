@@ -80,6 +80,38 @@ def test_acceptance_stats():
     assert stats.num_draft_tokens_per_pos == [3, 2, 1]
 
 
+def test_spec_decoding_logging_aggregates_steps():
+    """SpecDecodingLogging (metrics.py:66-146): totals over the observed steps, per-position
+    sums over lists of different lengths, rates from the totals, one log line, then a new
+    interval; an empty interval reports empty totals without logging; observing copies."""
+    from mvsd.spec_decode import SpecDecodingLogging, SpecDecodingStats
+
+    lines = []
+    agg = SpecDecodingLogging(log_fn=lambda fmt, *args: lines.append(fmt % args))
+    assert agg.log() == {"num_drafts": 0, "num_draft_tokens": 0, "num_accepted_tokens": 0,
+                         "accepted_tokens_per_pos": [], "draft_tokens_per_pos": [],
+                         "acceptance_rate": None, "mean_acceptance_length": None}
+    assert lines == [] and len(agg) == 0
+    a = stats_from_outputs([[1, 2, 3], [4], [5, 6]], [2, 3, 1], 3)   # accepted 2, 0, 1
+    b = SpecDecodingStats.new(4)
+    b.observe_draft(4, 4)
+    agg.observe(a)
+    agg.observe(b)
+    b.observe_draft(4, 1)                  # after observe: not counted
+    assert len(agg) == 2
+    got = agg.log()
+    assert got["num_drafts"] == 4 and got["num_draft_tokens"] == 10
+    assert got["num_accepted_tokens"] == 7
+    assert got["accepted_tokens_per_pos"] == [3, 2, 1, 1]
+    assert got["draft_tokens_per_pos"] == [4, 3, 2, 1]
+    assert got["acceptance_rate"] == 0.7
+    assert got["mean_acceptance_length"] == 1 + 7 / 4
+    assert got["draft_throughput"] > 0 and got["accepted_throughput"] > 0
+    assert len(lines) == 1 and "Mean acceptance length: 2.75" in lines[0]
+    assert "Accepted: 7 tokens, Drafted: 10 tokens, Avg Draft acceptance rate: 70.0%" in lines[0]
+    assert len(agg) == 0 and agg.log()["num_drafts"] == 0
+
+
 def test_block_method_is_refused():
     spec = type("S", (), {"rejection_sample_method": "block"})()
     with pytest.raises(NotImplementedError):
