@@ -112,6 +112,36 @@ def test_spec_decoding_logging_aggregates_steps():
     assert len(agg) == 0 and agg.log()["num_drafts"] == 0
 
 
+def test_ngram_history_sync_copies_only_each_rows_history():
+    """update_ngram_gpu_tensors_incremental (reference ngram_proposer_gpu.py:348-416) on CPU
+    tensors: reordered rows move, new requests get their first n tokens in one batched copy,
+    entries past n keep what the device buffer held, and every active row's length syncs."""
+    from mvsd.spec_decode.ngram_proposer_gpu import update_ngram_gpu_tensors_incremental
+
+    class Batch:
+        pass
+
+    batch = Batch()
+    batch.token_ids_cpu = torch.tensor([[5, 6, 7, 8, 9], [1, 2, 0, 0, 0], [3, 3, 3, 4, 0]],
+                                       dtype=torch.int32)
+    batch.num_tokens_no_spec = torch.tensor([4, 2, 3], dtype=torch.int64)
+    batch.req_id_to_index = {"a": 0, "b": 1, "c": 2}
+    tokens = torch.full((3, 5), -7, dtype=torch.int32)
+    lens = torch.zeros(3, dtype=torch.int32)
+    update_ngram_gpu_tensors_incremental(batch, tokens, lens, {"a", "b", "c"}, None, "cpu")
+    assert tokens.tolist() == [[5, 6, 7, 8, -7], [1, 2, -7, -7, -7], [3, 3, 3, -7, -7]]
+    assert lens.tolist() == [4, 2, 3]
+    # "c" moves to row 0, "a" to row 2, "d" is new in row 1 with an empty history
+    batch.token_ids_cpu[1] = torch.tensor([0, 0, 0, 0, 0], dtype=torch.int32)
+    batch.num_tokens_no_spec = torch.tensor([3, 0, 4], dtype=torch.int64)
+    batch.req_id_to_index = {"c": 0, "d": 1, "a": 2}
+    update_ngram_gpu_tensors_incremental(batch, tokens, lens, {"d"}, {"a": 0, "b": 1, "c": 2},
+                                         "cpu")
+    assert tokens[0].tolist() == [3, 3, 3, -7, -7] and tokens[2].tolist() == [5, 6, 7, 8, -7]
+    assert tokens[1].tolist() == [1, 2, -7, -7, -7]  # nothing to copy for an empty history
+    assert lens.tolist() == [3, 0, 4]
+
+
 def test_block_method_is_refused():
     spec = type("S", (), {"rejection_sample_method": "block"})()
     with pytest.raises(NotImplementedError):

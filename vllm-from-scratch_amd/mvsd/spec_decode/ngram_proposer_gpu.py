@@ -179,8 +179,11 @@ class NgramProposerGPU:
             sampled, input_batch, token_ids_gpu, num_tokens_no_spec_gpu, discard)
         drafts, num_valid = self.propose(self.k, num_tokens_no_spec_gpu, token_ids_gpu,
                                          valid_ids, counts)
-        return DraftTokenIds(req_ids=[t.req_id for t in rows], draft_token_ids=drafts.cpu().tolist(),
-                             num_valid_draft_tokens=num_valid.cpu().tolist())
+        # one device-to-host copy: the drafts with the valid count as an extra column
+        host = torch.cat([drafts.to(torch.int64), num_valid.to(torch.int64)[:, None]], dim=1).cpu()
+        return DraftTokenIds(req_ids=[t.req_id for t in rows],
+                             draft_token_ids=host[:, :-1].tolist(),
+                             num_valid_draft_tokens=host[:, -1].tolist())
 
     def remove_requests(self, req_ids) -> None:
         pass
@@ -214,11 +217,19 @@ def update_ngram_gpu_tensors_incremental(input_batch, token_ids_gpu_tensor,
         copy_ids = [r for r in new_req_ids if r in current]
     else:
         copy_ids = list(current)
-    for req_id in copy_ids:
-        index = current[req_id]
-        n = int(input_batch.num_tokens_no_spec[index])
-        if n > 0:
-            token_ids_gpu_tensor[index, :n].copy_(input_batch.token_ids_cpu[index, :n],
-                                                  non_blocking=True)
+    if copy_ids:
+        # One host-to-device copy for all of them: the histories padded to the longest, with
+        # each row's length as a last column; only the first n entries of a row are written.
+        rows = torch.tensor([current[r] for r in copy_ids], dtype=torch.long)
+        lens = input_batch.num_tokens_no_spec[rows].to(torch.int64)
+        width = min(int(lens.max()), token_ids_gpu_tensor.shape[1])
+        if width > 0:
+            block = torch.cat([input_batch.token_ids_cpu[rows, :width].to(torch.int64),
+                               lens[:, None]], dim=1).to(device)
+            rows_gpu = rows.to(device)
+            keep = (torch.arange(width, device=device)[None, :] < block[:, -1:])
+            current_rows = token_ids_gpu_tensor[rows_gpu, :width]
+            token_ids_gpu_tensor[rows_gpu, :width] = torch.where(
+                keep, block[:, :width].to(token_ids_gpu_tensor.dtype), current_rows)
     values = input_batch.num_tokens_no_spec[torch.tensor(active, dtype=torch.long)]
     num_tokens_no_spec_gpu.index_copy_(0, active_gpu, values.to(device=device, dtype=torch.int32))
