@@ -235,4 +235,3 @@ def test_short_synthetic_rates_are_refused():
     dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
     with pytest.raises(ValueError, match="synthetic_conditional_rates"):
         rejection_sample(**dev, synthetic_conditional_rates=torch.tensor([0.9, 0.5]).cuda())
-
