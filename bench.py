@@ -76,6 +76,10 @@ TRAFFIC = {
     "c4": (ROOT / "profiles" / "constraints_and_verify_c4_traffic.md",
            VERIFY_SOURCES + [_CSRC + "constraints.hip"]),
     "c5": (ROOT / "profiles" / "verify_kernel_c5_traffic.md", VERIFY_SOURCES),
+    "c1": (ROOT / "profiles" / "verify_kernel_c1_traffic.md", VERIFY_SOURCES),
+    "c2": (ROOT / "profiles" / "verify_kernel_c2_traffic.md", VERIFY_SOURCES),
+    "v2": (ROOT / "profiles" / "v2_verify_kernels_traffic.md",
+           [_CSRC + f for f in ("v2_verify.hip", "verify.h", "mvsd_device.h")]),
 }
 
 
@@ -561,7 +565,7 @@ def bench_ngram_host_api(tokens_np, lens_np, steps, warmup, device):
     return (time.perf_counter() - t0) / steps * 1e3
 
 
-def bench_v2(device, steps, warmup, with_cpu, cpu_seconds):
+def bench_v2(device, steps, warmup, with_cpu, cpu_seconds, pmc=False):
     """The V2 runner's verification (mvsd.worker.gpu.spec_decode.rejection_sample) on the
     headline shape: B=256, k=4, V=151936 fp32, all random at T=0.8, draft logits
     [B, k, V] pre-temperature, target = draft + N(0, 0.5^2) (already scaled), drafts sampled
@@ -599,6 +603,9 @@ def bench_v2(device, steps, warmup, with_cpu, cpu_seconds):
     def step():
         return rejection_sample(**case)
 
+    if pmc:
+        pmc_driver(step, device)
+        return None
     ms, wall_ms, (s, n) = time_steps(step, steps, warmup)
     n_host = n.cpu().numpy()
     s_host = s.cpu().numpy()
@@ -607,12 +614,15 @@ def bench_v2(device, steps, warmup, with_cpu, cpu_seconds):
     nbytes = 2 * P * V * 4 + n_bonus * V * 4 + rows * (4 + 8 + 4 + 4) + B * (4 + 4 + 4 + 8) \
         + B * (K + 1) * 8 + B * 4
     gbs = nbytes / (ms / 1e3) / 1e9
+    traffic = load_traffic("v2")
     entry = {"workload": "v2 B=256 k=4 V=151936 fp32 random T=0.8, draft logits [B, k, V]",
              "steps": steps, "warmup": warmup, "dtype": "f32",
              "ms_per_step": round(ms, 5), "wall_ms_per_step": round(wall_ms, 5),
              "kernel_bytes": nbytes, "GBps_on_kernel_bytes": round(gbs, 2),
              "frac_on_kernel_bytes": round(gbs / HBM_PEAK_GBS, 4),
              "kernels": "v2_stats + v2_chain + v2_resample + v2_insert per call",
+             "traffic": traffic,
+             "traffic_over_kernel_bytes": None if traffic is None else round(traffic / nbytes, 4),
              "verified_tok_per_s": round(float(n_host.sum()) / (ms / 1e3), 1),
              "accept_length_hist": np.bincount(n_host - 1, minlength=K + 1).tolist(),
              "cpu_baseline": None, "parity": None}
@@ -747,6 +757,9 @@ def main():
                 **bench_ngram(device, args.steps, args.warmup, with_cpu, args.cpu_seconds)}
         line["value"] = line["requests_per_s"]
         print(json.dumps(line), flush=True)
+        return
+    if args.config == "v2" and args.pmc_driver:
+        bench_v2(device, args.steps, args.warmup, False, 0.0, pmc=True)
         return
     if args.config == "v2":
         line = {"metric": "V2 rejection-sampler HBM GB/s (% of peak) + verified tok/s, "
