@@ -142,6 +142,39 @@ def test_greedy_argmax_at_every_position(device, dtype, V):
     assert got == logits.float().argmax(-1).cpu().tolist()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("V", [4096 + 8, 151936])
+def test_greedy_16bit_special_values(device, dtype, V):
+    """16-bit greedy rows (their argmax runs over ordered 16-bit keys): NaN ranks first and the
+    first NaN wins whatever its sign or payload; -0 and +0 tie; -inf rows give column 0; +inf
+    beats every finite value; an entry at the last column and one in the partial last
+    sub-chunk win.  Expected: the first index of the maximum, NaN above every number."""
+    def row(fill=-1.0):
+        return torch.full((V,), fill, dtype=torch.float32)
+    rows, expect = [], []
+    r = row(); r[100] = 5.0; r[3000] = float("nan"); r[3500] = float("nan"); rows.append(r); expect.append(3000)
+    r = row(); r[10] = 7.0; rows.append(r); expect.append(10)
+    r = row(-float("inf")); rows.append(r); expect.append(0)
+    r = row(-2.0); r[40] = -0.0; r[41] = 0.0; r[7] = -0.0; rows.append(r); expect.append(7)
+    r = row(); r[V - 1] = float("inf"); r[5] = 60000.0; rows.append(r); expect.append(V - 1)
+    r = row(); r[V - 3] = 3.0; rows.append(r); expect.append(V - 3)
+    r = row(); r[200] = -float("inf"); r[201] = -0.5; rows.append(r); expect.append(201)
+    logits = torch.stack(rows).to(dtype)
+    # a NaN with the sign bit set ranks first as well
+    bits = logits.view(torch.int16)
+    bits[0, 3000] = bits[0, 3000] | -32768
+    logits = logits.to(device)
+    n = len(rows)
+    drafts = [[0] for _ in range(n)]
+    meta = make_metadata(drafts, device=device)
+    out = rs.rejection_sample(meta.draft_token_ids, meta.num_draft_tokens, 1,
+                              meta.cu_num_draft_tokens, None, logits,
+                              torch.full((n, 1), 7, dtype=torch.int32, device=device),
+                              sm_for([0.0] * n, drafts, device))
+    got = out[:, 0].cpu().tolist()
+    assert got == expect, (got, expect)
+
+
 def test_greedy_argmax_treats_signed_zeros_as_equal(device):
     """-0.0 == +0.0 for torch.argmax: the first of them is the argmax."""
     logits = torch.tensor([[-1.0, -0.0, 0.0, -2.0], [-3.0, 0.0, -0.0, -0.0]], device=device)

@@ -437,6 +437,55 @@ __device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int n
     bv[g] = -INFINITY;
     bi[g] = (int)v0;
   }
+  if constexpr (Elem<DT>::kVec == 8) {
+    // 16-bit targets, 8 consecutive columns per thread and sub-chunk.  Per row the sub-chunk's
+    // maximum comes from a tree of max operations and its NaN test from a tree of sums (a NaN
+    // entry, or +inf beside -inf, makes the sum NaN); only a lane whose maximum exceeds its
+    // best so far then looks for the first column holding it.  Sub-chunks whose sum is NaN,
+    // and rows with a mask, take the per-entry rule below (NaN first, lowest column).  Entries
+    // past vend hold -inf (the checked loads' fill) at higher columns than every entry of the
+    // chunk, so they never win: ties keep the lower column.
+    static_assert(EPT == 8, "one 16-byte vector per row and sub-chunk");
+    bool has_mask[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)  // a neutral mask (A = B = -inf) masks nothing
+      has_mask[g] = MASKED && (mk[g].x != -INFINITY || mk[g].y != -INFINITY);
+    auto body = [&](const TargetBuf<DT, EPT, G>& buf, int64_t s0, auto) {
+      const int col0 = elem_index<DT, EPT>(s0, 0);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        if (g < nrows) {
+          float x[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) x[k] = raw_elem<DT>(buf.x[g], k);
+          const float sum = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+          if (has_mask[g] || sum != sum) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              float v = x[k];
+              if constexpr (MASKED) v = row_masked(mk[g], v, col0 + k) ? -INFINITY : v;
+              const bool take = (v > bv[g]) | ((v != v) & (bv[g] == bv[g]));
+              bv[g] = take ? v : bv[g];
+              bi[g] = take ? col0 + k : bi[g];
+            }
+          } else {
+            const float lm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                                   fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+            if (lm > bv[g]) {
+              int kk = 7;
+#pragma unroll
+              for (int k = 6; k >= 0; --k) kk = x[k] == lm ? k : kk;
+              bv[g] = lm;
+              bi[g] = col0 + kk;
+            }
+          }
+        }
+      }
+    };
+    pipeline<kVThreads * EPT, TargetBuf<DT, EPT, G>>(v0, vend, p.target_aligned,
+                                                     target_loader<DT, EPT, G>(p, tb, vend), body,
+                                                     after_loads);
+  } else {
   auto body = [&](const TargetBuf<DT, EPT, G>& buf, int64_t s0, auto fast) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -458,6 +507,7 @@ __device__ inline void task_argmax(const VerifyParams& p, int c, int row0, int n
   pipeline<kVThreads * EPT, TargetBuf<DT, EPT, G>>(v0, vend, p.target_aligned,
                                                    target_loader<DT, EPT, G>(p, tb, vend), body,
                                                    after_loads);
+  }
   uint64_t key[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) key[g] = argmax_key(bv[g], bi[g]);
@@ -480,10 +530,13 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
   float4 mk[G];
   row_masks<MASKED, G>(p, row0, nrows, mk);
   float m[G], s[G];
+  bool has_mask[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
     s[g] = 0.f;
+    // a neutral mask (A = B = -inf) masks nothing: such rows skip the per-entry test
+    has_mask[g] = MASKED && (mk[g].x != -INFINITY || mk[g].y != -INFINITY);
   }
   auto body = [&](const TargetBuf<DT, EPT, G>& buf, int64_t s0, auto) {
 #pragma unroll
@@ -501,14 +554,19 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
           m[g] = lm;
         }
         const float ref = m[g] == -INFINITY ? 0.f : m[g];
-        float acc = 0.f;
+        auto sum = [&](auto with_mask) {
+          float acc = 0.f;
 #pragma unroll
-        for (int k = 0; k < EPT; ++k) {
-          const float e = __builtin_amdgcn_exp2f((x[k] - ref) * c1);
-          if constexpr (MASKED) acc += row_masked(mk[g], x[k], elem_index<DT, EPT>(s0, k)) ? 0.f : e;
-          else acc += e;
-        }
-        s[g] += acc;
+          for (int k = 0; k < EPT; ++k) {
+            const float e = __builtin_amdgcn_exp2f((x[k] - ref) * c1);
+            if constexpr (decltype(with_mask)::value)
+              acc += row_masked(mk[g], x[k], elem_index<DT, EPT>(s0, k)) ? 0.f : e;
+            else
+              acc += e;
+          }
+          return acc;
+        };
+        s[g] += has_mask[g] ? sum(std::true_type()) : sum(std::false_type());
       }
     }
   };
