@@ -556,6 +556,11 @@ __device__ inline void task_stats(const VerifyParams& p, int c, float c1, int ro
         const float ref = m[g] == -INFINITY ? 0.f : m[g];
         auto sum = [&](auto with_mask) {
           float acc = 0.f;
+          // entries below A are masked: a lane whose entries are all below it adds nothing
+          // (a wave skips the exponentials when all its lanes do, as on most of a top-k row)
+          if constexpr (decltype(with_mask)::value) {
+            if (lm < mk[g].x) return acc;
+          }
 #pragma unroll
           for (int k = 0; k < EPT; ++k) {
             const float e = __builtin_amdgcn_exp2f((x[k] - ref) * c1);
@@ -706,24 +711,62 @@ __device__ inline uint64_t task_score(const VerifyParams& p, int r, float c1, in
   // (0, v0) and taking only strictly larger scores gives the same argmax without the clamp.
   float bv = 0.f;
   int bi = (int)v0;
+  // a neutral mask (A = B = -inf) masks nothing
+  const bool has_mask = MASKED && (mk.x != -INFINITY || mk.y != -INFINITY);
   auto body = [&](const Buf& buf, int64_t s0, auto fast) {
-    float inv[EPT];
+    if constexpr (MASKED) {
+      // entries below A are masked and score at most 0: a lane whose entries are all below it
+      // has nothing to score (a wave skips when all its lanes do, as on most of a top-k row)
+      if (has_mask) {
+        float xm = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) inv[k] = recip_rn(raw_f32(buf.e, k));
+        for (int k = 0; k < EPT; ++k) xm = fmaxf(xm, quad_elem<DT>(buf.x, k));
+        if (xm < mk.x) return;
+      }
+    }
+    float sc[EPT];
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
       const int idx = elem_index<MVSD_F32, EPT>(s0, k);
       const float x = quad_elem<DT>(buf.x, k);
       float prob = __builtin_amdgcn_exp2f(fmaf(x - MX, c1, NL));  // softmax
-      if constexpr (MASKED) prob = row_masked(mk, x, idx) ? 0.f : prob;
+      if constexpr (MASKED) prob = has_mask && row_masked(mk, x, idx) ? 0.f : prob;
       float w;
       if constexpr (HAS_DRAFT) w = prob - draft_elem<DD>(buf.q.w, k);  // clamp folded into bv >= 0
       else w = idx == d ? 0.f : prob;
-      const float score = w * inv[k];
-      // columns rise with s0 and k, so a strict compare keeps the first maximum
-      const bool take = (score > bv) & (decltype(fast)::value || idx < vend);
-      bv = take ? score : bv;
-      bi = take ? idx : bi;
+      const float score = w * recip_rn(raw_f32(buf.e, k));
+      sc[k] = (decltype(fast)::value || idx < vend) ? score : 0.f;
+    }
+    if constexpr (Elem<DT>::kVec == 4) {
+      // fp32 targets: a strict compare per entry keeps the first maximum (columns rise with s0
+      // and k); at 8 entries per lane this measured faster than the tree below
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) {
+        const bool take = sc[k] > bv;
+        bv = take ? sc[k] : bv;
+        bi = take ? elem_index<MVSD_F32, EPT>(s0, k) : bi;
+      }
+      return;
+    }
+    // 2-byte targets, 16 entries per lane: the lane's best of this sub-chunk from a tree of
+    // maxima; only a lane whose best beats its best so far looks for the first column holding
+    // it, so the first maximum is kept (columns rise with s0 and k).  A NaN score never wins
+    // (the tree drops it, and NaN > bv is false).
+    float t[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) t[k] = sc[k];
+#pragma unroll
+    for (int w = EPT / 2; w >= 1; w /= 2) {
+#pragma unroll
+      for (int k = 0; k < w; ++k) t[k] = fmaxf(t[k], t[k + w]);
+    }
+    const float m = t[0];
+    if (m > bv) {
+      int kk = EPT - 1;
+#pragma unroll
+      for (int k = EPT - 2; k >= 0; --k) kk = sc[k] == m ? k : kk;
+      bv = m;
+      bi = elem_index<MVSD_F32, EPT>(s0, kk);
     }
   };
   pipeline<kVThreads * EPT, Buf>(v0, vend, aligned, load, body, wait_stats);
