@@ -11,6 +11,8 @@ Bar:
   * the corrected division x / T the thresholds rely on equals IEEE division for every
     float x (mvsd_selftest(1))."""
 
+from dataclasses import replace
+
 import numpy as np
 import pytest
 import torch
@@ -98,14 +100,18 @@ def test_c4_masks_match_processed_path_and_oracle(device, B):
                           w.top_p.cpu().numpy()[req][rnd], "c4 in-kernel masks")
 
 
-@pytest.mark.parametrize("B,V,seed", [(128, configs.VOCAB, 2024), (4500, 1024, 2027)],
-                         ids=["B128", "B4500_several_launches"])
-def test_c4_in_kernel_constraints_then_verify(device, B, V, seed):
-    """rejection_sample on the raw bf16 rows with the divide and the constraints in the
+@pytest.mark.parametrize("B,V,seed,dtype", [(128, configs.VOCAB, 2024, torch.bfloat16),
+                                            (64, configs.VOCAB, 2025, torch.float16),
+                                            (4500, 1024, 2027, torch.bfloat16)],
+                         ids=["B128", "B64_fp16", "B4500_several_launches"])
+def test_c4_in_kernel_constraints_then_verify(device, B, V, seed, dtype):
+    """rejection_sample on the raw 2-byte rows with the divide and the constraints in the
     kernels, against the oracle sampler on the same rows masked by the processed path.  Beyond
     4096 requests the constraints kernel masks the whole batch once and several verify launches
     share its masks, plan order and slot arrays."""
     w = configs.ragged_c4(device, B=B, V=V, seed=seed)
+    if dtype != w.target_logits.dtype:
+        w = replace(w, target_logits=w.target_logits.to(dtype))
     sm = _metadata(w)
     out = rejection_sample(w.draft_token_ids, w.num_draft_tokens, w.max_spec_len,
                            w.cu_num_draft_tokens, w.draft_probs, w.target_logits,

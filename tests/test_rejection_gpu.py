@@ -145,10 +145,11 @@ def test_greedy_argmax_at_every_position(device, dtype, V):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("V", [4096 + 8, 151936])
 def test_greedy_16bit_special_values(device, dtype, V):
-    """16-bit greedy rows (their argmax runs over ordered 16-bit keys): NaN ranks first and the
-    first NaN wins whatever its sign or payload; -0 and +0 tie; -inf rows give column 0; +inf
-    beats every finite value; an entry at the last column and one in the partial last
-    sub-chunk win.  Expected: the first index of the maximum, NaN above every number."""
+    """16-bit greedy rows (each sub-chunk's maximum from a tree of maxima, a tree of sums
+    flagging NaN for the per-entry rule): NaN ranks first and the first NaN wins whatever its
+    sign or payload; -0 and +0 tie; -inf rows give column 0; +inf beats every finite value
+    (and, beside -inf, makes the sum NaN); an entry at the last column and one in the partial
+    last sub-chunk win.  Expected: the first index of the maximum, NaN above every number."""
     def row(fill=-1.0):
         return torch.full((V,), fill, dtype=torch.float32)
     rows, expect = [], []
@@ -376,22 +377,25 @@ def test_odd_vocab_sizes(device, V):
     assert np.array_equal(run_workload(g).cpu().numpy(), oracle_for(g).output_token_ids)
 
 
-@pytest.mark.parametrize("ddtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("tdtype,ddtype", [(torch.bfloat16, torch.float32),
+                                           (torch.bfloat16, torch.bfloat16),
+                                           (torch.float16, torch.float32)])
 @pytest.mark.parametrize("V", [4097, 8200, 151936])
-def test_bf16_target_score_loads(device, V, ddtype):
-    """Random requests on a bf16 target, so that score tasks run on 2-byte targets: 4 columns
-    per lane and load for the target, draft and noise rows.  V = 4097 leaves the rows unaligned
-    (every load bounds-checked, element by element), V = 8200 ends each row in a partial
-    sub-chunk (8-byte loads where a quad fits, checked loads past it)."""
+def test_bf16_target_score_loads(device, V, tdtype, ddtype):
+    """Random requests on a 2-byte target (bf16, fp16), so that score tasks run on 2-byte
+    targets: 4 columns per lane and load for the target, draft and noise rows, and a tree of
+    maxima per lane and sub-chunk.  V = 4097 leaves the rows unaligned (every load
+    bounds-checked, element by element), V = 8200 ends each row in a partial sub-chunk (8-byte
+    loads where a quad fits, checked loads past it)."""
     w = configs.random_c2(device, B=32, k=4, V=V, seed=V + 17)
-    w = replace(w, target_logits=w.target_logits.to(torch.bfloat16),
+    w = replace(w, target_logits=w.target_logits.to(tdtype),
                 draft_probs=w.draft_probs.to(ddtype))
     out = run_workload(w)
     ref = oracle_for(w)
     rejected = sum(len([t for t in row if t != -1]) <= k
                    for row, k in zip(ref.output_token_ids.tolist(), w.num_draft_tokens))
     assert rejected > 0, "no request rejected a draft: no score task ran"
-    check_parity(w, out, ref, f"bf16 target V={V} draft {ddtype}")
+    check_parity(w, out, ref, f"{tdtype} target V={V} draft {ddtype}")
 
 
 def test_repeated_calls_are_identical(device):
