@@ -60,18 +60,41 @@ __global__ __launch_bounds__(kThreads) void ngram_kernel(NgramParams p) {
   const int max_n = p.max_n;
   const int min_n = p.min_n;
   if (tid <= max_n) s_first[tid] = INT_MAX;
-  if (act && tid < max_n && tid < L) s_suf[tid] = row[L - 1 - tid];
-  __syncthreads();
+  // the suffix is loaded with the first tile and stored after that tile's loads are issued,
+  // so both take one memory round trip
+  const bool has_suf = act && tid < max_n && tid < L;
+  const int32_t suf = has_suf ? row[L - 1 - tid] : 0;
+  if (!(act && L >= 2)) {
+    if (has_suf) s_suf[tid] = suf;
+    __syncthreads();
+  }
 
+  // the tile last loaded: tokens [tile_lo, tile_hi) at s_tok[tok - tile_lo]
+  int64_t tile_lo = 0, tile_hi = 0;
   if (act && L >= 2) {
     const int halo = max_n - 1;
     for (int64_t t0 = 0; t0 <= L - 2; t0 += kTile) {
       const int64_t t1 = (t0 + kTile < L - 1) ? t0 + kTile : L - 1;  // ends e in [t0, t1)
-      const int64_t span = t1 - t0 + halo;
-      for (int64_t i = tid; i < span; i += kThreads) {
+      // tokens [t0 - halo, t1], the one after the last window too (a draft may start there)
+      const int64_t span = t1 + 1 - t0 + halo;
+      // every load of the tile is issued before any is stored, so the tile costs one memory
+      // round trip instead of one per loop step
+      constexpr int kPer = (kTile + kNgramMaxN + kThreads - 1) / kThreads;
+      int32_t v[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int64_t i = tid + (int64_t)u * kThreads;
         const int64_t src = t0 - halo + i;
-        s_tok[i] = src >= 0 ? row[src] : 0;
+        v[u] = (i < span && src >= 0) ? row[src] : 0;
       }
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int64_t i = tid + (int64_t)u * kThreads;
+        if (i < span) s_tok[i] = v[u];
+      }
+      if (t0 == 0 && has_suf) s_suf[tid] = suf;
+      tile_lo = t0 - halo;
+      tile_hi = t1 + 1;
       __syncthreads();
       for (int64_t e = t0 + tid; e < t1; e += kThreads) {
         int l = 0;
@@ -103,7 +126,11 @@ __global__ __launch_bounds__(kThreads) void ngram_kernel(NgramParams p) {
   const int64_t avail = start >= 0 ? L - start : 0;
   const int64_t count = p.cap_by_model_len ? (avail < kk ? avail : kk) : avail;
   for (int j = tid; j < p.k; j += kThreads) {
-    s_draft[j] = (start >= 0 && j < count) ? row[start + j] : -1;
+    const int64_t pos = (int64_t)start + j;
+    // from the last tile when it holds the token (every thread saw the same tile bounds)
+    s_draft[j] = (start >= 0 && j < count)
+                     ? (pos >= tile_lo && pos < tile_hi && pos >= 0 ? s_tok[pos - tile_lo] : row[pos])
+                     : -1;
   }
   __syncthreads();
   if (tid == 0) {

@@ -35,11 +35,13 @@ def ngram_propose_device(token_ids: torch.Tensor, num_tokens: torch.Tensor, *, m
     device = token_ids.device
     num_reqs = token_ids.shape[0]
     assert num_tokens.shape[0] >= num_reqs
-    drafts = torch.empty((num_reqs, k), dtype=torch.int32, device=device)
-    num_valid = torch.empty((num_reqs,), dtype=torch.int32, device=device)
+    # one allocation for both outputs: the drafts [num_reqs, k] and the counts after them
+    out = torch.empty(num_reqs * (k + 1), dtype=torch.int32, device=device)
+    drafts = out[:num_reqs * k].view(num_reqs, k)
+    num_valid = out[num_reqs * k:]
     if num_reqs == 0:
         return drafts, num_valid
-    lengths = num_tokens[:num_reqs]
+    lengths = num_tokens if num_tokens.shape[0] == num_reqs else num_tokens[:num_reqs]
     if lengths.dtype != torch.int32 or not lengths.is_contiguous():
         lengths = lengths.to(torch.int32).contiguous()
     act = None
