@@ -170,7 +170,7 @@ int64_t mvsd_rejection_workspace_bytes(int64_t batch_size, int64_t num_tokens, i
   (void)max_spec_len;
   if (batch_size < 0 || num_tokens < 0 || vocab_size <= 0) return -1;
   const mvsd::VerifyPlan plan = mvsd::verify_plan(target_dtype, vocab_size, 0, 0,
-                                                  num_tokens + launch_requests(batch_size));
+                                                  num_tokens + launch_requests(batch_size), true);
   return verify_layout(launch_requests(batch_size), num_tokens, plan.nc_max).total;
 }
 
@@ -220,7 +220,7 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
   // Slot arrays are sized for the most chunks any plan can use, so the layout does not depend
   // on the device.
   const int64_t batch_rows = P + launch_requests(B);
-  const mvsd::VerifyPlan size_plan = mvsd::verify_plan(a->target_dtype, V, 0, 0, batch_rows);
+  const mvsd::VerifyPlan size_plan = mvsd::verify_plan(a->target_dtype, V, 0, 0, batch_rows, true);
   const WorkspaceLayout lay = verify_layout(launch_requests(B), P, size_plan.nc_max);
   if (!ws_ptr || ws_bytes < lay.total) return MVSD_E_WORKSPACE;
   if ((uintptr_t)ws_ptr % 256 != 0) return MVSD_E_ALIGN;
@@ -306,7 +306,7 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
     int64_t groups = Bl * groups_per_req;
     if (groups > P) groups = P;
     const int64_t units = groups + (scores ? Bl : 0);
-    const mvsd::VerifyPlan plan = mvsd::verify_plan(a->target_dtype, V, units, cap, batch_rows);
+    const mvsd::VerifyPlan plan = mvsd::verify_plan(a->target_dtype, V, units, cap, batch_rows, scores);
     q.chunk = plan.chunk;
     q.nc = plan.nc;
     int64_t grid = units * plan.nc;
@@ -323,6 +323,9 @@ int rejection_sample_impl(const mvsd_rejection_args* a, void* ws_ptr, int64_t ws
     // tasks cost more per byte, so the tail groups hold about one half-chunk stats ticket per
     // two workgroups (a quarter of that, or none, measured 0.3-1.2 % slower on bf16 batches).
     q.tail_groups = (int)((grid + 4 * plan.nc - 1) / (4 * plan.nc));
+    // A launch without score units whose tasks all start at once has no end to shorten: half
+    // tasks there would only give some workgroups a second task.
+    if (!scores && units * plan.nc <= cap) q.tail_groups = 0;
     // every workgroup may claim two tickets past the last task
     if (units * 2 * plan.nc > 0x7fffffff - 4 * grid) return MVSD_E_RANGE;
     err = mvsd::launch_verify(q, a->target_dtype, (int)grid, (hipStream_t)stream);

@@ -1381,7 +1381,7 @@ constexpr int ept_of() {
 }
 
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int cap,
-                       int64_t batch_rows) {
+                       int64_t batch_rows, bool even_chunks) {
   VerifyPlan plan;
   plan.ept = target_dtype == MVSD_F32 ? ept_of<MVSD_F32>() : ept_of<MVSD_BF16>();
   plan.g = kGroup;
@@ -1394,10 +1394,10 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int 
   // that cannot give every resident workgroup a task of kMinSubs sub-chunks (a few requests)
   // takes shorter tasks instead, down to kMinSubsSmall sub-chunks, so that its few megabytes
   // are spread over the device.
-  // Score tasks walk sub-chunks of twice the columns, so chunks hold an even number of
-  // sub-chunks.
+  // Score tasks walk sub-chunks of twice the columns, so the chunks of a launch with score
+  // units hold an even number of sub-chunks.
   const int64_t nc_regular = nsub / kMinSubs > 1 ? nsub / kMinSubs : 1;
-  const int64_t nc_small = nsub / kMinSubsSmall > 1 ? nsub / kMinSubsSmall : 1;
+  const int64_t nc_small = (nsub + kMinSubsSmall - 1) / kMinSubsSmall;
   // the workspace holds slots for nc_max chunks per row
   const int64_t nc_max = batch_rows <= kSmallBatchRows ? nc_small : nc_regular;
   int64_t nc_hi = nc_regular;
@@ -1412,7 +1412,7 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int 
     nc = nc < 1 ? 1 : (nc > nc_hi ? nc_hi : nc);
   }
   int64_t subs_per_chunk = (nsub + nc - 1) / nc;
-  if (subs_per_chunk > 1) subs_per_chunk += subs_per_chunk & 1;
+  if (subs_per_chunk > 1 && even_chunks) subs_per_chunk += subs_per_chunk & 1;
   plan.chunk = (int)(subs_per_chunk * plan.sub);
   plan.nc = (int)((vocab_size + plan.chunk - 1) / plan.chunk);
   plan.nc_max = (int)nc_max;

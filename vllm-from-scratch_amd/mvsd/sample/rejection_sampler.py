@@ -37,6 +37,7 @@ Differences from the reference, all on inputs the reference does not define:
 
 from __future__ import annotations
 
+import functools
 from dataclasses import replace
 from typing import TYPE_CHECKING
 
@@ -614,9 +615,9 @@ def rejection_sample(
 
     dtype = nat.dtype_code(target_logits.dtype)
     handle = nat.lib()
-    ws_bytes = handle.mvsd_rejection_workspace_bytes(batch_size, num_tokens, vocab_size, dtype,
-                                                     max_spec_len)
-    workspace = _workspace(device, int(ws_bytes))
+    stream = nat.stream_of(device)
+    workspace = _workspace(device, _workspace_bytes(batch_size, num_tokens, vocab_size, dtype,
+                                                    max_spec_len), stream)
     args = nat.RejectionArgs(
         output_token_ids=output_token_ids.data_ptr(),
         out_stride=output_token_ids.stride(0),
@@ -649,7 +650,7 @@ def rejection_sample(
         top_p=nat.ptr(top_p),
         debug_row_stats=nat.ptr(debug_row_stats),
     )
-    nat.check(handle.mvsd_rejection_sample(args, nat.stream_of(device)), "mvsd_rejection_sample")
+    nat.check(handle.mvsd_rejection_sample(args, stream), "mvsd_rejection_sample")
     return output_token_ids
 
 
@@ -830,8 +831,15 @@ _SAMPLE_RECOVERED_TOKENS = sample_recovered_tokens
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    stream = nat.stream_of(device)
+@functools.lru_cache(maxsize=256)
+def _workspace_bytes(batch_size: int, num_tokens: int, vocab_size: int, dtype: int,
+                     max_spec_len: int) -> int:
+    """The verify workspace's size for a call shape (a pure function of these values)."""
+    return int(nat.lib().mvsd_rejection_workspace_bytes(batch_size, num_tokens, vocab_size, dtype,
+                                                        max_spec_len))
+
+
+def _workspace(device: torch.device, nbytes: int, stream: int) -> torch.Tensor:
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
