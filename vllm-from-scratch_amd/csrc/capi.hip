@@ -91,7 +91,7 @@ int verify_capacity(int device, int dtype, int draft_dtype, bool masked) {
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 // Workspace layout of the verify kernel for launches of at most Bl requests over P verify
-// rows with at most nc chunks per row.  ctrl = {ticket, wait-failure flag, exit counter}.
+// rows with at most nc chunks per row.  ctrl holds the launch counters (mvsd::kCtrlInts ints).
 struct WorkspaceLayout {
   int64_t ctrl, req_cnt, score_cnt, decision, masks, order, stat_slots, score_slots, total;
 };
@@ -101,7 +101,7 @@ WorkspaceLayout verify_layout(int64_t Bl, int64_t P, int64_t nc) {
   int64_t off = 0;
   const int64_t b = Bl > 0 ? Bl : 1, rows = P > 0 ? P : 1;
   l.ctrl = off;
-  off = align_up(off + 3 * 4, 256);
+  off = align_up(off + mvsd::kCtrlInts * 4, 256);
   l.req_cnt = off;
   off = align_up(off + b * 4, 256);
   l.score_cnt = off;

@@ -296,8 +296,8 @@ __device__ inline void pipeline(int64_t v0, int64_t vend, bool aligned, Load&& l
 // ------------------------------------------------------------------ waits ------------
 // One wavefront polls the n slots at `slots` until every one is written, keeping the first
 // kKeep * 64 of them in registers (v[j] holds slot lane + 64 j).  Gives up after
-// p.spin_limit polls, or sooner once the failure flag ctrl[1] is set (so one wait that cannot
-// complete ends every other wait quickly); giving up sets the flag and returns false.
+// p.spin_limit polls, or sooner once the failure flag ctrl[kCtrlFlag] is set (so one wait that
+// cannot complete ends every other wait quickly); giving up sets the flag and returns false.
 // first_read: v already holds a first read of those slots (wave_read_slots), issued ahead of
 // other loads so that the in-order load counter does not hold the poll behind them.
 constexpr int kKeep = 2;
@@ -328,10 +328,10 @@ __device__ inline bool wave_poll(const VerifyParams& p, const uint64_t* slots, i
     }
     for (int c = lane + kKeep * kWave; c < n; c += kWave) ready &= slot_load(slots + c) != 0;
     if (__all(ready)) return true;
-    if ((spins & 255) == 255 && atomic_load_relaxed(&p.ctrl[1]) != 0) break;
+    if ((spins & 255) == 255 && atomic_load_relaxed(&p.ctrl[kCtrlFlag]) != 0) break;
     __builtin_amdgcn_s_sleep(1);
   }
-  if (lane == 0) atomic_store_relaxed(&p.ctrl[1], 1);
+  if (lane == 0) atomic_store_relaxed(&p.ctrl[kCtrlFlag], 1);
   return false;
 }
 
@@ -1216,7 +1216,7 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
   __shared__ float s_c1[kMaxLaunchRequests];
 
   const int tid = threadIdx.x;
-  int* ticket = &p.ctrl[0];
+  int* ticket = &p.ctrl[kCtrlTicket];
   // the first ticket is claimed before the tables are built, so its round trip overlaps them
   int tfirst = 0;
   if (tid == 0) tfirst = atomic_add_relaxed(ticket, 1);
@@ -1273,8 +1273,8 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
         int d = info[7];
         for (int spins = 0; d == 0; ++spins) {
           if (spins >= p.spin_limit ||
-              ((spins & 255) == 255 && atomic_load_relaxed(&p.ctrl[1]) != 0)) {
-            atomic_store_relaxed(&p.ctrl[1], 1);
+              ((spins & 255) == 255 && atomic_load_relaxed(&p.ctrl[kCtrlFlag]) != 0)) {
+            atomic_store_relaxed(&p.ctrl[kCtrlFlag], 1);
             break;
           }
           d = atomic_load_relaxed(&p.decision[r]);
@@ -1319,10 +1319,11 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
   // the launch.  Workgroups that exit after the failure count with acquire-release, which
   // orders their stores before that clean-up.
   if (tid == 0) {
-    const bool failed = atomic_load_relaxed(&p.ctrl[1]) != 0;
-    const int n = failed ? atomic_add_acq_rel(&p.ctrl[2], 1) : atomic_add_relaxed(&p.ctrl[2], 1);
+    const bool failed = atomic_load_relaxed(&p.ctrl[kCtrlFlag]) != 0;
+    int* exits = &p.ctrl[kCtrlExit];
+    const int n = failed ? atomic_add_acq_rel(exits, 1) : atomic_add_relaxed(exits, 1);
     s_last = n == (int)gridDim.x - 1;
-    s_dec = s_last && atomic_load_acquire(&p.ctrl[1]) != 0;
+    s_dec = s_last && atomic_load_acquire(&p.ctrl[kCtrlFlag]) != 0;
   }
   __syncthreads();
   if (s_last) {
@@ -1340,11 +1341,11 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
         atomic_store_relaxed(&p.decision[r], 0);
       }
       __syncthreads();
-      if (tid == 0) atomic_store_relaxed(&p.ctrl[1], 0);
+      if (tid == 0) atomic_store_relaxed(&p.ctrl[kCtrlFlag], 0);
     }
     if (tid == 0) {
-      atomic_store_relaxed(&p.ctrl[0], 0);
-      atomic_store_relaxed(&p.ctrl[2], 0);
+      atomic_store_relaxed(&p.ctrl[kCtrlTicket], 0);
+      atomic_store_relaxed(&p.ctrl[kCtrlExit], 0);
     }
   }
 }
