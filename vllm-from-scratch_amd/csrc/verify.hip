@@ -1013,28 +1013,37 @@ __device__ void finish_scores(const VerifyParams& p, const Tables& tb, int r, in
 // tail is the stats units of the last tail_groups groups and every score unit after the first
 // of them (with tail_groups = 0: the score units after the last stats unit).
 
-// Exclusive scan of one value per thread over the kVThreads-thread block: shuffle scans within
-// the waves, then one barrier for the wave totals.  Returns this thread's exclusive prefix;
-// total receives the block's sum.  `s_wave` holds kVWaves ints.
-__device__ inline int block_exclusive_scan(int v, int& total, int* s_wave) {
+// Exclusive scans of three values per thread over the kVThreads-thread block, side by side:
+// shuffle scans within the waves, then one barrier for the wave totals.  v[i] becomes this
+// thread's exclusive prefix of value i and total[i] the block's sum.  `s_wave` holds
+// 3 * kVWaves ints.
+__device__ inline void block_exclusive_scan3(int (&v)[3], int (&total)[3], int* s_wave) {
   const int lane = lane_id(), w = wave_id();
-  int x = v;
+  int x[3] = {v[0], v[1], v[2]};
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
-    const int y = __shfl_up(x, d, kWave);
-    x += lane >= d ? y : 0;
-  }
-  if (lane == kWave - 1) s_wave[w] = x;
-  __syncthreads();
-  int before = 0, sum = 0;
 #pragma unroll
-  for (int i = 0; i < kVWaves; ++i) {
-    const int t = s_wave[i];
-    before += i < w ? t : 0;
-    sum += t;
+    for (int i = 0; i < 3; ++i) {
+      const int y = __shfl_up(x[i], d, kWave);
+      x[i] += lane >= d ? y : 0;
+    }
   }
-  total = sum;
-  return before + x - v;
+  if (lane == kWave - 1)
+#pragma unroll
+    for (int i = 0; i < 3; ++i) s_wave[i * kVWaves + w] = x[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    int before = 0, sum = 0;
+#pragma unroll
+    for (int j = 0; j < kVWaves; ++j) {
+      const int s = s_wave[i * kVWaves + j];
+      before += j < w ? s : 0;
+      sum += s;
+    }
+    total[i] = sum;
+    v[i] = before + x[i] - v[i];
+  }
 }
 
 // Every workgroup builds the tables: each thread reads the metadata of a run of consecutive
@@ -1063,12 +1072,10 @@ __device__ inline void build_tables(const VerifyParams& p, Tables& tb, int* s_wa
     tb.kflags[r] = k | ((greedy ? kGreedy : 0) | (full ? kFull : 0)) << 16;
     tb.c1[r] = exp2_scale(req_temperature(p, r));
   }
-  int tot_r, tot_g, nfull;
-  int acc_r = block_exclusive_scan(run_r, tot_r, s_wave);
-  __syncthreads();  // s_wave is reused by each scan
-  int acc_g = block_exclusive_scan(run_g, tot_g, s_wave);
-  __syncthreads();
-  int acc_f = block_exclusive_scan(run_f, nfull, s_wave);
+  int acc[3] = {run_r, run_g, run_f}, tot[3];
+  block_exclusive_scan3(acc, tot, s_wave);
+  int acc_r = acc[0], acc_g = acc[1], acc_f = acc[2];
+  const int tot_r = tot[0], tot_g = tot[1], nfull = tot[2];
   const int groups_r = tot_r & 0x3ffff, nreq_r = tot_r >> 18;
   const int groups = groups_r + (tot_g & 0x3ffff);
   for (int r = r0; r < r1; ++r) {
@@ -1209,7 +1216,7 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
   __shared__ int s_info[2][8];  // double-buffered decoded ticket (current, next)
   __shared__ int s_last;
   __shared__ int s_dec;
-  __shared__ int s_wave[kVWaves];
+  __shared__ int s_wave[3 * kVWaves];
   __shared__ DecideSmem dsm;
   __shared__ int s_gpos[kMaxLaunchRequests + 1], s_gstart[kMaxLaunchRequests];
   __shared__ int s_begin[kMaxLaunchRequests], s_kf[kMaxLaunchRequests], s_fpos[kMaxLaunchRequests];
