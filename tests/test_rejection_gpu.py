@@ -319,6 +319,33 @@ def test_greedy_edge_shapes_bit_exact(device, case):
         assert np.array_equal(out.cpu().numpy(), oracle_for(w).output_token_ids)
 
 
+@pytest.mark.parametrize("B", [1, 6, 7, 14, 28, 29])
+def test_greedy_batches_around_one_wave(device, B):
+    """All-greedy fp32 batches (k=3) at full vocabulary.  Up to 28 requests every task has a
+    workgroup of its own and the launch has no tail (chunks of 2, 3, 5 or 9 sub-chunks as the
+    count grows); at 29 the tasks outnumber the 256 resident workgroups and the launch claims
+    tickets with a half-chunk tail again.  Bit-exact against the oracle on both sides."""
+    w = configs.greedy_c1(device, B=B, k=3, seed=600 + B)
+    assert np.array_equal(run_workload(w).cpu().numpy(), oracle_for(w).output_token_ids)
+
+
+def test_supplied_recovered_ids_take_the_plan_without_scores(device, monkeypatch):
+    """Random requests whose recovered ids come from a replaced sample_recovered_tokens give the
+    launch no score units (chunks of any sub-chunk count, no tail when its tasks all start at
+    once).  The ids supplied are the standalone sampler's on the same noise, so the tokens
+    match the in-kernel scores' and the oracle's."""
+    w = configs.random_c2(device, B=6, k=3, seed=611)
+    ref = oracle_for(w)
+    check_parity(w, run_workload(w), ref, "in-kernel scores")
+    probs = orc.target_probs(w.target_logits.cpu(), orc.row_temperatures(
+        w.temperature.cpu(), w.num_draft_tokens, False, True))
+    rec = rs.sample_recovered_tokens(w.max_spec_len, w.num_draft_tokens, w.cu_num_draft_tokens,
+                                     w.draft_token_ids, w.draft_probs, probs.to(device), None,
+                                     device, exp_noise=w.exp_noise)
+    monkeypatch.setattr(rs, "sample_recovered_tokens", lambda *a, **k: rec)
+    check_parity(w, run_workload(w), ref, "supplied recovered ids")
+
+
 def test_more_requests_than_one_launch(device):
     """Batches beyond 4096 requests run as several launches over one workspace (request
     offsets, the first row of a later launch from cu[r0 - 1])."""

@@ -121,10 +121,9 @@ struct VerifyPlan {
 // units = stats groups + score units of the launch (0 gives the workspace-sizing plan);
 // cap = resident workgroups; batch_rows = verify rows + requests of the call (the same value
 // when sizing the workspace and when planning its launches: nc never exceeds nc_max);
-// even_chunks: the launch has score units, whose sub-chunks are twice the stats sub-chunk, so
-// its chunks hold an even number of sub-chunks.
+// score_units: the launch has score units (random requests without supplied recovered ids).
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int cap,
-                       int64_t batch_rows, bool even_chunks);
+                       int64_t batch_rows, bool score_units);
 
 // The verify kernel variant for a target dtype, draft dtype (-1: point-mass drafts) and
 // sampling constraints.

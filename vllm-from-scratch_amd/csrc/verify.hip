@@ -1389,7 +1389,7 @@ constexpr int ept_of() {
 }
 
 VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int cap,
-                       int64_t batch_rows, bool even_chunks) {
+                       int64_t batch_rows, bool score_units) {
   VerifyPlan plan;
   plan.ept = target_dtype == MVSD_F32 ? ept_of<MVSD_F32>() : ept_of<MVSD_BF16>();
   plan.g = kGroup;
@@ -1403,14 +1403,16 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int 
   // takes shorter tasks instead, down to kMinSubsSmall sub-chunks, so that its few megabytes
   // are spread over the device.
   // Score tasks walk sub-chunks of twice the columns, so the chunks of a launch with score
-  // units hold an even number of sub-chunks.
+  // units hold an even number of sub-chunks.  A launch without score units that can give every
+  // resident workgroup a task aims at one task each (no second round, no tail); with score
+  // units the count rounds up, the score tasks coming after the decisions anyway.
   const int64_t nc_regular = nsub / kMinSubs > 1 ? nsub / kMinSubs : 1;
   const int64_t nc_small = (nsub + kMinSubsSmall - 1) / kMinSubsSmall;
   // the workspace holds slots for nc_max chunks per row
   const int64_t nc_max = batch_rows <= kSmallBatchRows ? nc_small : nc_regular;
   int64_t nc_hi = nc_regular;
   if (units > 0 && cap > 0 && units * nc_regular < cap) {
-    const int64_t want = (cap + units - 1) / units;
+    const int64_t want = score_units ? (cap + units - 1) / units : cap / units;
     nc_hi = want < nc_max ? want : nc_max;
     if (nc_hi < nc_regular) nc_hi = nc_regular;
   }
@@ -1420,7 +1422,7 @@ VerifyPlan verify_plan(int target_dtype, int64_t vocab_size, int64_t units, int 
     nc = nc < 1 ? 1 : (nc > nc_hi ? nc_hi : nc);
   }
   int64_t subs_per_chunk = (nsub + nc - 1) / nc;
-  if (subs_per_chunk > 1 && even_chunks) subs_per_chunk += subs_per_chunk & 1;
+  if (subs_per_chunk > 1 && score_units) subs_per_chunk += subs_per_chunk & 1;
   plan.chunk = (int)(subs_per_chunk * plan.sub);
   plan.nc = (int)((vocab_size + plan.chunk - 1) / plan.chunk);
   plan.nc_max = (int)nc_max;
