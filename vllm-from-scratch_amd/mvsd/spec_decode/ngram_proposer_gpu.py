@@ -36,9 +36,10 @@ def ngram_propose_device(token_ids: torch.Tensor, num_tokens: torch.Tensor, *, m
     num_reqs = token_ids.shape[0]
     assert num_tokens.shape[0] >= num_reqs
     # one allocation for both outputs: the drafts [num_reqs, k] and the counts after them
+    # (as_strided views: cheaper on the host than slicing and reshaping)
     out = torch.empty(num_reqs * (k + 1), dtype=torch.int32, device=device)
-    drafts = out[:num_reqs * k].view(num_reqs, k)
-    num_valid = out[num_reqs * k:]
+    drafts = out.as_strided((num_reqs, k), (k, 1))
+    num_valid = out.as_strided((num_reqs,), (1,), num_reqs * k)
     if num_reqs == 0:
         return drafts, num_valid
     lengths = num_tokens if num_tokens.shape[0] == num_reqs else num_tokens[:num_reqs]
@@ -55,11 +56,14 @@ def ngram_propose_device(token_ids: torch.Tensor, num_tokens: torch.Tensor, *, m
             new = new.to(torch.int32).contiguous()
         new_stride, max_new = new.stride(0), new.shape[1]
         counts = new_counts[:num_reqs].to(torch.int32).contiguous()
-    nat.check(nat.lib().mvsd_ngram_propose(
+    status = nat.lib().mvsd_ngram_propose(
         drafts.data_ptr(), num_valid.data_ptr(), token_ids.data_ptr(), token_ids.stride(0),
-        token_ids.shape[1], lengths.data_ptr(), nat.ptr(new), new_stride, max_new,
-        nat.ptr(counts), nat.ptr(act), int(gate_on_new_counts), num_reqs, min_n, max_n, k,
-        int(cap_by_model_len), max_model_len, nat.stream_of(device)), "mvsd_ngram_propose")
+        token_ids.shape[1], lengths.data_ptr(), None if new is None else new.data_ptr(),
+        new_stride, max_new, None if counts is None else counts.data_ptr(),
+        None if act is None else act.data_ptr(), int(gate_on_new_counts), num_reqs, min_n, max_n,
+        k, int(cap_by_model_len), max_model_len, nat.stream_of(device))
+    if status:
+        nat.check(status, "mvsd_ngram_propose")
     return drafts, num_valid
 
 
