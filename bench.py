@@ -80,6 +80,8 @@ TRAFFIC = {
     "c2": (ROOT / "profiles" / "verify_kernel_c2_traffic.md", VERIFY_SOURCES),
     "v2": (ROOT / "profiles" / "v2_verify_kernels_traffic.md",
            [_CSRC + f for f in ("v2_verify.hip", "verify.h", "mvsd_device.h")]),
+    "c3": (ROOT / "profiles" / "ngram_kernel_c3_traffic.md",
+           [_CSRC + f for f in ("ngram.hip", "rows.h", "mvsd_device.h")]),
 }
 
 
@@ -462,10 +464,11 @@ def bench_verify_config(name, device, steps, warmup, cpu_seconds, with_cpu):
     return entry
 
 
-def bench_ngram(device, steps, warmup, with_cpu, cpu_seconds):
+def bench_ngram(device, steps, warmup, with_cpu, cpu_seconds, pmc=False):
     """C3: the ngram proposer over 256 histories of 4096 tokens (``ngram_propose_device``: the
     kernel on device-resident histories), the host-buffer API, and the CPU KMP matcher (the
-    reference CPU algorithm) on all host threads (requests split across threads) and on one."""
+    reference CPU algorithm) on all host threads (requests split across threads) and on one.
+    pmc: run the counter-calibration copy and three steps only."""
     from mvsd.spec_decode.ngram_proposer_gpu import ngram_propose_device
     from mvsd.testing import configs
     from oracle import ngram as ong
@@ -477,6 +480,9 @@ def bench_ngram(device, steps, warmup, with_cpu, cpu_seconds):
     def step():
         return ngram_propose_device(tokens, lens, min_n=2, max_n=5, k=5)
 
+    if pmc:
+        pmc_driver(step, device)
+        return None
     ms, wall_ms, (d, v) = time_steps(step, steps, warmup)
     nbytes = B * L * 4 + B * 4 + B * 5 * 4 + B * 4
     gbs = nbytes / (ms / 1e3) / 1e9
@@ -490,6 +496,9 @@ def bench_ngram(device, steps, warmup, with_cpu, cpu_seconds):
              "bound": "latency (one 16 KB history per workgroup, 4.2 MB per call; the "
                       "kernel takes about 7 us, the host wrapper and launch the rest)",
              "host_api": None, "cpu_baseline": None, "parity": None}
+    traffic = load_traffic("c3")
+    entry["traffic"] = traffic
+    entry["traffic_over_kernel_bytes"] = None if traffic is None else round(traffic / nbytes, 4)
     host_ms = bench_ngram_host_api(tn, ln, steps, warmup, device)
     entry["host_api"] = {"ms_per_call": round(host_ms, 5),
                          "requests_per_s": round(B / (host_ms / 1e3), 1),
@@ -750,6 +759,9 @@ def main():
         sys.exit(2)
     device = torch.device("cuda", 0)
     with_cpu = not args.no_cpu_baseline
+    if args.config == "c3" and args.pmc_driver:
+        bench_ngram(device, args.steps, args.warmup, False, 0.0, pmc=True)
+        return
     if args.config == "c3":
         line = {"metric": "ngram proposer drafts/s (C3)", "n_gpus": 1, "unit": "requests/s",
                 "higher_is_better": True, "scaling": "strong", "vs_baseline": None,
