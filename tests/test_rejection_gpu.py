@@ -435,12 +435,14 @@ def test_repeated_calls_are_identical(device):
 
 
 def test_workspace_is_left_zeroed_across_shapes(device):
-    """Calls of different shapes share one cached workspace; each must leave it zeroed."""
+    """Calls of different shapes share one cached workspace; each must leave it zeroed (the
+    tiny greedy batch runs one task per workgroup and no tail)."""
     big = configs.random_c2(device, B=96, k=4, seed=41)
     small = configs.random_c2(device, B=8, k=2, seed=42)
     greedy = configs.greedy_c1(device, B=40, k=5, seed=43)
-    expect = {id(w): oracle_for(w).output_token_ids for w in (big, small, greedy)}
-    for w in (big, small, greedy, small, big, greedy, big):
+    tiny = configs.greedy_c1(device, B=4, k=3, seed=44)
+    expect = {id(w): oracle_for(w).output_token_ids for w in (big, small, greedy, tiny)}
+    for w in (big, small, greedy, tiny, small, big, tiny, greedy, big):
         out = run_workload(w).cpu().numpy()
         rep = orc.compare(out, orc.OracleResult(expect[id(w)], *([np.full(w.num_tokens, np.nan)] * 4),
                                                 np.zeros(w.num_tokens, bool)),
