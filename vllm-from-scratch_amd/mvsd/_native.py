@@ -189,7 +189,7 @@ _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 def stream_of(device: torch.device) -> int:
     """The HIP stream handle of the current stream on `device`."""
-    if _raw_stream is not None:
+    if _raw_stream is not None and torch.cuda.is_initialized():
         index = device.index
         return _raw_stream(torch.cuda.current_device() if index is None else index)
     return torch.cuda.current_stream(device).cuda_stream
