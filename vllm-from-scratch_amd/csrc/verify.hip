@@ -881,7 +881,9 @@ constexpr uint64_t kSkipKey = 2;
 // their output row here (kPoison in every entry if a wait gave up), and every slot of the
 // request is cleared.  A kFull request publishes its decision instead; the slots of its
 // rejected row stay for the score tasks, and its output row is written by finish_scores.
-__device__ void decide_request(const VerifyParams& p, const Tables& tb, int r, DecideSmem& sm) {
+// Always inlined, as is finish_scores: a call makes the kernel copy its parameters to scratch.
+__device__ __forceinline__ void decide_request(const VerifyParams& p, const Tables& tb, int r,
+                                               DecideSmem& sm) {
   const int begin = tb.begin[r];
   const int kf = tb.kflags[r];
   const int K = kf & 0xffff;
@@ -968,7 +970,8 @@ __device__ void decide_request(const VerifyParams& p, const Tables& tb, int r, D
 // request's output row: the accepted drafts, then the recovered id at the rejected position,
 // or the bonus after a fully accepted chain; kPoison in every entry if any wait gave up.  Then
 // clears everything the request used.
-__device__ void finish_scores(const VerifyParams& p, const Tables& tb, int r, int dec, int nslots) {
+__device__ __forceinline__ void finish_scores(const VerifyParams& p, const Tables& tb, int r,
+                                              int dec, int nslots) {
   if (wave_id() != 0) return;
   const int lane = lane_id();
   const int begin = tb.begin[r];
@@ -1046,6 +1049,19 @@ __device__ inline void block_exclusive_scan3(int (&v)[3], int (&total)[3], int* 
   }
 }
 
+// Length of the prefix of [0, n) on which pred holds (pred holds on a prefix; n <= 64 * 64),
+// found by one wave in two rounds: the first index of each of 64 blocks, then the entries of
+// the block holding the end.  Called by every lane of a wave; every lane receives the count.
+template <typename Pred>
+__device__ inline int wave_prefix_count(int n, Pred&& pred) {
+  const int lane = lane_id();
+  const int step = (n + kWave - 1) / kWave;
+  const int blocks = __popcll(__ballot(lane * step < n && pred(lane * step)));
+  if (blocks == 0) return 0;
+  const int base = (blocks - 1) * step;
+  return base + __popcll(__ballot(lane < step && base + lane < n && pred(base + lane)));
+}
+
 // Every workgroup builds the tables: each thread reads the metadata of a run of consecutive
 // requests once, then block scans give the group offsets and the kFull ordinals.  Stats
 // groups run random requests first, then greedy requests (each in request order): greedy
@@ -1110,24 +1126,21 @@ __device__ inline void build_tables(const VerifyParams& p, Tables& tb, int* s_wa
   // starts at stats unit gt; its score units are those with S_k > tau.
   tb.gt = max(0, groups - p.tail_groups);
   const int tau = p.tail_groups > 0 ? tb.gt : groups - 1;
-  int lo = 0, hi = nfull;  // kt = #{k : S_k <= tau}
-  while (lo < hi) {
-    const int mid = (lo + hi) / 2;
-    if ((tb.fpos[mid] >> 12) - mid <= tau) lo = mid + 1;
-    else hi = mid;
-  }
-  tb.kt = lo;
+  tb.kt = wave_prefix_count(nfull, [&](int k) { return (tb.fpos[k] >> 12) - k <= tau; });
   tb.u0 = tb.gt + tb.kt;
 }
 
 constexpr int kStatsTask = 1;
 constexpr int kScoreTask = 2;
 
-// Thread 0: decode ticket t into dst[0..7] = {t, slot (the chunk, or 2 * chunk + half in the
-// tail), kind | tail << 4, request, first row, rows | groups << 8 | flags << 16 (stats) or
-// K | flags << 16 (score), bits of c1, the request's decision as read now (score units; 0 if
-// not yet published)}.  kind 0: past the last unit.
+// Wave 0, every lane: decode ticket t (lane 0's value) into dst[0..7] = {t, slot (the chunk,
+// or 2 * chunk + half in the tail), kind | tail << 4, request, first row, rows | groups << 8 |
+// flags << 16 (stats) or K | flags << 16 (score), bits of c1, the request's decision as read
+// now (score units; 0 if not yet published)}, written by lane 0.  kind 0: past the last unit.
+// The table searches take two rounds of LDS reads across the wave (a search by one thread
+// took about 1.3 us, in the middle of the task whose loads it follows).
 __device__ inline void fetch_task(const VerifyParams& p, const Tables& tb, int t, int* dst) {
+  t = __builtin_amdgcn_readfirstlane(t);
   const int units = tb.groups + tb.nfull;
   const int reg = tb.u0 * p.nc;
   int u, part, tail;
@@ -1143,27 +1156,19 @@ __device__ inline void fetch_task(const VerifyParams& p, const Tables& tb, int t
   }
   int kind = 0, r = 0, row0 = 0, info = 0, dec = 0;
   if (u < units) {
-    int lo = 0, hi = tb.nfull;  // score units at positions < u
-    while (lo < hi) {
-      const int mid = (lo + hi) / 2;
-      if ((tb.fpos[mid] >> 12) < u) lo = mid + 1;
-      else hi = mid;
-    }
+    // score units at positions < u
+    const int lo = wave_prefix_count(tb.nfull, [&](int k) { return (tb.fpos[k] >> 12) < u; });
     if (lo < tb.nfull && (tb.fpos[lo] >> 12) == u) {
       kind = kScoreTask;
       r = tb.fpos[lo] & 0xfff;
       row0 = tb.begin[r];
       info = tb.kflags[r];
-      dec = atomic_load_relaxed(&p.decision[r]);
+      if (lane_id() == 0) dec = atomic_load_relaxed(&p.decision[r]);
     } else {
       kind = kStatsTask;
       const int li = u - lo;
-      int a = 0, b = p.B - 1;  // the last position whose first group is <= li owns it
-      while (a < b) {
-        const int mid = (a + b + 1) / 2;
-        if ((tb.gpos[mid] >> 12) <= li) a = mid;
-        else b = mid - 1;
-      }
+      // the last position whose first group is <= li owns it (position 0's first group is 0)
+      const int a = wave_prefix_count(p.B, [&](int i) { return (tb.gpos[i] >> 12) <= li; }) - 1;
       r = tb.gpos[a] & 0xfff;
       const int kf = tb.kflags[r];
       const int k = kf & 0xffff;
@@ -1173,14 +1178,16 @@ __device__ inline void fetch_task(const VerifyParams& p, const Tables& tb, int t
       info = min(p.G, k - g * p.G) | ng << 8 | (kf >> 16) << 16;
     }
   }
-  dst[0] = t;
-  dst[1] = part;
-  dst[2] = kind | tail << 4;
-  dst[3] = r;
-  dst[4] = row0;
-  dst[5] = info;
-  dst[6] = __float_as_int(tb.c1[r]);
-  dst[7] = dec;
+  if (lane_id() == 0) {
+    dst[0] = t;
+    dst[1] = part;
+    dst[2] = kind | tail << 4;
+    dst[3] = r;
+    dst[4] = row0;
+    dst[5] = info;
+    dst[6] = __float_as_int(tb.c1[r]);
+    dst[7] = dec;
+  }
 }
 
 // Columns [v0, vend) of task slot `part`: chunk `part` in full, or in the tail half
@@ -1238,7 +1245,7 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
 
   // The next ticket is claimed when a task starts and decoded once the task's loads are in
   // flight, so the atomic and the decode overlap with HBM traffic.
-  if (tid == 0) fetch_task(p, tb, tfirst, s_info[0]);
+  if (wave_id() == 0) fetch_task(p, tb, tfirst, s_info[0]);
   __syncthreads();
   for (int par = 0;; par ^= 1) {
     const int* info = s_info[par];
@@ -1247,7 +1254,7 @@ __global__ __launch_bounds__(kVThreads) void verify_kernel(VerifyParams p) {
     int tnext = 0;
     if (tid == 0) tnext = atomic_add_relaxed(ticket, 1);
     auto prefetch = [&]() {
-      if (tid == 0) fetch_task(p, tb, tnext, s_info[par ^ 1]);
+      if (wave_id() == 0) fetch_task(p, tb, tnext, s_info[par ^ 1]);
     };
     const int kind = info[2] & 0xf;
     const bool tail = info[2] >> 4;
