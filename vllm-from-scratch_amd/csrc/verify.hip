@@ -1075,10 +1075,13 @@ __device__ inline void build_tables(const VerifyParams& p, Tables& tb, int* s_wa
   // per class (random, greedy): requests << 18 | groups, which a launch keeps below 2^31
   int run_r = 0, run_g = 0, run_f = 0;
   for (int r = r0; r < r1; ++r) {
+    // the temperature is read once, beside the bounds (req_is_greedy and req_temperature each
+    // read it, and the compiler kept the two reads, one round trip after the other)
+    const float temp = p.all_greedy ? 0.f : p.temperature[r];
     int b, k;
     req_range(p, r, b, k);
     const int ng = (k + p.G - 1) / p.G;
-    const bool greedy = req_is_greedy(p, r);
+    const bool greedy = temp == 0.f;  // req_is_greedy
     const bool full = !greedy && !p.recovered && k > 0;
     tb.gstart[r] = ng;
     if (greedy) run_g += (1 << 18) + ng;
@@ -1086,7 +1089,7 @@ __device__ inline void build_tables(const VerifyParams& p, Tables& tb, int* s_wa
     run_f += full ? 1 : 0;
     tb.begin[r] = b;
     tb.kflags[r] = k | ((greedy ? kGreedy : 0) | (full ? kFull : 0)) << 16;
-    tb.c1[r] = exp2_scale(req_temperature(p, r));
+    tb.c1[r] = exp2_scale(p.apply_temperature && !greedy ? temp : 1.f);  // req_temperature
   }
   int acc[3] = {run_r, run_g, run_f}, tot[3];
   block_exclusive_scan3(acc, tot, s_wave);
