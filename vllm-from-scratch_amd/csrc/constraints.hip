@@ -789,11 +789,12 @@ __device__ __forceinline__ bool row_thresholds(const VerifyParams& p, int row, C
       divide_group(dv, v, q);
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
-        if (j < n && !(v[j] < A)) {
-          const float d = vmax - q[j];
-          const unsigned long long m = mass_of(d);
-          if (m) atomicAdd(&sm.u.hist[mass_bin(d)], m);
-        }
+        // one branch per entry: the mass is computed for every entry and cleared for a masked
+        // entry or a lane past n
+        const float d = vmax - q[j];
+        const unsigned long long keep = 0ull - (unsigned long long)(j < n && !(v[j] < A));
+        const unsigned long long m = mass_of(d) & keep;
+        if (m) atomicAdd(&sm.u.hist[mass_bin(d)], m);
       }
     });
     __syncthreads();
